@@ -1,0 +1,240 @@
+/*
+ * nyion_hip.h — C ABI of the MI355X (gfx950) attention path for Nyion.
+ *
+ * One shared library, libnyion_hip.so, built with hipcc --offload-arch=gfx950.
+ * Plain pointers and sizes only.  Every entry point returns an int status
+ * (0 = NYION_OK, < 0 = error) and leaves a message in nyion_last_error()
+ * (thread-local), so a binding can map "!= 0" to the reference's `false` /
+ * GpuError::NotAvailable and take its CPU fallback
+ * (swamp-engine/src/executor.rs:709-764, swamp-gpu/src/lib.rs:618-624).
+ * The exceptions are the swamp-kernels symbols (mojo_*), which keep the
+ * reference's void/handle signatures and silent-return-on-null behaviour.
+ *
+ * Device pointers ("d_" or pool arguments) must point into memory on the
+ * current HIP device.  Streams are hipStream_t passed as void* (NULL = the
+ * default stream).  Calls are asynchronous on that stream unless stated.
+ * No entry point allocates device memory on the attention hot path: split-K
+ * partial results go into a caller-provided workspace.
+ *
+ * KV pool layout (paged):   [num_blocks][n_kv_heads][block_tokens][row]
+ *   row = head_dim f32 (NYION_KV_F32) or ceil(head_dim/32)*20 bytes of the
+ *   reference's Q4-20B groups (NYION_KV_Q4_20B: f16 d, f16 dmin, 16 nibble
+ *   bytes; element i of a group in byte 4+i/2, low nibble when i is even;
+ *   swamp-engine/src/cache.rs:637-663, 375-394).
+ *   Token t of sequence b lives in block block_tables[b*max_blocks_per_seq +
+ *   t/block_tokens], slot t%block_tokens.  block_tokens is a power of two.
+ */
+#ifndef NYION_HIP_H
+#define NYION_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* nyion_stream_t; /* hipStream_t */
+
+enum nyion_status {
+    NYION_OK = 0,
+    NYION_ERR_INVALID = -1,     /* bad argument (null, size, alignment, shape) */
+    NYION_ERR_UNSUPPORTED = -2, /* valid but not implemented for this shape */
+    NYION_ERR_NO_DEVICE = -3,   /* no HIP device / not gfx950 */
+    NYION_ERR_OOM = -4,         /* allocation failed (arena or HIP) */
+    NYION_ERR_LAUNCH = -5,      /* HIP launch or runtime error */
+    NYION_ERR_WORKSPACE = -6    /* caller workspace too small */
+};
+
+enum nyion_kv_dtype { NYION_KV_F32 = 0, NYION_KV_Q4_20B = 1 };
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* nyion_last_error(void);
+/* Selects `device`, checks it is gfx950.  Replaces gpu_init()
+ * (swamp-gpu/src/lib.rs:626). */
+int nyion_init(int device);
+int nyion_device_count(void);
+/* Waits for all work on the current device (gpu_sync, fused_attention.cu:181-189). */
+int nyion_sync(void);
+/* Library version string. */
+const char* nyion_version(void);
+
+/* ------------------------------------------------------ decode attention */
+
+/* The ComputeGraph Attention node, executed now on `stream`.
+ * Replaces ComputeNodeOp::Attention {d_q, d_k, d_v, d_scores, d_out, n_heads,
+ * n_kv_heads, seq_len, head_dim, kv_stride} (swamp-gpu/src/compute_graph.rs:14-25)
+ * recorded by GpuComputeContext::add_attention_node (swamp-gpu/src/lib.rs:505-519)
+ * and run by submit_and_wait (lib.rs:479-489).
+ * Semantics: ops::attention (swamp-engine/src/ops.rs:170-278) for one query
+ * token at q_pos = seq_len-1: out[h] = softmax(q[h].K[kv(h)]^T / sqrt(D)) V,
+ * kv(h) = h / (n_heads/n_kv_heads).
+ * Layout: d_q, d_out [n_heads][head_dim] f32; d_k, d_v [n_kv_heads][kv_stride][row].
+ * d_scores: optional f32 scratch of n_heads*kv_stride floats (the node's
+ * scores buffer, swamp-gpu/src/lib.rs:317); when given it holds the split-K
+ * partial results, when NULL the node runs one partition per head group. */
+int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v,
+                         float* d_scores, float* d_out, uint32_t n_heads,
+                         uint32_t n_kv_heads, uint32_t seq_len, uint32_t head_dim,
+                         uint32_t kv_stride, int kv_dtype, nyion_stream_t stream);
+
+/* Project ABI names of the unlinked CUDA file, same arguments (f32 KV,
+ * [n_kv_heads][kv_stride][head_dim]): gpu_attention_device
+ * (swamp-gpu/kernels/fused_attention.cu:194-204) and gpu_attention_streamed
+ * (fused_attention.cu:483-494).  Return 0 / -1 as those did; unlike them,
+ * they allocate nothing per call. */
+int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* d_v_cache,
+                         float* d_output, int n_heads, int n_kv_heads, int seq_len,
+                         int head_dim, int kv_stride);
+int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float* d_v_cache,
+                           float* d_output, int n_heads, int n_kv_heads, int seq_len,
+                           int head_dim, int kv_stride, nyion_stream_t stream);
+
+/* Batched paged GQA decode with split-K partitions and a log-sum-exp merge.
+ * Replaces the CPU decode call of the executor (executor.rs:739-763):
+ *   window <= 0           : ops::attention / attention_tracked semantics
+ *                           (ops.rs:170-278, 283-401) over [0, valid_end],
+ *                           valid_end = min(q_pos, ctx_len-1);
+ *   window > 0            : ops::attention_sparse (ops.rs:85-168): globals
+ *                           global_stride*g, g < min(window_start/stride, 128)
+ *                           (none when global_stride <= 0), then the window
+ *                           [window_start, valid_end], window_start =
+ *                           valid_end-window+1 if valid_end > window else 0.
+ *   kv_dtype Q4_20B       : K/V dequantised in registers exactly as
+ *                           dequant_block (cache.rs:375-394).
+ * d_q, d_out: [batch][n_heads][head_dim] f32.  ctx_lens[batch] (>= 1);
+ * q_pos[batch] or NULL (= ctx_len-1).  max_ctx: host upper bound of ctx_lens,
+ * sizes the grid.  scale <= 0 means 1/sqrt(head_dim).
+ * head_dim in {64, 128}; n_heads % n_kv_heads == 0.
+ * d_workspace: >= nyion_paged_decode_workspace_size(...) bytes, or NULL when
+ * that size is 0. */
+size_t nyion_paged_decode_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
+                                         int max_ctx, int window, int global_stride);
+int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_tables, int max_blocks_per_seq,
+                                 const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                 int n_heads, int n_kv_heads, int head_dim, int block_tokens,
+                                 int num_blocks, int kv_dtype, int window, int global_stride,
+                                 int max_ctx, float scale, float* d_out, void* d_workspace,
+                                 size_t workspace_bytes, nyion_stream_t stream);
+
+/* Decode over explicit position lists (ops::attention_fugu, ops.rs:445-541,
+ * whose list is the sparse set plus DSPark positions; also the Mojo
+ * sparse_attention_q4 FFI, swamp-gpu/src/mojo.rs:5).  Softmax over exactly
+ * the listed positions.  positions: [batch][max_positions] int32,
+ * n_positions[batch]; every listed position must be < that sequence's length
+ * in its block table. */
+size_t nyion_paged_decode_positions_workspace_size(int batch, int n_heads, int n_kv_heads,
+                                                   int head_dim, int max_positions);
+int nyion_paged_decode_attention_positions(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* positions, const int32_t* n_positions,
+    int max_positions, int batch, int n_heads, int n_kv_heads, int head_dim, int block_tokens,
+    int num_blocks, int kv_dtype, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, nyion_stream_t stream);
+
+/* Split-K partition length (tokens, power of two 16..4096) used by the decode
+ * entry points; 0 restores the automatic choice.  Process-wide; for tuning. */
+int nyion_set_decode_partition_tokens(int tokens);
+int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len);
+
+/* ----------------------------------------------------- prefill attention */
+
+/* Causal prefill of one chunk on MFMA (bf16 in, f32 accumulate, f32 out).
+ * Replaces the per-token ops::attention loop of prefill_slice
+ * (executor.rs:106-137): row i attends to keys [0, start_pos+i] of this chunk
+ * (start_pos = 0: the chunk is the whole prefix).  Layout: q [n][n_heads][D],
+ * k, v [n][n_kv_heads][D] bf16 (raw uint16 bits); out [n][n_heads][D] f32.
+ * causal = 0 attends to all n keys.  head_dim 128 or 64.
+ * When k_pool is non-NULL, the chunk's K/V are also written into the paged
+ * cache at positions start_pos.. (the save_at loop, executor.rs:106-111),
+ * widened to f32 or quantised to Q4-20B per kv_dtype. */
+int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n,
+                                 int n_heads, int n_kv_heads, int head_dim, int causal,
+                                 float scale, float* out, void* k_pool, void* v_pool,
+                                 const int32_t* block_table, int block_tokens, int num_blocks,
+                                 int kv_dtype, int start_pos, nyion_stream_t stream);
+
+/* --------------------------------------------------------------- KV cache */
+
+/* Writes n_tokens tokens of one sequence at positions start_pos.. into the
+ * paged pools.  k, v: [n_tokens][n_kv_heads][head_dim] f32 (device).
+ * Replaces PagedKVCache::save / save_at (cache.rs:613-679, 749-811) and the
+ * CUDA gpu_copy_kv_layer / kernel_kv_save (fused_attention.cu:288-310,
+ * 1462-1472).  Q4_20B quantises on device byte-identically to save(). */
+int nyion_kv_write(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
+                   int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
+                   int n_tokens, const float* k, const float* v, nyion_stream_t stream);
+
+/* One new token per sequence (the decode-step save of executor.rs:702):
+ * k, v [batch][n_kv_heads][head_dim]; token written at positions[b]. */
+int nyion_kv_append_batch(void* k_pool, void* v_pool, const int32_t* block_tables,
+                          int max_blocks_per_seq, const int32_t* positions, int batch,
+                          int block_tokens, int num_blocks, int n_kv_heads, int head_dim,
+                          int kv_dtype, const float* k, const float* v, nyion_stream_t stream);
+
+/* Debug/validation kernels sharing the decode kernels' index and unpack code:
+ * gather tokens [0, n_tokens) of one sequence into [n_kv_heads][n_tokens][D]
+ * f32 (dequantising Q4), and row-wise Q4-20B dequantise / quantise. */
+int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_tokens,
+                    int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
+                    float* out, nyion_stream_t stream);
+int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out,
+                     nyion_stream_t stream);
+int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* out,
+                      nyion_stream_t stream);
+
+/* --------------------------------------------------------- HMA arena */
+
+/* The HeterogeneousMemoryAllocator contract (swamp-tensors/src/hma.rs:5-9,
+ * 30-36, 215-260): DeviceLocal allocations are carved from one hipMalloc
+ * region (first-fit free list, 256-byte aligned), HostPinned from one
+ * hipHostMalloc region, UnifiedMapped from hipMallocManaged. */
+enum nyion_mem_location {
+    NYION_MEM_HOST_PINNED = 0,
+    NYION_MEM_DEVICE_LOCAL = 1,
+    NYION_MEM_UNIFIED_MAPPED = 2
+};
+typedef struct nyion_allocation {
+    void*    ptr;
+    size_t   size;
+    int32_t  location;
+    int32_t  _pad;
+    uint64_t device_handle; /* device address (0 for host pinned) */
+} nyion_allocation;
+
+void* nyion_hma_create(size_t device_bytes, size_t host_pinned_bytes);
+int   nyion_hma_alloc(void* hma, size_t size, int location, nyion_allocation* out);
+int   nyion_hma_free(void* hma, const nyion_allocation* a);
+int   nyion_hma_upload(void* hma, const nyion_allocation* dst, const void* src, size_t bytes);
+int   nyion_hma_download(void* hma, void* dst, const nyion_allocation* src, size_t bytes);
+int   nyion_hma_reset(void* hma);
+int   nyion_hma_stats(void* hma, int location, size_t* used, size_t* capacity);
+void  nyion_hma_destroy(void* hma);
+
+/* ------------------------------------------------- swamp-kernels C-ABI */
+
+/* Same symbols and signatures as swamp-kernels/src/lib.rs:36-85,181-223.
+ * Host pointers; null arguments or n <= 0 return silently, as there.
+ * mojo_softmax_padic runs the Q16.16 pipeline of the reference's AVX-512
+ * branch on the GPU (staged through device memory). */
+void  mojo_softmax_padic(const float* logits, float* probs, int n, float temperature);
+void* mojo_stokes_init(int head_dim);
+void  mojo_stokes_append(void* cache, int token_id, const float* key, const float* value,
+                         float score);
+void  mojo_stokes_free(void* cache);
+
+/* Device form of mojo_softmax_padic: d_logits, d_probs device f32[n]. */
+int nyion_softmax_padic_dev(const float* d_logits, float* d_probs, int n, float temperature,
+                            nyion_stream_t stream);
+/* Stokes introspection: token count, and copies of the resident keys, values
+ * and scores into host buffers ([count][head_dim], [count][head_dim], [count]). */
+int nyion_stokes_count(const void* cache);
+int nyion_stokes_read(const void* cache, float* keys, float* values, float* scores);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NYION_HIP_H */

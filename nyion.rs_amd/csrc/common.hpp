@@ -1,0 +1,114 @@
+// common.hpp — shared host/device helpers of libnyion_hip.so (gfx950 only).
+//
+// The Q4-20B unpack and the paged row addressing here are used by the decode
+// kernels, the KV-write kernels and the debug gather/dequant kernels alike,
+// so the debug entry points validate exactly the code the hot path runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/nyion_hip.h"
+
+namespace nyion {
+
+// ------------------------------------------------------------ errors
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define NYION_CHECK_HIP(expr)                                                                \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return ::nyion::set_error(NYION_ERR_LAUNCH, "%s: %s (%s:%d)", #expr,             \
+                                      hipGetErrorString(e_), __FILE__, __LINE__);            \
+    } while (0)
+
+// Launch-error check after a <<<>>> launch.
+int check_launch(const char* what);
+
+// True when the current device is a gfx950 (cached per device).
+int require_device();
+
+static inline bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
+static inline int ilog2(long long x) {
+    int r = 0;
+    while ((1ll << r) < x) r++;
+    return r;
+}
+static inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ------------------------------------------------------------ Q4-20B
+
+constexpr int kQ4GroupBytes = 20;  // f16 d, f16 dmin, 16 nibble bytes
+constexpr int kQ4GroupElems = 32;
+
+__host__ __device__ constexpr int q4_row_bytes(int head_dim) {
+    return ((head_dim + 31) / 32) * kQ4GroupBytes;
+}
+
+// f16 bits -> f32 (exact).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+
+// Dequantise one nibble exactly as dequant_block (swamp-engine/src/cache.rs:
+// 385-392): f32(d) * (f32)nib + f32(dmin), two separately rounded operations.
+__device__ __forceinline__ float q4_dequant(float d, float dmin, uint32_t nib) {
+    return __fadd_rn(__fmul_rn(d, (float)nib), dmin);
+}
+
+// Dequantise 8 consecutive elements whose nibbles are the 4 bytes of `w`
+// (element 2i in the low nibble of byte i, 2i+1 in its high nibble).
+__device__ __forceinline__ void q4_dequant8(uint32_t w, float d, float dmin, float* out) {
+    const uint32_t lo = w & 0x0f0f0f0fu;
+    const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;
+    out[0] = q4_dequant(d, dmin, lo & 0xffu);
+    out[1] = q4_dequant(d, dmin, hi & 0xffu);
+    out[2] = q4_dequant(d, dmin, (lo >> 8) & 0xffu);
+    out[3] = q4_dequant(d, dmin, (hi >> 8) & 0xffu);
+    out[4] = q4_dequant(d, dmin, (lo >> 16) & 0xffu);
+    out[5] = q4_dequant(d, dmin, (hi >> 16) & 0xffu);
+    out[6] = q4_dequant(d, dmin, lo >> 24);
+    out[7] = q4_dequant(d, dmin, hi >> 24);
+}
+
+// Dequantise 4 consecutive elements from the 2 bytes in the low half of `w`.
+__device__ __forceinline__ void q4_dequant4(uint32_t w, float d, float dmin, float* out) {
+    out[0] = q4_dequant(d, dmin, w & 0xfu);
+    out[1] = q4_dequant(d, dmin, (w >> 4) & 0xfu);
+    out[2] = q4_dequant(d, dmin, (w >> 8) & 0xfu);
+    out[3] = q4_dequant(d, dmin, (w >> 12) & 0xfu);
+}
+
+// ------------------------------------------------------------ paged rows
+
+// Where row (token t, kv head h) of one sequence lives.  Strides are in
+// units of the row element (f32 elements, or bytes for Q4).
+struct RowMap {
+    const int32_t* table;  // this sequence's block table, or nullptr (block 0)
+    long long block_stride;
+    long long head_stride;
+    int token_stride;
+    int bt_log2;   // log2(block_tokens)
+    int num_blocks;
+    int table_len;  // entries in this sequence's table
+};
+
+// Offset of the row, or -1 when the token is past the table or its block id
+// is out of [0, num_blocks).
+__device__ __forceinline__ long long row_offset(const RowMap& m, int t, int h) {
+    int blk = 0;
+    if (m.table) {
+        if ((t >> m.bt_log2) >= m.table_len) return -1;
+        blk = m.table[t >> m.bt_log2];
+        if ((unsigned)blk >= (unsigned)m.num_blocks) return -1;
+    }
+    return (long long)blk * m.block_stride + (long long)h * m.head_stride +
+           (long long)(t & ((1 << m.bt_log2) - 1)) * m.token_stride;
+}
+
+}  // namespace nyion

@@ -1,0 +1,446 @@
+// kv_cache.hip — paged KV writes (f32 copy or on-device Q4-20B quantise),
+// and the debug gather / dequantise / quantise kernels.
+//
+// Q4-20B quantisation restates PagedKVCache::save / save_at
+// (swamp-engine/src/cache.rs:637-663, 771-806) byte for byte:
+//   d = max|x|/7 (0 when max|x| <= 1e-10), dmin = min x, in f32;
+//   stored as IEEE f16 (round to nearest even) at bytes [0,2), [2,4);
+//   q = clamp(round_half_away((x - dmin)/d), 0, 15) with the f32 d, dmin;
+//   element i -> byte 4 + i/2, low nibble when i is even.
+// The library is compiled with -ffp-contract=off, so (x - dmin)/d and the
+// dequantiser's d*nib + dmin keep their separate roundings; division is the
+// correctly rounded IEEE divide.
+#include <float.h>
+#include <math.h>
+
+#include "common.hpp"
+
+namespace nyion {
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// Quantise one group of `len` (<= 32) elements into 5 words (20 bytes).
+__device__ __forceinline__ void q4_quantize_group(const float* x, int len, uint32_t w[5]) {
+    float mx = 0.0f, mn = FLT_MAX;
+    for (int i = 0; i < len; i++) {
+        mx = fmaxf(mx, fabsf(x[i]));
+        mn = fminf(mn, x[i]);
+    }
+    const float d = (mx > 1e-10f) ? mx / 7.0f : 0.0f;
+    const float dmin = mn;
+    w[0] = f32_to_f16_bits(d) | (f32_to_f16_bits(dmin) << 16);
+    w[1] = w[2] = w[3] = w[4] = 0u;
+    if (d > 1e-10f) {
+        for (int i = 0; i < len; i++) {
+            float r = roundf((x[i] - dmin) / d);
+            r = fmaxf(r, 0.0f);
+            r = fminf(r, 15.0f);
+            w[1 + (i >> 3)] |= ((uint32_t)r) << (4 * (i & 7));
+        }
+    }
+}
+
+// ------------------------------------------------------------- kernels
+
+// bf16 -> f32 is exact (the bf16 bits are the high half of the f32).
+__device__ __forceinline__ float4 bf16x4_to_f32(uint2 w) {
+    return float4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                  __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+}
+
+struct WriteArgs {
+    void* k_pool;
+    void* v_pool;
+    const int32_t* tables;  // [batch][table_stride]
+    const int32_t* positions;  // per-sequence position (append) or nullptr
+    const float* k;  // [rows][Hkv][D] f32, or nullptr when the bf16 source is used
+    const float* v;
+    const uint16_t* k16;  // [rows][Hkv][D] bf16 bits (prefill path)
+    const uint16_t* v16;
+    int table_stride;
+    int start_pos;  // used when positions == nullptr
+    int rows;       // tokens (single sequence) or sequences (append)
+    int per_seq;    // 1: row r is sequence r at positions[r]; 0: row r is token start_pos+r of seq 0
+    int n_kv_heads;
+    int head_dim;
+    int bt_log2;
+    int num_blocks;
+    long long block_stride;  // row units
+    long long head_stride;
+    int token_stride;
+};
+
+__device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r, int h) {
+    const int seq = a.per_seq ? r : 0;
+    const int pos = a.per_seq ? a.positions[r] : a.start_pos + r;
+    if (pos < 0) return -1;
+    RowMap m;
+    m.table = a.tables + (long long)seq * a.table_stride;
+    m.block_stride = a.block_stride;
+    m.head_stride = a.head_stride;
+    m.token_stride = a.token_stride;
+    m.bt_log2 = a.bt_log2;
+    m.num_blocks = a.num_blocks;
+    m.table_len = a.table_stride;
+    return row_offset(m, pos, h);
+}
+
+// One thread per (row, head, 4 floats).
+__global__ void kv_write_f32_kernel(WriteArgs a) {
+    const int vec = a.head_dim / 4;
+    const long long n = (long long)a.rows * a.n_kv_heads * vec;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int x = (int)(i % vec);
+        const int h = (int)((i / vec) % a.n_kv_heads);
+        const int r = (int)(i / ((long long)vec * a.n_kv_heads));
+        const long long off = write_row_offset(a, r, h);
+        if (off < 0) continue;
+        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 4 * x;
+        float4 kk, vv;
+        if (a.k16) {
+            kk = bf16x4_to_f32(*(const uint2*)(a.k16 + src));
+            vv = bf16x4_to_f32(*(const uint2*)(a.v16 + src));
+        } else {
+            kk = *(const float4*)(a.k + src);
+            vv = *(const float4*)(a.v + src);
+        }
+        *(float4*)((float*)a.k_pool + off + 4 * x) = kk;
+        *(float4*)((float*)a.v_pool + off + 4 * x) = vv;
+    }
+}
+
+// One thread per (row, head, group): quantise K and V groups.
+__global__ void kv_write_q4_kernel(WriteArgs a) {
+    const int groups = (a.head_dim + 31) / 32;
+    const long long n = (long long)a.rows * a.n_kv_heads * groups;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int g = (int)(i % groups);
+        const int h = (int)((i / groups) % a.n_kv_heads);
+        const int r = (int)(i / ((long long)groups * a.n_kv_heads));
+        const long long off = write_row_offset(a, r, h);
+        if (off < 0) continue;
+        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 32 * g;
+        const int len = min(32, a.head_dim - 32 * g);
+        float kb[32], vb[32];
+        const float* ks = a.k + (a.k16 ? 0 : src);
+        const float* vs = a.v + (a.k16 ? 0 : src);
+        if (a.k16) {
+            for (int e = 0; e < len; e++) {
+                kb[e] = __uint_as_float((uint32_t)a.k16[src + e] << 16);
+                vb[e] = __uint_as_float((uint32_t)a.v16[src + e] << 16);
+            }
+            ks = kb;
+            vs = vb;
+        }
+        uint32_t w[5];
+        q4_quantize_group(ks, len, w);
+        uint32_t* dk = (uint32_t*)((uint8_t*)a.k_pool + off + kQ4GroupBytes * g);
+#pragma unroll
+        for (int t = 0; t < 5; t++) dk[t] = w[t];
+        q4_quantize_group(vs, len, w);
+        uint32_t* dv = (uint32_t*)((uint8_t*)a.v_pool + off + kQ4GroupBytes * g);
+#pragma unroll
+        for (int t = 0; t < 5; t++) dv[t] = w[t];
+    }
+}
+
+struct GatherArgs {
+    const void* pool;
+    const int32_t* table;
+    float* out;  // [Hkv][n_tokens][D]
+    long long block_stride;
+    long long head_stride;
+    int token_stride;
+    int bt_log2;
+    int num_blocks;
+    int n_kv_heads;
+    int head_dim;
+    int n_tokens;
+    int kvt;
+};
+
+// One thread per (head, token, 8 dims), through the decode kernels' RowMap
+// and q4_dequant8.
+__global__ void kv_gather_kernel(GatherArgs a) {
+    const int vec = a.head_dim / 8;
+    const long long n = (long long)a.n_kv_heads * a.n_tokens * vec;
+    RowMap m;
+    m.table = a.table;
+    m.block_stride = a.block_stride;
+    m.head_stride = a.head_stride;
+    m.token_stride = a.token_stride;
+    m.bt_log2 = a.bt_log2;
+    m.num_blocks = a.num_blocks;
+    m.table_len = (a.n_tokens + (1 << a.bt_log2) - 1) >> a.bt_log2;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int x = (int)(i % vec);
+        const int t = (int)((i / vec) % a.n_tokens);
+        const int h = (int)(i / ((long long)vec * a.n_tokens));
+        float* dst = a.out + ((long long)h * a.n_tokens + t) * a.head_dim + 8 * x;
+        const long long off = row_offset(m, t, h);
+        float vals[8];
+        if (off < 0) {
+            for (int e = 0; e < 8; e++) vals[e] = __builtin_nanf("");
+        } else if (a.kvt == NYION_KV_F32) {
+            const float* src = (const float*)a.pool + off + 8 * x;
+            for (int e = 0; e < 8; e++) vals[e] = src[e];
+        } else {
+            const uint8_t* row = (const uint8_t*)a.pool + off;
+            const int e0 = 8 * x;
+            const int g = e0 >> 5;
+            const uint32_t hdr = *(const uint32_t*)(row + kQ4GroupBytes * g);
+            const uint32_t w = *(const uint32_t*)(row + kQ4GroupBytes * g + 4 + ((e0 & 31) >> 1));
+            q4_dequant8(w, f16_bits_to_f32(hdr), f16_bits_to_f32(hdr >> 16), vals);
+        }
+        for (int e = 0; e < 8; e++) dst[e] = vals[e];
+    }
+}
+
+// Row-wise Q4-20B dequantise: one thread per (row, 8 elements).
+__global__ void q4_dequant_kernel(const uint8_t* in, long long n_rows, int head_dim, float* out) {
+    const int vec = head_dim / 8;
+    const int rb = q4_row_bytes(head_dim);
+    const long long n = n_rows * vec;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const long long r = i / vec;
+        const int e0 = 8 * (int)(i % vec);
+        const uint8_t* row = in + r * rb;
+        const int g = e0 >> 5;
+        const uint32_t hdr = *(const uint32_t*)(row + kQ4GroupBytes * g);
+        const uint32_t w = *(const uint32_t*)(row + kQ4GroupBytes * g + 4 + ((e0 & 31) >> 1));
+        float vals[8];
+        q4_dequant8(w, f16_bits_to_f32(hdr), f16_bits_to_f32(hdr >> 16), vals);
+        float* dst = out + r * head_dim + e0;
+        for (int e = 0; e < 8; e++) dst[e] = vals[e];
+    }
+}
+
+// Row-wise Q4-20B quantise: one thread per (row, group).
+__global__ void q4_quantize_kernel(const float* in, long long n_rows, int head_dim, uint8_t* out) {
+    const int groups = (head_dim + 31) / 32;
+    const int rb = q4_row_bytes(head_dim);
+    const long long n = n_rows * groups;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x) {
+        const long long r = i / groups;
+        const int g = (int)(i % groups);
+        uint32_t w[5];
+        q4_quantize_group(in + r * head_dim + 32 * g, min(32, head_dim - 32 * g), w);
+        uint32_t* dst = (uint32_t*)(out + r * rb + kQ4GroupBytes * g);
+        for (int t = 0; t < 5; t++) dst[t] = w[t];
+    }
+}
+
+static int grid_for(long long n, int block) {
+    long long g = (n + block - 1) / block;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_tokens,
+                           int num_blocks, int n_kv_heads, int head_dim, int kv_dtype) {
+    if (!k_pool || !v_pool) return set_error(NYION_ERR_INVALID, "kv write: null pool");
+    if (!is_pow2(block_tokens) || block_tokens > (1 << 20))
+        return set_error(NYION_ERR_INVALID, "kv write: block_tokens %d not a power of two",
+                         block_tokens);
+    if (num_blocks <= 0 || n_kv_heads <= 0)
+        return set_error(NYION_ERR_INVALID, "kv write: num_blocks/n_kv_heads");
+    if (kv_dtype == NYION_KV_F32) {
+        if (head_dim <= 0 || head_dim % 4)
+            return set_error(NYION_ERR_UNSUPPORTED, "kv write f32: head_dim %d not a multiple of 4",
+                             head_dim);
+        if (!aligned(k_pool, 16) || !aligned(v_pool, 16))
+            return set_error(NYION_ERR_INVALID, "kv write f32: pools must be 16-byte aligned");
+    } else if (kv_dtype == NYION_KV_Q4_20B) {
+        if (head_dim <= 0) return set_error(NYION_ERR_INVALID, "kv write q4: head_dim");
+        if (!aligned(k_pool, 4) || !aligned(v_pool, 4))
+            return set_error(NYION_ERR_INVALID, "kv write q4: pools must be 4-byte aligned");
+    } else {
+        return set_error(NYION_ERR_INVALID, "kv write: kv_dtype %d", kv_dtype);
+    }
+    const long long row = kv_dtype == NYION_KV_F32 ? head_dim : q4_row_bytes(head_dim);
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.bt_log2 = ilog2(block_tokens);
+    a.num_blocks = num_blocks;
+    a.token_stride = (int)row;
+    a.head_stride = (long long)block_tokens * row;
+    a.block_stride = (long long)n_kv_heads * block_tokens * row;
+    return NYION_OK;
+}
+
+static int launch_write(const WriteArgs& a, int kv_dtype, hipStream_t stream) {
+    if (kv_dtype == NYION_KV_F32) {
+        const long long n = (long long)a.rows * a.n_kv_heads * (a.head_dim / 4);
+        hipLaunchKernelGGL(kv_write_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
+    } else {
+        const long long n = (long long)a.rows * a.n_kv_heads * ((a.head_dim + 31) / 32);
+        hipLaunchKernelGGL(kv_write_q4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
+    }
+    return check_launch("kv write");
+}
+
+// Used by the prefill entry point (prefill_attention.hip).
+int kv_write_impl(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
+                  int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
+                  int n_tokens, const float* k, const float* v, hipStream_t stream) {
+    int rc;
+    WriteArgs a{};
+    if ((rc = fill_write_args(a, k_pool, v_pool, block_tokens, num_blocks, n_kv_heads, head_dim,
+                              kv_dtype)) != NYION_OK)
+        return rc;
+    if (!block_table || !k || !v) return set_error(NYION_ERR_INVALID, "kv write: null argument");
+    if (start_pos < 0 || n_tokens <= 0)
+        return set_error(NYION_ERR_INVALID, "kv write: start_pos %d, n_tokens %d", start_pos, n_tokens);
+    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 16) || !aligned(v, 16)))
+        return set_error(NYION_ERR_INVALID, "kv write: k/v must be 16-byte aligned");
+    a.tables = block_table;
+    a.positions = nullptr;
+    a.k = k;
+    a.v = v;
+    a.table_stride = (int)(((long long)start_pos + n_tokens + block_tokens - 1) / block_tokens);
+    a.start_pos = start_pos;
+    a.rows = n_tokens;
+    a.per_seq = 0;
+    return launch_write(a, kv_dtype, stream);
+}
+
+int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
+                       int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
+                       int n_tokens, const uint16_t* k, const uint16_t* v, hipStream_t stream) {
+    int rc;
+    WriteArgs a{};
+    if ((rc = fill_write_args(a, k_pool, v_pool, block_tokens, num_blocks, n_kv_heads, head_dim,
+                              kv_dtype)) != NYION_OK)
+        return rc;
+    if (!block_table || !k || !v) return set_error(NYION_ERR_INVALID, "kv write: null argument");
+    if (start_pos < 0 || n_tokens <= 0)
+        return set_error(NYION_ERR_INVALID, "kv write: start_pos %d, n_tokens %d", start_pos, n_tokens);
+    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 8) || !aligned(v, 8)))
+        return set_error(NYION_ERR_INVALID, "kv write: bf16 k/v must be 8-byte aligned");
+    a.tables = block_table;
+    a.positions = nullptr;
+    a.k16 = k;
+    a.v16 = v;
+    a.table_stride = (int)(((long long)start_pos + n_tokens + block_tokens - 1) / block_tokens);
+    a.start_pos = start_pos;
+    a.rows = n_tokens;
+    a.per_seq = 0;
+    return launch_write(a, kv_dtype, stream);
+}
+
+}  // namespace nyion
+
+using namespace nyion;
+
+extern "C" {
+
+int nyion_kv_write(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
+                   int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
+                   int n_tokens, const float* k, const float* v, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    return kv_write_impl(k_pool, v_pool, block_table, block_tokens, num_blocks, n_kv_heads,
+                         head_dim, kv_dtype, start_pos, n_tokens, k, v, (hipStream_t)stream);
+}
+
+int nyion_kv_append_batch(void* k_pool, void* v_pool, const int32_t* block_tables,
+                          int max_blocks_per_seq, const int32_t* positions, int batch,
+                          int block_tokens, int num_blocks, int n_kv_heads, int head_dim,
+                          int kv_dtype, const float* k, const float* v, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    WriteArgs a{};
+    if ((rc = fill_write_args(a, k_pool, v_pool, block_tokens, num_blocks, n_kv_heads, head_dim,
+                              kv_dtype)) != NYION_OK)
+        return rc;
+    if (!block_tables || !positions || !k || !v || batch <= 0 || max_blocks_per_seq <= 0)
+        return set_error(NYION_ERR_INVALID, "kv append: null argument or non-positive size");
+    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 16) || !aligned(v, 16)))
+        return set_error(NYION_ERR_INVALID, "kv append: k/v must be 16-byte aligned");
+    a.tables = block_tables;
+    a.positions = positions;
+    a.k = k;
+    a.v = v;
+    a.table_stride = max_blocks_per_seq;
+    a.rows = batch;
+    a.per_seq = 1;
+    return launch_write(a, kv_dtype, (hipStream_t)stream);
+}
+
+int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_tokens,
+                    int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
+                    float* out, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!pool || !block_table || !out || n_tokens <= 0 || n_kv_heads <= 0 || num_blocks <= 0)
+        return set_error(NYION_ERR_INVALID, "kv gather: null argument or non-positive size");
+    if (head_dim <= 0 || head_dim % 8)
+        return set_error(NYION_ERR_UNSUPPORTED, "kv gather: head_dim %d not a multiple of 8",
+                         head_dim);
+    if (!is_pow2(block_tokens)) return set_error(NYION_ERR_INVALID, "kv gather: block_tokens");
+    if (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B)
+        return set_error(NYION_ERR_INVALID, "kv gather: kv_dtype");
+    const long long row = kv_dtype == NYION_KV_F32 ? head_dim : q4_row_bytes(head_dim);
+    GatherArgs a{};
+    a.pool = pool;
+    a.table = block_table;
+    a.out = out;
+    a.token_stride = (int)row;
+    a.head_stride = (long long)block_tokens * row;
+    a.block_stride = (long long)n_kv_heads * block_tokens * row;
+    a.bt_log2 = ilog2(block_tokens);
+    a.num_blocks = num_blocks;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.n_tokens = n_tokens;
+    a.kvt = kv_dtype;
+    const long long n = (long long)n_kv_heads * n_tokens * (head_dim / 8);
+    hipLaunchKernelGGL(kv_gather_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                       a);
+    return check_launch("kv gather");
+}
+
+int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out,
+                     nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!in || !out || n_rows <= 0) return set_error(NYION_ERR_INVALID, "q4 dequant: arguments");
+    if (head_dim <= 0 || head_dim % 32)
+        return set_error(NYION_ERR_UNSUPPORTED, "q4 dequant: head_dim %d not a multiple of 32",
+                         head_dim);
+    if (!aligned(in, 4)) return set_error(NYION_ERR_INVALID, "q4 dequant: input not 4-byte aligned");
+    const long long n = (long long)n_rows * (head_dim / 8);
+    hipLaunchKernelGGL(q4_dequant_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                       in, (long long)n_rows, head_dim, out);
+    return check_launch("q4 dequant");
+}
+
+int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* out,
+                      nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!in || !out || n_rows <= 0 || head_dim <= 0)
+        return set_error(NYION_ERR_INVALID, "q4 quantize: arguments");
+    if (!aligned(out, 4)) return set_error(NYION_ERR_INVALID, "q4 quantize: output not 4-byte aligned");
+    const long long n = (long long)n_rows * ((head_dim + 31) / 32);
+    hipLaunchKernelGGL(q4_quantize_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                       (hipStream_t)stream, in, (long long)n_rows, head_dim, out);
+    return check_launch("q4 quantize");
+}
+
+}  // extern "C"

@@ -1,0 +1,276 @@
+"""ctypes binding of libnyion_hip.so (the C ABI in include/nyion_hip.h).
+
+The product is the HIP library; this module only passes device pointers and
+sizes through the C ABI.  Tensors come from PyTorch (device memory and the
+current HIP stream).  There is no fallback: if the library is missing or the
+device is not a gfx950, every call raises NyionError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnyion_hip.so")
+
+KV_F32 = 0
+KV_Q4_20B = 1
+
+MEM_HOST_PINNED = 0
+MEM_DEVICE_LOCAL = 1
+MEM_UNIFIED_MAPPED = 2
+
+OK = 0
+ERR_INVALID = -1
+ERR_UNSUPPORTED = -2
+ERR_NO_DEVICE = -3
+ERR_OOM = -4
+ERR_LAUNCH = -5
+ERR_WORKSPACE = -6
+
+
+class NyionError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"nyion error {code}: {msg}")
+        self.code = code
+
+
+class Allocation(C.Structure):
+    _fields_ = [("ptr", C.c_void_p), ("size", C.c_size_t), ("location", C.c_int32),
+                ("_pad", C.c_int32), ("device_handle", C.c_uint64)]
+
+
+vp, i32, u32, i64, f32, sz = C.c_void_p, C.c_int, C.c_uint32, C.c_int64, C.c_float, C.c_size_t
+
+# name -> (restype, argtypes); the full list of symbols the header declares.
+SIGNATURES = {
+    "nyion_last_error": (C.c_char_p, []),
+    "nyion_init": (i32, [i32]),
+    "nyion_device_count": (i32, []),
+    "nyion_sync": (i32, []),
+    "nyion_version": (C.c_char_p, []),
+    "nyion_attention_node": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, i32, vp]),
+    "gpu_attention_device": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "gpu_attention_streamed": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+    "nyion_paged_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
+    "nyion_paged_decode_attention": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32,
+                                           i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
+    "nyion_paged_decode_positions_workspace_size": (sz, [i32, i32, i32, i32, i32]),
+    "nyion_paged_decode_attention_positions": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
+                                                     i32, i32, i32, i32, i32, f32, vp, vp, sz,
+                                                     vp]),
+    "nyion_set_decode_partition_tokens": (i32, [i32]),
+    "nyion_get_decode_partition_tokens": (i32, [i32, i32, i32, i32]),
+    "nyion_prefill_attention_bf16": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp, vp,
+                                           vp, i32, i32, i32, i32, vp]),
+    "nyion_kv_write": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
+    "nyion_kv_append_batch": (i32, [vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, vp, vp,
+                                    vp]),
+    "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_q4_dequant": (i32, [vp, i64, i32, vp, vp]),
+    "nyion_q4_quantize": (i32, [vp, i64, i32, vp, vp]),
+    "nyion_hma_create": (vp, [sz, sz]),
+    "nyion_hma_alloc": (i32, [vp, sz, i32, C.POINTER(Allocation)]),
+    "nyion_hma_free": (i32, [vp, C.POINTER(Allocation)]),
+    "nyion_hma_upload": (i32, [vp, C.POINTER(Allocation), vp, sz]),
+    "nyion_hma_download": (i32, [vp, vp, C.POINTER(Allocation), sz]),
+    "nyion_hma_reset": (i32, [vp]),
+    "nyion_hma_stats": (i32, [vp, i32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "nyion_hma_destroy": (None, [vp]),
+    "mojo_softmax_padic": (None, [vp, vp, i32, f32]),
+    "mojo_stokes_init": (vp, [i32]),
+    "mojo_stokes_append": (None, [vp, i32, vp, vp, f32]),
+    "mojo_stokes_free": (None, [vp]),
+    "nyion_softmax_padic_dev": (i32, [vp, vp, i32, f32, vp]),
+    "nyion_stokes_count": (i32, [vp]),
+    "nyion_stokes_read": (i32, [vp, vp, vp, vp]),
+}
+
+_lib = None
+
+
+def load():
+    """Load the library (raises NyionError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NyionError(ERR_NO_DEVICE, f"{LIB_PATH} not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return load().nyion_last_error().decode()
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != OK:
+        raise NyionError(rc, f"{what}: {last_error()}")
+
+
+# ----------------------------------------------------------------------------
+# torch helpers
+# ----------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(stream=None) -> int | None:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def init(device: int = 0) -> None:
+    check(load().nyion_init(device), "nyion_init")
+
+
+# ----------------------------------------------------------------------------
+# decode
+# ----------------------------------------------------------------------------
+
+def attention_node(q, k, v, out, n_heads, n_kv_heads, seq_len, head_dim, kv_stride,
+                   kv_dtype=KV_F32, scores=None, stream=None):
+    rc = load().nyion_attention_node(ptr(q), ptr(k), ptr(v), ptr(scores), ptr(out), n_heads,
+                                     n_kv_heads, seq_len, head_dim, kv_stride, kv_dtype,
+                                     stream_handle(stream))
+    check(rc, "nyion_attention_node")
+
+
+def decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_ctx, window=0,
+                          global_stride=0) -> int:
+    return int(load().nyion_paged_decode_workspace_size(batch, n_heads, n_kv_heads, head_dim,
+                                                         max_ctx, window, global_stride))
+
+
+def alloc_workspace(nbytes: int, device="cuda"):
+    torch = _torch()
+    if nbytes <= 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def paged_decode(q, k_pool, v_pool, block_tables, ctx_lens, out, n_heads, n_kv_heads, head_dim,
+                 block_tokens, kv_dtype=KV_F32, window=0, global_stride=0, max_ctx=None,
+                 q_pos=None, scale=0.0, workspace=None, stream=None):
+    """q [B][Hq][D] f32, pools [num_blocks][Hkv][block_tokens][row], block_tables [B][max_blocks]
+    int32, ctx_lens [B] int32.  All device tensors."""
+    B = q.shape[0]
+    max_blocks = block_tables.shape[1]
+    num_blocks = k_pool.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = load().nyion_paged_decode_attention(
+        ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), max_blocks, ptr(ctx_lens),
+        ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens, num_blocks, kv_dtype, window,
+        global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes, stream_handle(stream))
+    check(rc, "nyion_paged_decode_attention")
+    return workspace
+
+
+def paged_decode_positions(q, k_pool, v_pool, block_tables, positions, n_positions, out, n_heads,
+                           n_kv_heads, head_dim, block_tokens, kv_dtype=KV_F32, scale=0.0,
+                           workspace=None, stream=None):
+    B = q.shape[0]
+    max_pos = positions.shape[1]
+    need = int(load().nyion_paged_decode_positions_workspace_size(B, n_heads, n_kv_heads, head_dim,
+                                                                  max_pos))
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = load().nyion_paged_decode_attention_positions(
+        ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1], ptr(positions),
+        ptr(n_positions), max_pos, B, n_heads, n_kv_heads, head_dim, block_tokens,
+        k_pool.shape[0], kv_dtype, scale, ptr(out), ptr(workspace), ws_bytes,
+        stream_handle(stream))
+    check(rc, "nyion_paged_decode_attention_positions")
+    return workspace
+
+
+def set_partition_tokens(tokens: int) -> None:
+    check(load().nyion_set_decode_partition_tokens(tokens), "set_partition_tokens")
+
+
+def partition_tokens(batch, n_kv_heads, head_dim, max_len) -> int:
+    return int(load().nyion_get_decode_partition_tokens(batch, n_kv_heads, head_dim, max_len))
+
+
+# ----------------------------------------------------------------------------
+# prefill
+# ----------------------------------------------------------------------------
+
+def prefill_bf16(q, k, v, out, n_heads, n_kv_heads, head_dim, causal=True, scale=0.0,
+                 k_pool=None, v_pool=None, block_table=None, block_tokens=16,
+                 kv_dtype=KV_F32, start_pos=0, stream=None):
+    """q [N][Hq][D], k/v [N][Hkv][D] bf16 (torch.bfloat16); out [N][Hq][D] f32."""
+    n = q.shape[0]
+    num_blocks = 0 if k_pool is None else k_pool.shape[0]
+    rc = load().nyion_prefill_attention_bf16(
+        ptr(q), ptr(k), ptr(v), n, n_heads, n_kv_heads, head_dim, 1 if causal else 0, scale,
+        ptr(out), ptr(k_pool), ptr(v_pool), ptr(block_table), block_tokens, num_blocks, kv_dtype,
+        start_pos, stream_handle(stream))
+    check(rc, "nyion_prefill_attention_bf16")
+
+
+# ----------------------------------------------------------------------------
+# KV cache
+# ----------------------------------------------------------------------------
+
+def kv_write(k_pool, v_pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dtype,
+             start_pos, k, v, stream=None):
+    rc = load().nyion_kv_write(ptr(k_pool), ptr(v_pool), ptr(block_table), block_tokens,
+                               k_pool.shape[0], n_kv_heads, head_dim, kv_dtype, start_pos,
+                               k.shape[0], ptr(k), ptr(v), stream_handle(stream))
+    check(rc, "nyion_kv_write")
+
+
+def kv_append_batch(k_pool, v_pool, block_tables, positions, block_tokens, n_kv_heads, head_dim,
+                    kv_dtype, k, v, stream=None):
+    rc = load().nyion_kv_append_batch(ptr(k_pool), ptr(v_pool), ptr(block_tables),
+                                      block_tables.shape[1], ptr(positions), positions.shape[0],
+                                      block_tokens, k_pool.shape[0], n_kv_heads, head_dim,
+                                      kv_dtype, ptr(k), ptr(v), stream_handle(stream))
+    check(rc, "nyion_kv_append_batch")
+
+
+def kv_gather(pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dtype, n_tokens, out,
+              stream=None):
+    rc = load().nyion_kv_gather(ptr(pool), ptr(block_table), block_tokens, pool.shape[0],
+                                n_kv_heads, head_dim, kv_dtype, n_tokens, ptr(out),
+                                stream_handle(stream))
+    check(rc, "nyion_kv_gather")
+
+
+def q4_dequant(inp, n_rows, head_dim, out, stream=None):
+    check(load().nyion_q4_dequant(ptr(inp), n_rows, head_dim, ptr(out), stream_handle(stream)),
+          "nyion_q4_dequant")
+
+
+def q4_quantize(inp, n_rows, head_dim, out, stream=None):
+    check(load().nyion_q4_quantize(ptr(inp), n_rows, head_dim, ptr(out), stream_handle(stream)),
+          "nyion_q4_quantize")
+
+
+# ----------------------------------------------------------------------------
+# swamp-kernels C-ABI
+# ----------------------------------------------------------------------------
+
+def softmax_padic_dev(logits, probs, temperature=1.0, stream=None):
+    check(load().nyion_softmax_padic_dev(ptr(logits), ptr(probs), logits.numel(),
+                                         float(temperature), stream_handle(stream)),
+          "nyion_softmax_padic_dev")

@@ -1,0 +1,635 @@
+/*
+ * nyion_oracle.c — CPU restatement of the Nyion attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the CPU baseline).  The product
+ * library never links or calls this file.  Build: oracle/Makefile, which
+ * compiles with -ffp-contract=off so that every multiply-then-add written
+ * below stays two roundings, exactly as the Rust source (no contraction)
+ * does; fused operations are spelled fmaf() where the reference uses an FMA
+ * intrinsic.
+ *
+ * Citations are reference file:line (repository-relative).
+ */
+#include "nyion_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#if defined(__x86_64__) && defined(__GNUC__) && !defined(__clang__)
+#define ORC_CLONES __attribute__((target_clones("arch=skylake-avx512", "arch=haswell", "default")))
+#else
+#define ORC_CLONES
+#endif
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------
+ * simd.rs primitives
+ * --------------------------------------------------------------------- */
+
+/* dot_product_avx512 (swamp-kernels/src/simd.rs:35-68): 16 FMA lanes over
+ * full 16-chunks, one 8-wide FMA into lanes 0-7 (the reference widens a
+ * 256-bit load with _mm512_castps256_ps512, whose upper half is undefined;
+ * it is taken as zero here), a scalar mul+add tail, then the reduction tree
+ * (lanes 0-3 + 4-7) + (8-11 + 12-15), two horizontal adds, plus the tail. */
+static inline float dot16(const float* a, const float* b, int n) {
+    float acc[16];
+    for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+    if (i + 8 <= n) {
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+        i += 8;
+    }
+    float tail = 0.0f;
+    for (; i < n; i++) tail = tail + a[i] * b[i];
+    float s[4];
+    for (int l = 0; l < 4; l++) {
+        float s1 = acc[l] + acc[4 + l];
+        float s2 = acc[8 + l] + acc[12 + l];
+        s[l] = s1 + s2;
+    }
+    float h0 = s[0] + s[1];
+    float h1 = s[2] + s[3];
+    return (h0 + h1) + tail;
+}
+
+/* weighted_sum_avx512 (simd.rs:106-121): out = fma(score, v, out) over
+ * 16-chunks, scalar out += score*v tail. */
+static inline void axpy16(float* out, const float* v, float score, int n) {
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 16; l++) out[i + l] = fmaf(score, v[i + l], out[i + l]);
+    for (; i < n; i++) out[i] = out[i] + score * v[i];
+}
+
+float orc_dot_avx512_order(const float* a, const float* b, int n) { return dot16(a, b, n); }
+void orc_weighted_sum(float* out, const float* v, float score, int n) { axpy16(out, v, score, n); }
+
+/* ------------------------------------------------------------------------
+ * IEEE binary16 (the `half` 2.7.1 crate's f16::from_f32 / to_f32, used at
+ * cache.rs:376-383,651-652).  Round-to-nearest-even, overflow to infinity,
+ * gradual underflow; NaN stays NaN with the quiet bit set.
+ * --------------------------------------------------------------------- */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ex = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (ex == 0xffu) {
+        if (man == 0) return (uint16_t)(sign | 0x7c00u);
+        return (uint16_t)(sign | 0x7c00u | 0x200u | (man >> 13));
+    }
+    int e = (int)ex - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t m = man | 0x800000u;
+        int shift = 14 - e; /* 14..24 */
+        uint32_t hm = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t hm = man >> 13;
+    uint32_t rem = man & 0x1fffu;
+    uint32_t h = sign | ((uint32_t)e << 10) | hm;
+    if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) h++;
+    return (uint16_t)h;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    uint32_t bits;
+    if (ex == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            float v = ldexpf((float)man, -24);
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (ex == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((ex - 15u + 127u) << 23) | (man << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* ------------------------------------------------------------------------
+ * Q4-20B codec
+ * Quantise: PagedKVCache::save / save_at (cache.rs:637-663, 771-806).
+ *   per 32-element group: d = max|x|/7 (0 when max|x| <= 1e-10),
+ *   dmin = min x, both f32, stored as f16 LE at bytes [0,2) and [2,4);
+ *   q_i = clamp(round_half_away((x_i - dmin)/d), 0, 15) with the f32 d, dmin;
+ *   element i -> byte 4 + i/2, low nibble if i even.
+ *   f32::max/min skip NaN, as fmaxf/fminf do.
+ * Dequantise: dequant_block (cache.rs:375-394): f32(d)*nib + f32(dmin),
+ *   a separate multiply and add.
+ * --------------------------------------------------------------------- */
+int orc_q4_row_bytes(int head_dim) { return ((head_dim + 31) / 32) * 20; }
+
+void orc_q4_quantize_row(const float* x, int head_dim, uint8_t* out) {
+    int groups = (head_dim + 31) / 32;
+    for (int g = 0; g < groups; g++) {
+        int start = g * 32;
+        int end = start + 32 < head_dim ? start + 32 : head_dim;
+        int len = end - start;
+        uint8_t* blk = out + g * 20;
+        float mx = 0.0f, mn = FLT_MAX;
+        for (int i = 0; i < len; i++) {
+            mx = fmaxf(mx, fabsf(x[start + i]));
+            mn = fminf(mn, x[start + i]);
+        }
+        float d = (mx > 1e-10f) ? mx / 7.0f : 0.0f;
+        float dmin = mn;
+        uint16_t dh = orc_f32_to_f16(d), mh = orc_f32_to_f16(dmin);
+        blk[0] = (uint8_t)(dh & 0xff);
+        blk[1] = (uint8_t)(dh >> 8);
+        blk[2] = (uint8_t)(mh & 0xff);
+        blk[3] = (uint8_t)(mh >> 8);
+        memset(blk + 4, 0, 16);
+        for (int i = 0; i < len; i++) {
+            uint8_t q = 0;
+            if (d > 1e-10f) {
+                float r = roundf((x[start + i] - dmin) / d);
+                r = fmaxf(r, 0.0f);
+                r = fminf(r, 15.0f);
+                q = (uint8_t)r;
+            }
+            blk[4 + i / 2] |= (uint8_t)(q << ((i % 2) ? 4 : 0));
+        }
+    }
+}
+
+void orc_q4_dequant_row(const uint8_t* in, int head_dim, float* out) {
+    int groups = (head_dim + 31) / 32;
+    for (int g = 0; g < groups; g++) {
+        const uint8_t* blk = in + g * 20;
+        float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        float dmin = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+        for (int i = 0; i < 32; i++) {
+            if (g * 32 + i >= head_dim) break;
+            uint8_t b = blk[4 + i / 2];
+            uint8_t nib = (i % 2 == 0) ? (uint8_t)(b & 0x0f) : (uint8_t)(b >> 4);
+            float prod = d * (float)nib;
+            out[g * 32 + i] = prod + dmin;
+        }
+    }
+}
+
+void orc_q4_quantize_rows(const float* x, int64_t n_rows, int head_dim, uint8_t* out) {
+    int rb = orc_q4_row_bytes(head_dim);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_rows; r++)
+        orc_q4_quantize_row(x + r * head_dim, head_dim, out + r * rb);
+}
+
+void orc_q4_dequant_rows(const uint8_t* in, int64_t n_rows, int head_dim, float* out) {
+    int rb = orc_q4_row_bytes(head_dim);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n_rows; r++)
+        orc_q4_dequant_row(in + r * rb, head_dim, out + r * head_dim);
+}
+
+/* ------------------------------------------------------------------------
+ * Zone page arithmetic (cache.rs:17-21 constants, 185-237 zone build and
+ * flat ids, 593-611 page_id/page_start_for/slot_in_page, 365/689/711 f32
+ * offsets, 627/665/733 Q4 offsets).
+ * --------------------------------------------------------------------- */
+static const int64_t ZSTART[3] = {0, 4096, 131072};
+static const int64_t ZBS[3] = {32, 128, 1024};
+
+int64_t orc_zone_index(int64_t pos) { return pos < ZSTART[1] ? 0 : (pos < ZSTART[2] ? 1 : 2); }
+int64_t orc_zone_block_size(int64_t pos) { return ZBS[orc_zone_index(pos)]; }
+
+static int64_t zone_pages(int z, int64_t max_seq_len) {
+    int64_t start = ZSTART[z];
+    int64_t end = z + 1 < 3 ? ZSTART[z + 1] : max_seq_len;
+    int64_t cov = end > start ? end - start : 0;
+    return cov > 0 ? (cov + ZBS[z] - 1) / ZBS[z] : 0;
+}
+
+int64_t orc_zone_total_pages(int64_t max_seq_len) {
+    return zone_pages(0, max_seq_len) + zone_pages(1, max_seq_len) + zone_pages(2, max_seq_len);
+}
+
+int64_t orc_zone_page_id(int64_t pos, int64_t max_seq_len) {
+    int z = (int)orc_zone_index(pos);
+    int64_t off = 0;
+    for (int i = 0; i < z; i++) off += zone_pages(i, max_seq_len);
+    return off + (pos - ZSTART[z]) / ZBS[z];
+}
+
+int64_t orc_zone_slot_in_page(int64_t pos) {
+    int z = (int)orc_zone_index(pos);
+    return (pos - ZSTART[z]) % ZBS[z];
+}
+
+int64_t orc_zone_page_start(int64_t pos) { return pos - orc_zone_slot_in_page(pos); }
+
+int64_t orc_zone_f32_offset(int64_t layer, int64_t kv_head, int64_t pos, int64_t n_kv_heads,
+                            int64_t head_dim) {
+    int64_t bs = orc_zone_block_size(pos);
+    return ((layer * n_kv_heads + kv_head) * bs + orc_zone_slot_in_page(pos)) * head_dim;
+}
+
+int64_t orc_zone_q4_offset(int64_t layer, int64_t kv_head, int64_t pos, int64_t n_kv_heads,
+                           int64_t head_dim) {
+    int64_t bs = orc_zone_block_size(pos);
+    int64_t rb = orc_q4_row_bytes((int)head_dim);
+    return (layer * n_kv_heads + kv_head) * bs * rb + orc_zone_slot_in_page(pos) * rb;
+}
+
+/* ------------------------------------------------------------------------
+ * Position sets
+ * attention_sparse (swamp-engine/src/ops.rs:97-113):
+ *   valid_end = min(q_pos, seq_len-1)
+ *   window_start = valid_end > window ? valid_end - window + 1 : 0   (strict >)
+ *   globals: stride*g for g < min(window_start/stride, 128)
+ *   then window_start..=valid_end
+ * The reference divides by global_stride unconditionally (a zero stride
+ * panics there); here stride <= 0 means no globals.
+ * attention_fugu (ops.rs:459-484): the same with sentinel_stride, then each
+ * dspark position p <= valid_end not already present, in the given order.
+ * --------------------------------------------------------------------- */
+static int sparse_into(int seq_len, int q_pos, int window, int stride, int32_t* out, int cap) {
+    if (seq_len <= 0 || q_pos < 0 || window < 0) return -1;
+    int valid_end = q_pos < seq_len - 1 ? q_pos : seq_len - 1;
+    int ws = valid_end > window ? valid_end - window + 1 : 0;
+    int n = 0;
+    if (stride > 0) {
+        int gc = ws / stride;
+        if (gc > 128) gc = 128;
+        for (int g = 0; g < gc; g++) {
+            if (n >= cap) return -2;
+            out[n++] = stride * g;
+        }
+    }
+    for (int t = ws; t <= valid_end; t++) {
+        if (n >= cap) return -2;
+        out[n++] = t;
+    }
+    return n;
+}
+
+int orc_sparse_positions(int seq_len, int q_pos, int window, int global_stride, int32_t* out,
+                         int cap) {
+    return sparse_into(seq_len, q_pos, window, global_stride, out, cap);
+}
+
+int orc_fugu_positions(int seq_len, int q_pos, int window, int sentinel_stride,
+                       const int32_t* dspark, int n_dspark, int32_t* out, int cap) {
+    int n = sparse_into(seq_len, q_pos, window, sentinel_stride, out, cap);
+    if (n < 0) return n;
+    int valid_end = q_pos < seq_len - 1 ? q_pos : seq_len - 1;
+    for (int i = 0; i < n_dspark; i++) {
+        int p = dspark[i];
+        if (p < 0 || p > valid_end) continue;
+        int present = 0;
+        for (int j = 0; j < n; j++)
+            if (out[j] == p) { present = 1; break; }
+        if (present) continue;
+        if (n >= cap) return -2;
+        out[n++] = p;
+    }
+    return n;
+}
+
+/* ------------------------------------------------------------------------
+ * Attention
+ * --------------------------------------------------------------------- */
+static inline int64_t row_index(const orc_kv_layout* kv, int64_t t, int64_t h) {
+    int64_t blk = kv->table ? (int64_t)kv->table[t / kv->block_tokens] : 0;
+    return blk * kv->block_stride + h * kv->head_stride + (t % kv->block_tokens) * kv->token_stride;
+}
+
+/* Returns a pointer to the f32 row; Q4 rows are dequantised into tmp first,
+ * as the reference reads Q4 pages through their f32 view (cache.rs:338-405). */
+static inline const float* fetch_row(const orc_kv_layout* kv, const void* base, int64_t t,
+                                     int64_t h, int head_dim, float* tmp) {
+    int64_t idx = row_index(kv, t, h);
+    if (kv->dtype == ORC_KV_F32) return (const float*)base + idx;
+    orc_q4_dequant_row((const uint8_t*)base + idx, head_dim, tmp);
+    return tmp;
+}
+
+/* One head of ops::attention / attention_tracked (ops.rs:170-278, 283-401):
+ * scores for t in [0, valid_end], -inf for (valid_end, seq_len), max, exp,
+ * sum in t order, multiply by 1/sum (normalise before accumulating), then
+ * out = sum_t p_t V_t with weighted_sum. */
+ORC_CLONES
+static void head_full(float* out, const float* qh, const orc_kv_layout* kv, int kvh, int seq_len,
+                      int valid_end, int head_dim, float scale, float* scores, float* tmp) {
+    float mx = -INFINITY;
+    for (int t = 0; t <= valid_end; t++) {
+        const float* kr = fetch_row(kv, kv->k_base, t, kvh, head_dim, tmp);
+        float s = dot16(qh, kr, head_dim) * scale;
+        scores[t] = s;
+        if (s > mx) mx = s;
+    }
+    for (int t = valid_end + 1; t < seq_len; t++) scores[t] = -INFINITY;
+    float sum = 0.0f;
+    for (int t = 0; t < seq_len; t++) {
+        float e = expf(scores[t] - mx);
+        scores[t] = e;
+        sum += e;
+    }
+    float inv = 1.0f / sum;
+    for (int t = 0; t < seq_len; t++) scores[t] *= inv;
+    for (int d = 0; d < head_dim; d++) out[d] = 0.0f;
+    for (int t = 0; t <= valid_end; t++) {
+        const float* vr = fetch_row(kv, kv->v_base, t, kvh, head_dim, tmp);
+        axpy16(out, vr, scores[t], head_dim);
+    }
+}
+
+/* One head of attention_sparse / attention_fugu (ops.rs:126-166, 497-540):
+ * softmax over exactly the listed positions, no mask. */
+ORC_CLONES
+static void head_positions(float* out, const float* qh, const orc_kv_layout* kv, int kvh,
+                           const int32_t* pos, int n_pos, int head_dim, float scale,
+                           float* scores, float* tmp) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n_pos; i++) {
+        const float* kr = fetch_row(kv, kv->k_base, pos[i], kvh, head_dim, tmp);
+        float s = dot16(qh, kr, head_dim) * scale;
+        scores[i] = s;
+        if (s > mx) mx = s;
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < n_pos; i++) {
+        float e = expf(scores[i] - mx);
+        scores[i] = e;
+        sum += e;
+    }
+    float inv = 1.0f / sum;
+    for (int i = 0; i < n_pos; i++) scores[i] *= inv;
+    for (int d = 0; d < head_dim; d++) out[d] = 0.0f;
+    for (int i = 0; i < n_pos; i++) {
+        const float* vr = fetch_row(kv, kv->v_base, pos[i], kvh, head_dim, tmp);
+        axpy16(out, vr, scores[i], head_dim);
+    }
+}
+
+static int check_heads(int n_heads, int n_kv_heads, int head_dim) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0) return -1;
+    if (n_heads % n_kv_heads != 0) return -1;
+    return 0;
+}
+
+int orc_attention(float* out, const float* q, const orc_kv_layout* kv, int seq_len, int q_pos,
+                  int n_heads, int n_kv_heads, int head_dim, double* importance, int nthreads) {
+    if (!out || !q || !kv || seq_len <= 0 || q_pos < 0) return -1;
+    if (check_heads(n_heads, n_kv_heads, head_dim)) return -1;
+    int n_rep = n_heads / n_kv_heads;
+    int valid_end = q_pos < seq_len - 1 ? q_pos : seq_len - 1;
+    float scale = 1.0f / sqrtf((float)head_dim);
+    /* Per-head probabilities are kept so that the importance sum can be
+     * taken in head order (the reference adds under a Mutex in whatever
+     * order rayon finishes, ops.rs:362-368). */
+    float* probs = importance ? (float*)malloc(sizeof(float) * (size_t)seq_len * (size_t)n_heads) : NULL;
+    if (importance && !probs) return -3;
+    int err = 0;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)seq_len);
+        float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        if (!scores || !tmp) {
+#pragma omp atomic write
+            err = -3;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int h = 0; h < n_heads; h++) {
+                head_full(out + (size_t)h * head_dim, q + (size_t)h * head_dim, kv, h / n_rep,
+                          seq_len, valid_end, head_dim, scale, scores, tmp);
+                if (probs) memcpy(probs + (size_t)h * seq_len, scores, sizeof(float) * (size_t)seq_len);
+            }
+        }
+        free(scores);
+        free(tmp);
+    }
+    if (probs) {
+        if (!err)
+            for (int h = 0; h < n_heads; h++)
+                for (int t = 0; t < seq_len; t++) importance[t] += (double)probs[(size_t)h * seq_len + t];
+        free(probs);
+    }
+    return err;
+}
+
+int orc_attention_positions(float* out, const float* q, const orc_kv_layout* kv,
+                            const int32_t* positions, int n_pos, int n_heads, int n_kv_heads,
+                            int head_dim, int nthreads) {
+    if (!out || !q || !kv || !positions || n_pos <= 0) return -1;
+    if (check_heads(n_heads, n_kv_heads, head_dim)) return -1;
+    int n_rep = n_heads / n_kv_heads;
+    float scale = 1.0f / sqrtf((float)head_dim);
+    int err = 0;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)n_pos);
+        float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        if (!scores || !tmp) {
+#pragma omp atomic write
+            err = -3;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int h = 0; h < n_heads; h++)
+                head_positions(out + (size_t)h * head_dim, q + (size_t)h * head_dim, kv, h / n_rep,
+                               positions, n_pos, head_dim, scale, scores, tmp);
+        }
+        free(scores);
+        free(tmp);
+    }
+    return err;
+}
+
+/* Prefill as the reference executes it: one ops::attention call per token
+ * with seq_len = abs_pos + 1 and q_pos = abs_pos (executor.rs:132-137). */
+int orc_attention_rows(float* out, const float* q, int64_t q_row_stride, int64_t out_row_stride,
+                       const orc_kv_layout* kv, const int32_t* rows, int n_rows, int n_heads,
+                       int n_kv_heads, int head_dim, int nthreads) {
+    if (!out || !q || !kv || !rows || n_rows <= 0) return -1;
+    if (check_heads(n_heads, n_kv_heads, head_dim)) return -1;
+    int n_rep = n_heads / n_kv_heads;
+    float scale = 1.0f / sqrtf((float)head_dim);
+    int max_row = 0;
+    for (int i = 0; i < n_rows; i++) {
+        if (rows[i] < 0) return -1;
+        if (rows[i] > max_row) max_row = rows[i];
+    }
+    int err = 0;
+    long long total = (long long)n_rows * n_heads;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(max_row + 1));
+        float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        if (!scores || !tmp) {
+#pragma omp atomic write
+            err = -3;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (long long w = 0; w < total; w++) {
+                int ri = (int)(w / n_heads), h = (int)(w % n_heads);
+                int r = rows[ri];
+                head_full(out + (size_t)r * out_row_stride + (size_t)h * head_dim,
+                          q + (size_t)r * q_row_stride + (size_t)h * head_dim, kv, h / n_rep, r + 1,
+                          r, head_dim, scale, scores, tmp);
+            }
+        }
+        free(scores);
+        free(tmp);
+    }
+    return err;
+}
+
+/* ------------------------------------------------------------------------
+ * mojo_softmax_padic (swamp-kernels/src/lib.rs:181-223) following its
+ * AVX-512 branch (lib.rs:110-179, 202-206), the one x86-64 AVX-512 hosts
+ * take; the scalar fallback (lib.rs:209-222) is not restated.
+ * --------------------------------------------------------------------- */
+
+/* Rust `f32 as i32`: truncate toward zero, saturate, NaN -> 0. */
+static int32_t sat_i32(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+/* exp_q16_16 (lib.rs:102-108) */
+int32_t orc_exp_q16_16(int32_t x_fixed) {
+    if (x_fixed < -655360) return 0;
+    if (x_fixed >= 0) return 65536;
+    float xr = (float)x_fixed / 65536.0f;
+    float r = roundf(expf(xr) * 65536.0f);
+    r = fmaxf(r, 0.0f);
+    return sat_i32(r);
+}
+
+void orc_softmax_padic(const float* logits, float* probs, int n, float temperature) {
+    if (!logits || !probs || n <= 0) return;
+    float inv_tmp = 1.0f / fmaxf(temperature, 1e-6f);
+    int32_t* fixed = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t* e = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+    if (!fixed || !e) {
+        free(fixed);
+        free(e);
+        return;
+    }
+    for (int i = 0; i < n; i++) fixed[i] = sat_i32((logits[i] * inv_tmp) * 65536.0f);
+    int32_t mx = INT32_MIN;
+    for (int i = 0; i < n; i++)
+        if (fixed[i] > mx) mx = fixed[i];
+    int64_t sum = 0;
+    for (int i = 0; i < n; i++) {
+        int32_t diff = (int32_t)((uint32_t)fixed[i] - (uint32_t)mx); /* wrapping, as release Rust */
+        e[i] = orc_exp_q16_16(diff);
+        sum += e[i];
+    }
+    if (sum > 0) {
+        int32_t inv = (int32_t)(uint32_t)((1ull << 32) / (uint64_t)sum);
+        int simd_end = (n / 16) * 16;
+        for (int i = 0; i < simd_end; i++) /* _mm512_mullo_epi32 + _mm512_srli_epi32(.,16) */
+            e[i] = (int32_t)(((uint32_t)e[i] * (uint32_t)inv) >> 16);
+        for (int i = simd_end; i < n; i++)
+            e[i] = (int32_t)(((int64_t)e[i] * (int64_t)inv) >> 16);
+    }
+    for (int i = 0; i < n; i++) probs[i] = (float)e[i] / 65536.0f;
+    free(fixed);
+    free(e);
+}
+
+/* ------------------------------------------------------------------------
+ * StokesKVCacheSim + mojo_stokes_* (swamp-kernels/src/lib.rs:27-85):
+ * append K, V, score; above 4096 tokens drop the first minimum-score token.
+ * The reference panics on a NaN comparison (partial_cmp().unwrap()); here
+ * that case returns -1 and leaves the cache unchanged past the append.
+ * --------------------------------------------------------------------- */
+typedef struct {
+    int n, cap, head_dim;
+    float *keys, *values, *scores;
+} orc_stokes;
+
+void* orc_stokes_init(int head_dim) {
+    orc_stokes* c = (orc_stokes*)calloc(1, sizeof(orc_stokes));
+    if (c) c->head_dim = head_dim;
+    return c;
+}
+
+void orc_stokes_free(void* p) {
+    orc_stokes* c = (orc_stokes*)p;
+    if (!c) return;
+    free(c->keys);
+    free(c->values);
+    free(c->scores);
+    free(c);
+}
+
+int orc_stokes_append(void* p, int token_id, const float* key, const float* value, float score) {
+    (void)token_id;
+    orc_stokes* c = (orc_stokes*)p;
+    if (!c || !key || !value) return 0;
+    int hd = c->head_dim;
+    if (c->n == c->cap) {
+        int nc = c->cap ? c->cap * 2 : 64;
+        float* k = (float*)realloc(c->keys, sizeof(float) * (size_t)nc * (size_t)hd);
+        if (!k) return -3;
+        c->keys = k;
+        float* v = (float*)realloc(c->values, sizeof(float) * (size_t)nc * (size_t)hd);
+        if (!v) return -3;
+        c->values = v;
+        float* s = (float*)realloc(c->scores, sizeof(float) * (size_t)nc);
+        if (!s) return -3;
+        c->scores = s;
+        c->cap = nc;
+    }
+    memcpy(c->keys + (size_t)c->n * hd, key, sizeof(float) * (size_t)hd);
+    memcpy(c->values + (size_t)c->n * hd, value, sizeof(float) * (size_t)hd);
+    c->scores[c->n] = score;
+    c->n++;
+    if (c->n > 4096) {
+        int mi = 0;
+        for (int i = 0; i < c->n; i++)
+            if (c->scores[i] != c->scores[i]) return -1;
+        for (int i = 1; i < c->n; i++)
+            if (c->scores[i] < c->scores[mi]) mi = i;
+        size_t tail = (size_t)(c->n - mi - 1);
+        memmove(c->keys + (size_t)mi * hd, c->keys + (size_t)(mi + 1) * hd, sizeof(float) * tail * hd);
+        memmove(c->values + (size_t)mi * hd, c->values + (size_t)(mi + 1) * hd, sizeof(float) * tail * hd);
+        memmove(c->scores + mi, c->scores + mi + 1, sizeof(float) * tail);
+        c->n--;
+    }
+    return 0;
+}
+
+int orc_stokes_count(const void* p) { return p ? ((const orc_stokes*)p)->n : 0; }
+
+int orc_stokes_read(const void* p, float* keys, float* values, float* scores) {
+    const orc_stokes* c = (const orc_stokes*)p;
+    if (!c) return -1;
+    if (keys) memcpy(keys, c->keys, sizeof(float) * (size_t)c->n * c->head_dim);
+    if (values) memcpy(values, c->values, sizeof(float) * (size_t)c->n * c->head_dim);
+    if (scores) memcpy(scores, c->scores, sizeof(float) * (size_t)c->n);
+    return c->n;
+}

@@ -1,0 +1,269 @@
+"""ctypes front-end of the CPU oracle (oracle/nyion_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker.  The product library never
+imports it.
+
+The oracle restates the reference's CPU attention (swamp-engine/src/ops.rs),
+its Q4-20B codec and zone page arithmetic (swamp-engine/src/cache.rs) and the
+swamp-kernels C-ABI (swamp-kernels/src/lib.rs).  Each C function cites the
+lines it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnyion_oracle.so")
+
+KV_F32 = 0
+KV_Q4 = 1
+CONTIGUOUS = 1 << 40  # block_tokens larger than any position
+
+
+class KVLayout(C.Structure):
+    _fields_ = [
+        ("k_base", C.c_void_p),
+        ("v_base", C.c_void_p),
+        ("table", C.c_void_p),
+        ("block_tokens", C.c_int64),
+        ("block_stride", C.c_int64),
+        ("head_stride", C.c_int64),
+        ("token_stride", C.c_int64),
+        ("dtype", C.c_int32),
+        ("_pad", C.c_int32),
+    ]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        f32p = C.POINTER(C.c_float)
+        i32p = C.POINTER(C.c_int32)
+        L.orc_dot_avx512_order.restype = C.c_float
+        L.orc_dot_avx512_order.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.orc_weighted_sum.argtypes = [C.c_void_p, C.c_void_p, C.c_float, C.c_int]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_q4_row_bytes.restype = C.c_int
+        L.orc_q4_row_bytes.argtypes = [C.c_int]
+        L.orc_q4_quantize_row.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+        L.orc_q4_dequant_row.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+        L.orc_q4_quantize_rows.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+        L.orc_q4_dequant_rows.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+        for name in ("orc_zone_index", "orc_zone_block_size", "orc_zone_slot_in_page",
+                     "orc_zone_page_start", "orc_zone_total_pages"):
+            getattr(L, name).restype = C.c_int64
+            getattr(L, name).argtypes = [C.c_int64]
+        L.orc_zone_page_id.restype = C.c_int64
+        L.orc_zone_page_id.argtypes = [C.c_int64, C.c_int64]
+        L.orc_zone_f32_offset.restype = C.c_int64
+        L.orc_zone_f32_offset.argtypes = [C.c_int64] * 5
+        L.orc_zone_q4_offset.restype = C.c_int64
+        L.orc_zone_q4_offset.argtypes = [C.c_int64] * 5
+        L.orc_sparse_positions.restype = C.c_int
+        L.orc_sparse_positions.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int]
+        L.orc_fugu_positions.restype = C.c_int
+        L.orc_fugu_positions.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int,
+                                         C.c_void_p, C.c_int]
+        L.orc_attention.restype = C.c_int
+        L.orc_attention.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(KVLayout), C.c_int, C.c_int,
+                                    C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int]
+        L.orc_attention_positions.restype = C.c_int
+        L.orc_attention_positions.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(KVLayout),
+                                              C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                              C.c_int]
+        L.orc_attention_rows.restype = C.c_int
+        L.orc_attention_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
+                                         C.POINTER(KVLayout), C.c_void_p, C.c_int, C.c_int,
+                                         C.c_int, C.c_int, C.c_int]
+        L.orc_exp_q16_16.restype = C.c_int32
+        L.orc_exp_q16_16.argtypes = [C.c_int32]
+        L.orc_softmax_padic.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        L.orc_stokes_init.restype = C.c_void_p
+        L.orc_stokes_init.argtypes = [C.c_int]
+        L.orc_stokes_append.restype = C.c_int
+        L.orc_stokes_append.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_float]
+        L.orc_stokes_free.argtypes = [C.c_void_p]
+        L.orc_stokes_count.restype = C.c_int
+        L.orc_stokes_count.argtypes = [C.c_void_p]
+        L.orc_stokes_read.restype = C.c_int
+        L.orc_stokes_read.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_max_threads.restype = C.c_int
+        _ = (f32p, i32p)
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+# ----------------------------------------------------------------------------
+# layouts
+# ----------------------------------------------------------------------------
+
+def paged_layout(k_pool: np.ndarray, v_pool: np.ndarray, table: np.ndarray | None,
+                 block_tokens: int, n_kv_heads: int, head_dim: int, dtype: int = KV_F32):
+    """Pool [num_blocks][Hkv][block_tokens][row] with row = D f32 or Q4 bytes."""
+    row = head_dim if dtype == KV_F32 else q4_row_bytes(head_dim)
+    lay = KVLayout(k_pool.ctypes.data, v_pool.ctypes.data,
+                   None if table is None else table.ctypes.data, block_tokens,
+                   n_kv_heads * block_tokens * row, block_tokens * row, row, dtype, 0)
+    lay._keep = (k_pool, v_pool, table)
+    return lay
+
+
+def contiguous_layout(k: np.ndarray, v: np.ndarray, kv_stride: int, head_dim: int,
+                      dtype: int = KV_F32):
+    """[Hkv][kv_stride][row] (the Attention node / gpu_attention_device layout)."""
+    row = head_dim if dtype == KV_F32 else q4_row_bytes(head_dim)
+    lay = KVLayout(k.ctypes.data, v.ctypes.data, None, CONTIGUOUS, 0, kv_stride * row, row,
+                   dtype, 0)
+    lay._keep = (k, v)
+    return lay
+
+
+def token_major_layout(k: np.ndarray, v: np.ndarray, n_kv_heads: int, head_dim: int):
+    """[N][Hkv][D] f32 (the per-token K/V the QKV projection produces)."""
+    lay = KVLayout(k.ctypes.data, v.ctypes.data, None, CONTIGUOUS, 0, head_dim,
+                   n_kv_heads * head_dim, KV_F32, 0)
+    lay._keep = (k, v)
+    return lay
+
+
+# ----------------------------------------------------------------------------
+# attention
+# ----------------------------------------------------------------------------
+
+def attention(q: np.ndarray, layout: KVLayout, seq_len: int, q_pos: int, n_heads: int,
+              n_kv_heads: int, head_dim: int, importance: bool = False, threads: int = 1):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    imp = np.zeros(seq_len, dtype=np.float64) if importance else None
+    rc = lib().orc_attention(out.ctypes.data, q.ctypes.data, C.byref(layout), seq_len, q_pos,
+                             n_heads, n_kv_heads, head_dim, _ptr(imp), threads)
+    if rc != 0:
+        raise ValueError(f"orc_attention failed rc={rc}")
+    return (out, imp) if importance else out
+
+
+def attention_positions(q: np.ndarray, layout: KVLayout, positions: np.ndarray, n_heads: int,
+                        n_kv_heads: int, head_dim: int, threads: int = 1):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    rc = lib().orc_attention_positions(out.ctypes.data, q.ctypes.data, C.byref(layout),
+                                       pos.ctypes.data, len(pos), n_heads, n_kv_heads, head_dim,
+                                       threads)
+    if rc != 0:
+        raise ValueError(f"orc_attention_positions failed rc={rc}")
+    return out
+
+
+def attention_rows(q: np.ndarray, layout: KVLayout, rows, n_heads: int, n_kv_heads: int,
+                   head_dim: int, threads: int = 1, out: np.ndarray | None = None):
+    """q: [N][Hq*D] f32.  Returns out [N][Hq*D] with only `rows` filled."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n = q.shape[0]
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    if out is None:
+        out = np.zeros((n, n_heads * head_dim), dtype=np.float32)
+    rc = lib().orc_attention_rows(out.ctypes.data, q.ctypes.data, n_heads * head_dim,
+                                  n_heads * head_dim, C.byref(layout), rows.ctypes.data,
+                                  len(rows), n_heads, n_kv_heads, head_dim, threads)
+    if rc != 0:
+        raise ValueError(f"orc_attention_rows failed rc={rc}")
+    return out
+
+
+def sparse_positions(seq_len: int, q_pos: int, window: int, global_stride: int) -> np.ndarray:
+    cap = window + 130
+    buf = np.empty(cap, dtype=np.int32)
+    n = lib().orc_sparse_positions(seq_len, q_pos, window, global_stride, buf.ctypes.data, cap)
+    if n < 0:
+        raise ValueError(f"orc_sparse_positions rc={n}")
+    return buf[:n].copy()
+
+
+def fugu_positions(seq_len: int, q_pos: int, window: int, sentinel_stride: int,
+                   dspark) -> np.ndarray:
+    ds = np.ascontiguousarray(dspark, dtype=np.int32)
+    cap = window + 130 + len(ds)
+    buf = np.empty(cap, dtype=np.int32)
+    n = lib().orc_fugu_positions(seq_len, q_pos, window, sentinel_stride, ds.ctypes.data, len(ds),
+                                 buf.ctypes.data, cap)
+    if n < 0:
+        raise ValueError(f"orc_fugu_positions rc={n}")
+    return buf[:n].copy()
+
+
+# ----------------------------------------------------------------------------
+# Q4 codec
+# ----------------------------------------------------------------------------
+
+def q4_row_bytes(head_dim: int) -> int:
+    return ((head_dim + 31) // 32) * 20
+
+
+def q4_quantize_rows(x: np.ndarray) -> np.ndarray:
+    """x [..., D] f32 -> [..., row_bytes] u8 (one Q4-20B row per leading index)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    rb = q4_row_bytes(d)
+    flat = x.reshape(-1, d)
+    out = np.zeros((flat.shape[0], rb), dtype=np.uint8)
+    lib().orc_q4_quantize_rows(flat.ctypes.data, flat.shape[0], d, out.ctypes.data)
+    return out.reshape(x.shape[:-1] + (rb,))
+
+
+def q4_dequant_rows(b: np.ndarray, head_dim: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    rb = q4_row_bytes(head_dim)
+    flat = b.reshape(-1, rb)
+    out = np.empty((flat.shape[0], head_dim), dtype=np.float32)
+    lib().orc_q4_dequant_rows(flat.ctypes.data, flat.shape[0], head_dim, out.ctypes.data)
+    return out.reshape(b.shape[:-1] + (head_dim,))
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().orc_f32_to_f16(float(x)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().orc_f16_to_f32(int(h)))
+
+
+# ----------------------------------------------------------------------------
+# swamp-kernels C-ABI
+# ----------------------------------------------------------------------------
+
+def softmax_padic(logits, temperature: float = 1.0) -> np.ndarray:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.zeros_like(x)
+    lib().orc_softmax_padic(x.ctypes.data, out.ctypes.data, len(x), float(temperature))
+    return out
+
+
+def exp_q16_16(x: int) -> int:
+    return int(lib().orc_exp_q16_16(int(x)))
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())

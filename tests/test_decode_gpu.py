@@ -1,0 +1,230 @@
+"""Decode attention on the GPU against the oracle (gpu).
+
+Tolerance (BASELINE): max-abs-err <= 2e-3 and rel-err <= 1e-3, where rel-err
+is max|gpu - ref| / max|ref| over the compared tensor (fp32 accumulation on
+both sides).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-3
+
+
+def assert_close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = np.max(np.abs(got - ref))
+    rel = err / max(np.max(np.abs(ref)), 1e-30)
+    assert err <= ATOL and rel <= RTOL, f"{what}: max-abs {err:.3e} rel {rel:.3e}"
+    return err, rel
+
+
+def to_dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def run_paged(gpu, pb, window=0, global_stride=0, q_pos=None, max_ctx=None):
+    q = to_dev(pb.q)
+    kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    qp = None if q_pos is None else to_dev(np.asarray(q_pos, np.int32))
+    out = torch.full_like(q, float("nan"))
+    gpu.paged_decode(q, kp, vp, tab, ctx, out, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                     pb.block_tokens, kv_dtype=pb.kv_dtype, window=window,
+                     global_stride=global_stride, max_ctx=max_ctx, q_pos=qp)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# ---------------------------------------------------------------- node form
+
+def test_attention_node_c1(gpu):
+    q, k, v = W.c1_contiguous(seed=0)
+    ref = oracle.attention(q.reshape(-1), oracle.contiguous_layout(k, v, 128, 64), 128, 127, 32,
+                           4, 64).reshape(32, 64)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    out = torch.full_like(dq, float("nan"))
+    gpu.attention_node(dq, dk, dv, out, 32, 4, 128, 64, 128)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, "node C1")
+    # with the node's scores buffer as split-K workspace
+    scores = torch.empty(32 * 128, dtype=torch.float32, device="cuda")
+    out2 = torch.full_like(dq, float("nan"))
+    gpu.attention_node(dq, dk, dv, out2, 32, 4, 128, 64, 128, scores=scores)
+    torch.cuda.synchronize()
+    assert_close(out2.cpu().numpy(), ref, "node C1 + scores")
+
+
+def test_attention_node_stride_and_project_names(gpu):
+    rng = np.random.default_rng(21)
+    S, stride = 1000, 1536
+    q = rng.standard_normal((32, 64), dtype=np.float32)
+    k = rng.standard_normal((4, stride, 64), dtype=np.float32)
+    v = rng.standard_normal((4, stride, 64), dtype=np.float32)
+    ref = oracle.attention(q.reshape(-1), oracle.contiguous_layout(k, v, stride, 64), S, S - 1,
+                           32, 4, 64).reshape(32, 64)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    out = torch.full_like(dq, float("nan"))
+    L = gpu.load()
+    assert L.gpu_attention_device(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), 32,
+                                  4, S, 64, stride) == 0
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, "gpu_attention_device")
+    out.fill_(float("nan"))
+    scores = torch.empty(32 * stride, dtype=torch.float32, device="cuda")
+    gpu.attention_node(dq, dk, dv, out, 32, 4, S, 64, stride, scores=scores)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, "node stride")
+
+
+# ---------------------------------------------------------------- paged full causal
+
+def test_paged_c2_layer(gpu):
+    """BASELINE config 2, one layer: ctx 4096 in 16-token blocks, shuffled table."""
+    pb = W.paged_batch([4096], seed=2)
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), "C2 layer")
+
+
+@pytest.mark.parametrize("lens", [[1], [15, 16, 17], [1, 2, 31, 32, 33, 500, 1023, 1024, 1025]])
+def test_paged_edge_lengths(gpu, lens):
+    pb = W.paged_batch(lens, seed=len(lens))
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"lens {lens}")
+
+
+def test_paged_variable_batch_and_partitions(gpu):
+    lens = W.c3_lengths(seed=3, batch=24, lo=1, hi=3000)
+    pb = W.paged_batch(lens, seed=3, spare_blocks=7)
+    ref = W.reference_decode(pb, threads=8)
+    try:
+        for p in (16, 32, 128, 1024, 0):
+            gpu.set_partition_tokens(p)
+            assert_close(run_paged(gpu, pb), ref, f"partition {p}")
+    finally:
+        gpu.set_partition_tokens(0)
+
+
+def test_paged_q_pos(gpu):
+    pb = W.paged_batch([300, 1000, 64], seed=4)
+    q_pos = [100, 999, 0]
+    assert_close(run_paged(gpu, pb, q_pos=q_pos), W.reference_decode(pb, q_pos=q_pos), "q_pos")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(8, 8, 64), (16, 8, 64), (32, 8, 128), (64, 4, 64),
+                                             (32, 1, 128), (40, 2, 64)])
+def test_paged_head_shapes(gpu, n_heads, n_kv, hd):
+    pb = W.paged_batch([37, 700], n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, seed=5)
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"{n_heads}/{n_kv}/{hd}")
+
+
+def test_paged_c3_full_size(gpu):
+    """BASELINE config 3 at full size: 64 sequences, ctx ~ U[512, 32768]."""
+    lens = W.c3_lengths(seed=0)
+    pb = W.paged_batch(lens, seed=0)
+    got = run_paged(gpu, pb)
+    ref = W.reference_decode(pb, threads=oracle.max_threads())
+    assert_close(got, ref, "C3")
+
+
+# ---------------------------------------------------------------- window / Q4
+
+@pytest.mark.parametrize("stride", [0, 64])
+def test_window_boundaries(gpu, stride):
+    # valid_end in {window-1, window, window+1} and far past it
+    w = 256
+    pb = W.paged_batch([w, w + 1, w + 2, 3000, 9000], seed=6)
+    got = run_paged(gpu, pb, window=w, global_stride=stride)
+    assert_close(got, W.reference_decode(pb, window=w, global_stride=stride), f"window {stride}")
+
+
+@pytest.mark.parametrize("stride", [0, 64])
+def test_q4_window(gpu, stride):
+    pb = W.paged_batch([5000, 4097, 300, 12000], seed=7, kv_dtype=oracle.KV_Q4)
+    got = run_paged(gpu, pb, window=4096, global_stride=stride)
+    assert_close(got, W.reference_decode(pb, window=4096, global_stride=stride), f"q4 {stride}")
+
+
+def test_q4_full_and_d128(gpu):
+    for hd in (64, 128):
+        pb = W.paged_batch([1, 33, 2000], head_dim=hd, seed=8, kv_dtype=oracle.KV_Q4)
+        assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"q4 full d{hd}")
+
+
+def test_c4_full_size_window(gpu):
+    """B=8, ctx 131072, window 4096, Q4-20B.  Only the rows
+    the position set touches hold quantised N(0,1) data; every other row is
+    random bytes, so reading a wrong row shows up as garbage or NaN."""
+    B, ctx, w, bt, hkv, hd = 8, 131072, 4096, 16, 4, 64
+    rng = np.random.default_rng(9)
+    nblk = ctx // bt
+    total = B * nblk
+    perm = rng.permutation(total).astype(np.int32)
+    tables = perm.reshape(B, nblk)
+    rb = oracle.q4_row_bytes(hd)
+    kp = rng.integers(0, 256, size=(total, hkv, bt, rb), dtype=np.uint8)
+    vp = rng.integers(0, 256, size=(total, hkv, bt, rb), dtype=np.uint8)
+    q = rng.standard_normal((B, 32, hd), dtype=np.float32)
+    for stride in (0, 64):
+        pos = oracle.sparse_positions(ctx, ctx - 1, w, stride)
+        for b in range(B):
+            blk = tables[b, pos // bt]
+            kp[blk, :, pos % bt] = oracle.q4_quantize_rows(
+                rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+            vp[blk, :, pos % bt] = oracle.q4_quantize_rows(
+                rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+        pb = W.PagedBatch(q, kp, vp, tables, np.full(B, ctx, np.int32), 32, hkv, hd, bt,
+                          oracle.KV_Q4, 9)
+        got = run_paged(gpu, pb, window=w, global_stride=stride)
+        ref = W.reference_decode(pb, window=w, global_stride=stride, threads=8)
+        assert_close(got, ref, f"C4 stride {stride}")
+
+
+# ---------------------------------------------------------------- position lists
+
+def test_positions_fugu_set(gpu):
+    pb = W.paged_batch([6000, 2500], seed=10)
+    sets = [oracle.fugu_positions(6000, 5999, 256, 64, [5, 77, 5990, 3000, 4]),
+            oracle.fugu_positions(2500, 2499, 1024, 0, [17, 18, 2499])]
+    maxp = max(len(s) for s in sets)
+    pos = np.zeros((2, maxp), np.int32)
+    npos = np.array([len(s) for s in sets], np.int32)
+    for b, s in enumerate(sets):
+        pos[b, :len(s)] = s
+    out = torch.full((2, 32, 64), float("nan"), device="cuda")
+    import nyion_hip
+    nyion_hip.paged_decode_positions(to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool),
+                                     to_dev(pb.tables), to_dev(pos), to_dev(npos), out, 32, 4, 64,
+                                     16)
+    torch.cuda.synchronize()
+    ref = np.stack([oracle.attention_positions(pb.q[b], pb.layout(b), sets[b], 32, 4, 64).reshape(
+        32, 64) for b in range(2)])
+    assert_close(out.cpu().numpy(), ref, "positions")
+
+
+# ---------------------------------------------------------------- errors
+
+def test_error_paths(gpu):
+    import nyion_hip
+    pb = W.paged_batch([100], seed=11)
+    q, kp, vp = to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    out = torch.empty_like(q)
+    with pytest.raises(nyion_hip.NyionError) as e:
+        nyion_hip.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 64, 12)
+    assert e.value.code == nyion_hip.ERR_INVALID
+    with pytest.raises(nyion_hip.NyionError) as e:
+        nyion_hip.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 96, 16)
+    assert e.value.code == nyion_hip.ERR_UNSUPPORTED
+    L = nyion_hip.load()
+    rc = L.nyion_paged_decode_attention(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), tab.data_ptr(),
+                                        tab.shape[1], ctx.data_ptr(), None, 1, 32, 4, 64, 16,
+                                        kp.shape[0], 0, 0, 0, 100000, 0.0, out.data_ptr(), None, 0,
+                                        None)
+    assert rc == nyion_hip.ERR_INVALID  # max_ctx beyond the table

@@ -1,0 +1,83 @@
+"""swamp-kernels C-ABI on the GPU: mojo_softmax_padic and mojo_stokes_* (gpu).
+
+The Q16.16 softmax is integer arithmetic around one expf per element.  The
+GPU evaluates expf correctly rounded; the oracle calls glibc's expf, which
+can differ by one ulp, which after *65536 and rounding moves e_i by at most
+one count.  Outputs are therefore equal except for a rare +-1/65536 step
+(counted and bounded below); inputs whose exponentials are exact (equal
+logits, one dominant logit) must agree bit for bit.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_softmax(gpu, x, t):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    gpu.load().mojo_softmax_padic(x.ctypes.data, out.ctypes.data, len(x), float(t))
+    return out
+
+
+def test_softmax_padic_exact_cases(gpu):
+    for x, t in [([0.0, 0.0], 1.0), (np.zeros(16), 1.0), (np.r_[100.0, np.zeros(15)], 1.0),
+                 ([100.0, 0.0], 1.0), ([1e-7, 0.0], 0.0), ([np.nan, 0.0], 1.0),
+                 ([1, 2, 3, .5, -1, 4, 2.5, 1.5], 1.0)]:
+        assert np.array_equal(gpu_softmax(gpu, x, t), oracle.softmax_padic(x, t)), x
+
+
+def test_softmax_padic_vocab(gpu):
+    rng = np.random.default_rng(0)
+    for n, t in [(32000, 1.0), (50000, 0.7), (17, 2.0), (4096, 1.0)]:
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        got = gpu_softmax(gpu, x, t)
+        ref = oracle.softmax_padic(x, t)
+        diff = np.abs(got - ref) * 65536
+        assert diff.max() <= 2, (n, diff.max())
+        assert np.count_nonzero(diff) <= max(2, n // 500), (n, np.count_nonzero(diff))
+
+
+def test_softmax_padic_device_entry(gpu):
+    x = torch.randn(1000, device="cuda") * 2
+    p = torch.empty_like(x)
+    gpu.softmax_padic_dev(x, p, 1.0)
+    torch.cuda.synchronize()
+    ref = oracle.softmax_padic(x.cpu().numpy(), 1.0)
+    assert np.max(np.abs(p.cpu().numpy() - ref)) <= 2 / 65536
+
+
+def test_stokes_matches_oracle(gpu):
+    L = gpu.load()
+    O = oracle.lib()
+    hd = 8
+    c = L.mojo_stokes_init(hd)
+    o = O.orc_stokes_init(hd)
+    assert c
+    rng = np.random.default_rng(1)
+    scores = rng.standard_normal(4200).astype(np.float32)
+    scores[4150] = scores[:4150].min()  # a tie with an earlier minimum
+    for i in range(4200):
+        kv = np.full(hd, i, np.float32)
+        L.mojo_stokes_append(c, i, kv.ctypes.data, kv.ctypes.data, float(scores[i]))
+        O.orc_stokes_append(o, i, kv.ctypes.data, kv.ctypes.data, float(scores[i]))
+    n = L.nyion_stokes_count(c)
+    assert n == O.orc_stokes_count(o) == 4096
+    kg, vg, sg = (np.zeros((n, hd), np.float32), np.zeros((n, hd), np.float32),
+                  np.zeros(n, np.float32))
+    ko, vo, so = np.zeros_like(kg), np.zeros_like(vg), np.zeros_like(sg)
+    assert L.nyion_stokes_read(c, kg.ctypes.data, vg.ctypes.data, sg.ctypes.data) == n
+    O.orc_stokes_read(o, ko.ctypes.data, vo.ctypes.data, so.ctypes.data)
+    assert np.array_equal(kg, ko) and np.array_equal(vg, vo) and np.array_equal(sg, so)
+    L.mojo_stokes_free(c)
+    O.orc_stokes_free(o)
+    # null handles return silently, as the reference's extern "C" functions do
+    L.mojo_stokes_append(None, 0, None, None, 0.0)
+    L.mojo_stokes_free(None)
+    L.mojo_softmax_padic(None, None, 0, 1.0)
+    _ = C

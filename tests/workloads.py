@@ -1,0 +1,152 @@
+"""Seeded synthetic workloads for the attention path (tests and bench.py).
+
+Every tensor is drawn on the host with numpy's PCG64 (default_rng(seed)):
+q, k, v ~ N(0, 1) f32, RoPE considered already applied, scale 1/sqrt(D).
+Paged caches use 16-token blocks and a shuffled block table
+(rng.permutation), one pool shared by all sequences of a batch.
+
+Pool layout: [num_blocks][n_kv_heads][block_tokens][row], row = D f32 or the
+Q4-20B bytes of one (token, kv head).
+"""
+from __future__ import annotations
+
+import dataclasses
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for sub in ("oracle", "nyion.rs_amd"):
+    p = os.path.join(ROOT, sub)
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import oracle  # noqa: E402  (the checker)
+
+
+@dataclasses.dataclass
+class PagedBatch:
+    q: np.ndarray            # [B][Hq][D] f32
+    k_pool: np.ndarray       # [NB][Hkv][bt][row] f32 or u8
+    v_pool: np.ndarray
+    tables: np.ndarray       # [B][max_blocks] int32
+    ctx_lens: np.ndarray     # [B] int32
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    block_tokens: int
+    kv_dtype: int
+    seed: int
+
+    @property
+    def batch(self) -> int:
+        return self.q.shape[0]
+
+    def layout(self, b: int):
+        return oracle.paged_layout(self.k_pool, self.v_pool, self.tables[b], self.block_tokens,
+                                   self.n_kv_heads, self.head_dim, self.kv_dtype)
+
+    def kv_bytes(self, attended=None) -> int:
+        """Algorithmic K+V bytes read: every attended (token, kv head) row once."""
+        row = self.head_dim * 4 if self.kv_dtype == oracle.KV_F32 else oracle.q4_row_bytes(
+            self.head_dim)
+        toks = int(self.ctx_lens.sum()) if attended is None else int(attended)
+        return 2 * toks * self.n_kv_heads * row
+
+
+def _normal(rng, shape):
+    return rng.standard_normal(size=shape, dtype=np.float32)
+
+
+def paged_batch(ctx_lens, n_heads=32, n_kv_heads=4, head_dim=64, block_tokens=16, seed=0,
+                kv_dtype=oracle.KV_F32, spare_blocks=0) -> PagedBatch:
+    """One shared pool; sequence b owns ceil(ctx_b/bt) blocks at shuffled ids."""
+    rng = np.random.default_rng(seed)
+    ctx = np.asarray(ctx_lens, dtype=np.int32)
+    B = len(ctx)
+    nblk = (ctx + block_tokens - 1) // block_tokens
+    total = int(nblk.sum()) + spare_blocks
+    perm = rng.permutation(total).astype(np.int32)
+    max_blocks = int(nblk.max())
+    tables = np.zeros((B, max_blocks), dtype=np.int32)
+    off = 0
+    for b in range(B):
+        tables[b, :nblk[b]] = perm[off:off + nblk[b]]
+        off += nblk[b]
+    q = _normal(rng, (B, n_heads, head_dim))
+    k = _normal(rng, (total, n_kv_heads, block_tokens, head_dim))
+    v = _normal(rng, (total, n_kv_heads, block_tokens, head_dim))
+    if kv_dtype == oracle.KV_Q4:
+        k = oracle.q4_quantize_rows(k)
+        v = oracle.q4_quantize_rows(v)
+    return PagedBatch(q, k, v, tables, ctx, n_heads, n_kv_heads, head_dim, block_tokens, kv_dtype,
+                      seed)
+
+
+def c1_contiguous(seed=0):
+    """B=1, 32/4 heads, D=64, contiguous f32 KV of 128 positions."""
+    rng = np.random.default_rng(seed)
+    q = _normal(rng, (32, 64))
+    k = _normal(rng, (4, 128, 64))
+    v = _normal(rng, (4, 128, 64))
+    return q, k, v
+
+
+def c3_lengths(seed=0, batch=64, lo=512, hi=32768):
+    """per-sequence context lengths ~ U[lo, hi]."""
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=batch).astype(np.int32)
+
+
+def reference_decode(pb: PagedBatch, window=0, global_stride=0, q_pos=None, threads=1,
+                     batches=None):
+    """Oracle output [B][Hq][D] for the batch (A1 or A3 semantics)."""
+    out = np.zeros_like(pb.q)
+    for b in (range(pb.batch) if batches is None else batches):
+        L = int(pb.ctx_lens[b])
+        qp = L - 1 if q_pos is None else int(q_pos[b])
+        lay = pb.layout(b)
+        if window > 0:
+            pos = oracle.sparse_positions(L, qp, window, global_stride)
+            out[b] = oracle.attention_positions(pb.q[b], lay, pos, pb.n_heads, pb.n_kv_heads,
+                                                pb.head_dim, threads).reshape(pb.n_heads, -1)
+        else:
+            out[b] = oracle.attention(pb.q[b], lay, L, qp, pb.n_heads, pb.n_kv_heads,
+                                      pb.head_dim, threads=threads).reshape(pb.n_heads, -1)
+    return out
+
+
+def prefill_inputs(n, n_heads=32, n_kv_heads=8, head_dim=128, seed=0):
+    """BASELINE config 5 shapes: fp32 N(0,1) q [n][Hq][D], k, v [n][Hkv][D]."""
+    rng = np.random.default_rng(seed)
+    q = _normal(rng, (n, n_heads, head_dim))
+    k = _normal(rng, (n, n_kv_heads, head_dim))
+    v = _normal(rng, (n, n_kv_heads, head_dim))
+    return q, k, v
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round f32 to the nearest bf16 (ties to even), returned as f32."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    lsb = (b >> 16) & 1
+    r = ((b + 0x7FFF + lsb) & 0xFFFF0000).astype(np.uint32)
+    nan = np.isnan(x)
+    r[nan] = (b[nan] | 0x00400000) & 0xFFFF0000
+    return r.view(np.float32)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def brute_force_attention(q, k, v, valid_end, scale=None):
+    """float64 softmax(q K^T * scale) V over keys [0, valid_end]; q [D], k/v [T][D]."""
+    q = q.astype(np.float64)
+    k = k[:valid_end + 1].astype(np.float64)
+    v = v[:valid_end + 1].astype(np.float64)
+    s = (k @ q) * (scale if scale is not None else 1.0 / np.sqrt(q.shape[0]))
+    s -= s.max()
+    p = np.exp(s)
+    p /= p.sum()
+    return p @ v
