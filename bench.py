@@ -1,0 +1,415 @@
+"""Benchmark of the MI355X attention path (one GPU).
+
+Workload of the headline line: one full 22-layer decode
+step at TinyLlama-1.1B attention shape -- batch 1, 32 q / 4 kv heads,
+head_dim 64, f32 KV context 4096 in a paged cache of 16-token blocks with a
+seeded random permutation block table.  A step is 22 calls of
+nyion_paged_decode_attention, one per layer, each on its own K/V pools.
+Inputs are resident in HBM before timing.  Three independent copies of the
+22-layer cache (555 MB) are rotated step to step, so the 185 MB of one step
+never sits in the 256 MB Infinity Cache from the previous step.
+
+metric/unit: achieved algorithmic HBM bandwidth of the decode step in GB/s
+(K + V + q + out + block table bytes, counted once), with us/layer beside it.
+The other BASELINE configs are measured in the same run and reported under
+"configs": C1 (contiguous 128-position node), C3 (64-sequence continuous
+batch), C4 (4-bit KV, 131072 context, window 4096) and C5 (causal prefill,
+TFLOP/s against the bf16 MFMA peak).
+
+roofline: the decode call (decode kernel + split-K merge kernel) timed with
+HIP events on the stream it is launched on, against 8 TB/s.
+cpu_baseline: the C restatement of ops::attention (oracle/, the reference's
+AVX-512 dot/axpy order, OpenMP over heads) on the host cores, one C2 layer at
+a time, 6 threads (the reference executor's rayon pool) and all cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for sub in ("nyion.rs_amd", "oracle", "tests"):
+    sys.path.insert(0, os.path.join(ROOT, sub))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = ("decode-attn µs/layer + achieved HBM GB/s (% peak); prefill TFLOP/s (% MFMA)")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5 (default all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 512 MiB device copy (PMC traffic calibration)")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------------------
+# helpers
+# ----------------------------------------------------------------------------
+
+def timed(fn, steps, warmup, torch):
+    """W untimed, then K timed; synchronize on both sides; ms per call."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def event_times(fn, reps, torch):
+    """Per-call device durations (ms) from HIP events on the current stream."""
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for i, (a, b) in enumerate(evs):
+        a.record(st)
+        fn(i)
+        b.record(st)
+    torch.cuda.synchronize()
+    return np.array([a.elapsed_time(b) for a, b in evs])
+
+
+def paged_tables(rng, n_seqs, nblk, total):
+    perm = rng.permutation(total).astype(np.int32)
+    return perm[: n_seqs * nblk].reshape(n_seqs, nblk)
+
+
+# ----------------------------------------------------------------------------
+# C2: 22-layer decode step (headline)
+# ----------------------------------------------------------------------------
+
+def bench_c2(nh, torch, steps, warmup, seed=0):
+    L, ctx, Hq, Hkv, D, bt = 22, 4096, 32, 4, 64, 16
+    R = 3  # rotated copies of the whole 22-layer cache
+    nblk = ctx // bt
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    layers = []
+    for r in range(R):
+        sets = []
+        for layer in range(L):
+            kp = torch.randn((nblk, Hkv, bt, D), generator=g, device="cuda")
+            vp = torch.randn((nblk, Hkv, bt, D), generator=g, device="cuda")
+            tab = torch.from_numpy(paged_tables(rng, 1, nblk, nblk)).cuda()
+            q = torch.randn((1, Hq, D), generator=g, device="cuda")
+            sets.append((q, kp, vp, tab))
+        layers.append(sets)
+    ctx_t = torch.full((1,), ctx, dtype=torch.int32, device="cuda")
+    outs = [torch.empty((1, Hq, D), device="cuda") for _ in range(L)]
+    ws_bytes = nh.decode_workspace_size(1, Hq, Hkv, D, ctx)
+    ws = nh.alloc_workspace(ws_bytes)
+
+    def layer_call(r, layer):
+        q, kp, vp, tab = layers[r][layer]
+        nh.paged_decode(q, kp, vp, tab, ctx_t, outs[layer], Hq, Hkv, D, bt, max_ctx=ctx,
+                        workspace=ws)
+
+    def step(i):
+        r = i % R
+        for layer in range(L):
+            layer_call(r, layer)
+
+    bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
+    ms = timed(step, steps, warmup, torch)
+    # roofline: per decode call, HIP events on the launching stream
+    per = event_times(lambda i: layer_call(i % R, i % L), steps * 4, torch)
+    us_call = float(np.mean(per) * 1e3)
+    achieved = bytes_layer / (us_call * 1e-6) / 1e9
+    return {
+        "ms_per_step": ms,
+        "us_per_layer": ms * 1e3 / L,
+        "gbs": L * bytes_layer / (ms * 1e-3) / 1e9,
+        "bytes_per_layer": bytes_layer,
+        "call_us_event_mean": us_call,
+        "call_us_event_p10_p90": [float(np.percentile(per, 10) * 1e3),
+                                  float(np.percentile(per, 90) * 1e3)],
+        "achieved_call_gbs": achieved,
+        "partition_tokens": nh.partition_tokens(1, Hkv, D, ctx),
+        "workspace_bytes": ws_bytes,
+    }
+
+
+def cpu_baseline_c2(seed=0):
+    """Oracle (C restatement of ops::attention) on C2 layers, host cores."""
+    import oracle
+    import workloads as W
+
+    pb = W.paged_batch([4096], seed=seed)
+    lay = pb.layout(0)
+    bytes_layer = 2 * 4096 * 4 * 64 * 4 + 256 * 4 + 2 * 32 * 64 * 4
+    res = {}
+    ncores = os.cpu_count() or 1
+    try:
+        ncores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    for label, thr in (("6", 6), ("all", ncores)):
+        oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr)  # warm
+        n, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr)
+            n += 1
+            el = time.perf_counter() - t0
+            if el > 5.0 or n >= 2000:
+                break
+        res[label] = (thr, n, el / n * 1e6)
+    thr6, n6, us6 = res["6"]
+    thra, na, usa = res["all"]
+    return {
+        "value": bytes_layer / (us6 * 1e-6) / 1e9,
+        "unit": "GB/s",
+        "cores": thr6,
+        "kind": "port",
+        "sample": (f"{n6} single-layer C2 decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
+                   f"at {thr6} threads: {us6:.0f} us/layer; all {thra} cores: {usa:.0f} us/layer "
+                   f"({bytes_layer / (usa * 1e-6) / 1e9:.2f} GB/s)"),
+        "us_per_layer": us6,
+        "us_per_layer_all_cores": usa,
+        "cores_all": thra,
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ----------------------------------------------------------------------------
+# other configs
+# ----------------------------------------------------------------------------
+
+def bench_c1(nh, torch, steps, warmup):
+    import workloads as W
+
+    q, k, v = (torch.from_numpy(x).cuda() for x in W.c1_contiguous(seed=0))
+    out = torch.empty_like(q)
+    scores = torch.empty(32 * 128, device="cuda")
+
+    def call(i):
+        nh.attention_node(q, k, v, out, 32, 4, 128, 64, 128, scores=scores)
+
+    ms = timed(call, steps * 10, warmup, torch)
+    per = event_times(call, steps * 4, torch)
+    return {"us_per_layer": ms * 1e3, "call_us_event_mean": float(np.mean(per) * 1e3),
+            "bytes_per_layer": 278528}
+
+
+def bench_c3(nh, torch, steps, warmup, seed=0):
+    import workloads as W
+
+    Hq, Hkv, D, bt = 32, 4, 64, 16
+    lens = W.c3_lengths(seed=seed)
+    nblk = (lens + bt - 1) // bt
+    total = int(nblk.sum())
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.zeros((64, int(nblk.max())), np.int32)
+    off = 0
+    for b in range(64):
+        tables[b, : nblk[b]] = perm[off: off + nblk[b]]
+        off += nblk[b]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
+    vp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
+    q = torch.randn((64, Hq, D), generator=g, device="cuda")
+    tab = torch.from_numpy(tables).cuda()
+    ctx = torch.from_numpy(lens).cuda()
+    out = torch.empty_like(q)
+    maxc = int(lens.max())
+    ws = nh.alloc_workspace(nh.decode_workspace_size(64, Hq, Hkv, D, maxc))
+
+    def call(i):
+        nh.paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, max_ctx=maxc, workspace=ws)
+
+    toks = int(lens.sum())
+    nbytes = 2 * toks * Hkv * D * 4 + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
+    ms = timed(call, steps, warmup, torch)
+    per = event_times(call, steps, torch)
+    us = float(np.mean(per) * 1e3)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"us_per_layer": us, "us_per_layer_wall": ms * 1e3, "bytes": nbytes, "tokens": toks,
+            "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
+
+
+def bench_c4(nh, torch, steps, warmup, seed=0):
+    B, ctx, w, Hq, Hkv, D, bt = 8, 131072, 4096, 32, 4, 64, 16
+    nblk = ctx // bt
+    total = B * nblk
+    rng = np.random.default_rng(seed)
+    tables = rng.permutation(total).astype(np.int32).reshape(B, nblk)
+    rb = 40
+    kp = torch.empty((total, Hkv, bt, rb), dtype=torch.uint8, device="cuda")
+    vp = torch.empty_like(kp)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    rows = total * Hkv * bt
+    chunk = 1 << 22
+    for pool in (kp, vp):
+        flat = pool.view(-1, rb)
+        for s in range(0, rows, chunk):
+            n = min(chunk, rows - s)
+            x = torch.randn((n, D), generator=g, device="cuda")
+            nh.q4_quantize(x, n, D, flat[s: s + n])
+    torch.cuda.synchronize()
+    q = torch.randn((B, Hq, D), generator=g, device="cuda")
+    tab = torch.from_numpy(tables).cuda()
+    ctxt = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    res = {}
+    for stride in (0, 64):
+        ws = nh.alloc_workspace(nh.decode_workspace_size(B, Hq, Hkv, D, ctx, w, stride))
+
+        def call(i):
+            nh.paged_decode(q, kp, vp, tab, ctxt, out, Hq, Hkv, D, bt, kv_dtype=nh.KV_Q4_20B,
+                            window=w, global_stride=stride, max_ctx=ctx, workspace=ws)
+
+        n_pos = w + (128 if stride else 0)
+        nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4 + B * (n_pos // bt + 8) * 4
+        ms = timed(call, steps, warmup, torch)
+        per = event_times(call, steps, torch)
+        us = float(np.mean(per) * 1e3)
+        res[f"stride{stride}"] = {"us_per_layer": us, "us_per_layer_wall": ms * 1e3,
+                                  "bytes_packed": nbytes,
+                                  "gbs_packed": nbytes / (us * 1e-6) / 1e9}
+    return res
+
+
+def bench_c5(nh, torch, steps, warmup, seed=0):
+    n, Hq, Hkv, D, bt = 8192, 32, 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((n, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((n, Hq, D), device="cuda")
+    nblk = n // bt
+    tab = torch.from_numpy(np.random.default_rng(seed).permutation(nblk).astype(np.int32)).cuda()
+    kp = torch.empty((nblk, Hkv, bt, D), device="cuda")
+    vp = torch.empty_like(kp)
+    flops = 4 * Hq * D * n * (n + 1) / 2
+
+    def attn(i):
+        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D)
+
+    def attn_kv(i):
+        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D, k_pool=kp, v_pool=vp, block_table=tab,
+                        block_tokens=bt)
+
+    s = max(3, steps // 5)
+    ms = timed(attn, s, max(1, warmup // 5), torch)
+    per = event_times(attn, s, torch)
+    us = float(np.mean(per) * 1e3)
+    ms_kv = timed(attn_kv, s, 1, torch)
+    tf = flops / (us * 1e-6) / 1e12
+    return {"us": us, "us_wall": ms * 1e3, "us_with_kv_write": ms_kv * 1e3, "flops": flops,
+            "tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+
+
+# ----------------------------------------------------------------------------
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention path has no multi-GPU mode (each GPU "
+              "would run its own sequences or kv heads with no exchange); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import nyion_hip as nh
+
+    nh.init(0)
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5"}
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    res = {}
+    if args.calib_copy:
+        a = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration copy: 3 x 512 MiB")
+        del a, b
+    if "c2" in only:
+        log("C2: 22-layer decode step, ctx 4096")
+        res["c2"] = bench_c2(nh, torch, steps, warmup)
+    if "c1" in only:
+        log("C1: contiguous 128-position node")
+        res["c1"] = bench_c1(nh, torch, steps, warmup)
+    if "c3" in only:
+        log("C3: 64-sequence continuous batch")
+        res["c3"] = bench_c3(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
+    if "c4" in only:
+        log("C4: Q4 KV, ctx 131072, window 4096")
+        res["c4"] = bench_c4(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
+    if "c5" in only:
+        log("C5: causal prefill N=8192")
+        res["c5"] = bench_c5(nh, torch, steps, warmup)
+    cpu = None
+    if not args.no_cpu and "c2" in only:
+        log("CPU baseline (oracle) on C2 layers")
+        cpu = cpu_baseline_c2()
+
+    c2 = res.get("c2")
+    line = {
+        "metric": METRIC,
+        "value": round(c2["gbs"], 2) if c2 else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(c2["ms_per_step"], 4) if c2 else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1); paged 16-token blocks, shuffled tables)",
+        "config": {"workload": "decode-22-layer-tinyllama-ctx4096-paged16-f32", "batch": 1,
+                   "layers": 22, "n_heads": 32, "n_kv_heads": 4, "head_dim": 64,
+                   "context": 4096, "block_tokens": 16, "parallelism": "single-gpu"},
+    }
+    if c2:
+        line["us_per_layer"] = round(c2["us_per_layer"], 3)
+        line["roofline"] = {
+            "bound": "hbm",
+            "achieved": round(c2["achieved_call_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(c2["achieved_call_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_kernel<64,f32> + decode_merge_kernel<64> (one decode call)",
+            "bytes_per_launch": c2["bytes_per_layer"],
+            "launch_us": round(c2["call_us_event_mean"], 3),
+        }
+    if cpu:
+        line["cpu_baseline"] = cpu
+    line["configs"] = {k: v for k, v in res.items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -108,8 +108,12 @@ int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float
  * q_pos[batch] or NULL (= ctx_len-1).  max_ctx: host upper bound of ctx_lens,
  * sizes the grid.  scale <= 0 means 1/sqrt(head_dim).
  * head_dim in {64, 128}; n_heads % n_kv_heads == 0.
- * d_workspace: >= nyion_paged_decode_workspace_size(...) bytes, or NULL when
- * that size is 0. */
+ * d_workspace: >= nyion_paged_decode_workspace_size(...) bytes (256-byte
+ * aligned), or NULL when that size is 0.  It holds the split-K partials and
+ * per-(sequence, kv head) arrival counters: it must be zero-filled before its
+ * first use (nyion_decode_workspace_init, or any zeroing) and is left with
+ * the counters at zero by every call.  Calls that run concurrently need
+ * separate workspaces. */
 size_t nyion_paged_decode_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
                                          int max_ctx, int window, int global_stride);
 int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
@@ -135,7 +139,12 @@ int nyion_paged_decode_attention_positions(
     int num_blocks, int kv_dtype, float scale, float* d_out, void* d_workspace,
     size_t workspace_bytes, nyion_stream_t stream);
 
-/* Split-K partition length (tokens, power of two 16..4096) used by the decode
+/* Zero-fills a decode workspace on `stream` (a fill kernel, so it may be
+ * recorded into a HIP graph).  Needed once before first use. */
+int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion_stream_t stream);
+
+/* Split-K partition length in tokens per workgroup (4 wavefronts x 16-token
+ * tiles x tiles per wavefront: a power of two in 64..4096) used by the decode
  * entry points; 0 restores the automatic choice.  Process-wide; for tuning. */
 int nyion_set_decode_partition_tokens(int tokens);
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len);

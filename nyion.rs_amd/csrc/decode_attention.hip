@@ -3,29 +3,40 @@
 // One query token per sequence (the executor's decode step,
 // swamp-engine/src/executor.rs:739-763).  Semantics follow ops::attention
 // (swamp-engine/src/ops.rs:170-278) and ops::attention_sparse (ops.rs:85-168);
-// see the header for the position sets.
+// the header states the position sets.
 //
-// Work decomposition.  A wavefront owns one (sequence, kv head, group of up
-// to 16 q heads, split-K partition).  Four independent wavefronts share a
-// 256-thread workgroup; they never synchronise and use no LDS.  The 8 q heads
-// of a GQA group are processed together so each K/V byte is read from HBM
-// exactly once.
+// Work decomposition.  A 256-thread workgroup owns one (sequence, kv head,
+// group of up to 16 q heads, split-K partition); its four wavefronts take
+// consecutive runs of 16-token tiles of that partition.  All q heads of a GQA
+// group are processed together, so each K/V byte is read from HBM once.
 //
-// Per 16-token tile the wavefront issues two MFMA chains on
+// Per 16-token tile a wavefront runs two MFMA chains on
 // v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate):
 //   S[16 tok][16 heads] = K_tile[16][D] . Q^T[D][16]       (D/4 MFMAs)
 //   O[16 heads][D]     += P[16 heads][16 tok] . V_tile      (D/4 MFMAs)
 // The MFMA output layout of S (lane = head + 16*token_quad, reg = token in
-// quad) is exactly the A-operand layout P needs for the second product, so
-// probabilities never leave registers.  K and V rows are streamed with
-// 128-bit loads straight from the paged pool: for K, lanes (token i, quad k)
-// read 64 contiguous bytes per instruction of each row; for V, 16 lanes read
-// one whole row per instruction.  Q4-20B rows are dequantised in registers.
+// quad) is exactly the A-operand layout P needs in the second product, so the
+// probabilities never leave registers.
 //
-// Online softmax runs in the log2 domain on the S registers: tile max over
-// the 4 registers and the 4 token quads (lane xor 16, 32), rescale, exp2.
-// Partitions that do not cover the whole sequence write (m, l, acc) partials
-// to the workspace; decode_merge_kernel combines them (log-sum-exp).
+// Memory.  Tiles are aligned to 16 positions, so with blocks of >= 16 tokens
+// a tile lies in one block: its block id is one wave-uniform value, read from
+// a per-wavefront copy of the block-table slice loaded once.  K rows arrive as
+// 128-bit loads (the four token quads of a row read 64 contiguous bytes per
+// instruction), V rows as 16 lanes x 16 B = one whole row per instruction.
+// The next tile's loads are issued before the current tile's MFMAs (register
+// double buffering).  Q4-20B rows stay packed in registers until the tile is
+// consumed and are dequantised there, bit-exactly as dequant_block.
+//
+// Softmax.  Online, in the log2 domain, on the S registers: tile max over the
+// 4 registers and the 4 token quads (lane xor 16, 32), rescale, exp2.
+//
+// Split-K.  The four wavefronts of a workgroup merge through LDS.  When a
+// sequence needs several workgroups, each writes one (m, l, O) partial to the
+// workspace with device-coherent (write-through) stores, waits for them, and
+// counts its arrival with an agent-scope atomic; the last workgroup to arrive
+// reads the partials with device-coherent loads, merges them with
+// log-sum-exp, writes the output and resets its counter to 0.  No L2
+// write-back or invalidate is issued, and one decode call is one launch.
 #include <float.h>
 #include <math.h>
 
@@ -41,7 +52,7 @@ struct DecodeArgs {
     const float* q;  // [B][Hq][D]
     const void* k;
     const void* v;
-    const int32_t* tables;  // [B][table_stride] or nullptr (contiguous)
+    const int32_t* tables;     // [B][table_stride] or nullptr (contiguous)
     const int32_t* ctx_lens;   // [B] or nullptr (uniform_len)
     const int32_t* q_pos;      // [B] or nullptr (len - 1)
     const int32_t* positions;  // MODE_LIST: [B][pos_stride]
@@ -49,6 +60,7 @@ struct DecodeArgs {
     float* out;                // [B][Hq][D]
     float* ws_acc;             // [(b*Hq + head)*max_parts + p][D]
     float2* ws_ml;             // [(b*Hq + head)*max_parts + p] = (m log2, l)
+    int* counters;             // [B][Hkv][n_hg], zero between calls
     long long block_stride;
     long long head_stride;
     int table_stride;
@@ -64,56 +76,73 @@ struct DecodeArgs {
     int window;
     int global_stride;
     int mode;
-    int part_tokens;  // multiple of 16
-    int max_parts;
-    int max_len;       // host bound on attended positions per sequence
+    int tpw;        // tiles per wavefront per partition
+    int max_parts;  // workgroup partitions per (sequence, kv head, head group): grid.x
+    int max_len;    // host bound on attended positions per sequence
     float scale_log2;  // scale * log2(e)
 };
 
-struct SeqExtent {
-    int L;       // number of attended positions
-    int ws;      // window start (MODE_WINDOW)
-    int n_glob;  // strided globals before the window (MODE_WINDOW)
+// Attended positions of one sequence.
+//  aligned path (FULL/WINDOW, blocks >= 16 tokens): the contiguous range
+//    [lo, hi] walked in 16-aligned tiles from lo & ~15, plus n_glob strided
+//    globals (stride*g) in one extra partition;
+//  gather path: L virtual positions (the same sets, or an explicit list).
+struct Extent {
+    int lo, hi, n_glob, L;
+    int main_tiles;  // aligned: tiles over [lo & ~15, hi]
+    int np_main;     // partitions over the main tiles (aligned) or all tiles (gather)
+    int np;          // total partitions
 };
 
-// Attended position set of sequence b (ops.rs:97-113 for the window form,
-// ops.rs:183 for valid_end).
-// L is clamped to the host bound the grid and workspace were sized for.
-__device__ __forceinline__ SeqExtent seq_extent(const DecodeArgs& a, int b) {
-    SeqExtent e{0, 0, 0};
+template <bool ALIGNED>
+__device__ __forceinline__ Extent extent(const DecodeArgs& a, int b) {
+    Extent e{0, -1, 0, 0, 0, 0, 0};
+    const int per_part = 4 * a.tpw;  // tiles per workgroup partition
+    // per-sequence values are wave-uniform: keep them (and everything derived
+    // from them) in scalar registers so tile loops branch uniformly
     if (a.mode == MODE_LIST) {
-        e.L = min(max(a.n_pos[b], 0), a.max_len);
-        return e;
+        e.L = min(max(__builtin_amdgcn_readfirstlane(a.n_pos[b]), 0), a.max_len);
+    } else {
+        const int len = a.ctx_lens ? __builtin_amdgcn_readfirstlane(a.ctx_lens[b]) : a.uniform_len;
+        const int qp = a.q_pos ? __builtin_amdgcn_readfirstlane(a.q_pos[b]) : len - 1;
+        if (len <= 0 || qp < 0) return e;
+        const int ve = min(qp, len - 1);  // ops.rs:183
+        int lo = 0;
+        if (a.mode == MODE_WINDOW) {
+            lo = ve > a.window ? ve - a.window + 1 : 0;  // strict '>' (ops.rs:100)
+            e.n_glob = a.global_stride > 0 ? min(lo / a.global_stride, 128) : 0;
+        }
+        e.lo = lo;
+        e.hi = min(ve, lo + a.max_len - 1);
+        e.L = e.n_glob + (e.hi - lo + 1);
     }
-    const int len = a.ctx_lens ? a.ctx_lens[b] : a.uniform_len;
-    if (len <= 0) return e;
-    const int qp = a.q_pos ? a.q_pos[b] : len - 1;
-    if (qp < 0) return e;
-    const int ve = min(qp, len - 1);
-    if (a.mode == MODE_FULL) {
-        e.L = min(ve + 1, a.max_len);
-        return e;
+    if (ALIGNED) {
+        if (e.hi < e.lo) return e;
+        e.main_tiles = (e.hi - (e.lo & ~15)) / 16 + 1;
+        e.np_main = (e.main_tiles + per_part - 1) / per_part;
+        e.np = min(e.np_main + (e.n_glob > 0 ? 1 : 0), a.max_parts);
+    } else {
+        const int tiles = (e.L + 15) / 16;
+        e.np_main = (tiles + per_part - 1) / per_part;
+        e.np = min(e.np_main, a.max_parts);
     }
-    const int ws = ve > a.window ? ve - a.window + 1 : 0;
-    const int ng = a.global_stride > 0 ? min(ws / a.global_stride, 128) : 0;
-    e.ws = ws;
-    e.n_glob = ng;
-    e.L = min(ng + (ve - ws + 1), a.max_len);
     return e;
 }
 
-__device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const SeqExtent& e, int b, int v) {
+// Virtual index -> position, gather path (and the globals of the aligned path).
+__device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e, int b, int v) {
     if (a.mode == MODE_FULL) return v;
-    if (a.mode == MODE_WINDOW) return v < e.n_glob ? v * a.global_stride : e.ws + (v - e.n_glob);
+    if (a.mode == MODE_WINDOW) return v < e.n_glob ? v * a.global_stride : e.lo + (v - e.n_glob);
     return a.positions[(long long)b * a.pos_stride + v];
 }
 
-// ---------------------------------------------------------------- loaders
+// ---------------------------------------------------------------- tiles
 // K operand of lane (row i, quad kq): NC = D/4 values, one per QK MFMA.
 //   f32: call c = 4x+y holds dim 16x + 4kq + y  (per x, the 4 quads of a row
 //        read 64 contiguous bytes)
 //   Q4 : call c holds dim kq*D/4 + c            (contiguous nibbles)
-// The Q operand uses the same map (qk_dim).
+// The Q operand uses the same map (qk_dim).  V operand of lane (col j, quad
+// kq), row 4kq+r: DPL = D/16 consecutive dims from DPL*j.
 template <int D, int KVT>
 __device__ __forceinline__ int qk_dim(int c, int kq) {
     if constexpr (KVT == NYION_KV_F32)
@@ -122,99 +151,361 @@ __device__ __forceinline__ int qk_dim(int c, int kq) {
         return kq * (D / 4) + c;
 }
 
+// Raw (undecoded) registers of one tile for one lane.
 template <int D, int KVT>
-__device__ __forceinline__ void load_k(const void* base, long long off, int kq, float* kv) {
-    constexpr int NC = D / 4;
-    if (off < 0) {
-#pragma unroll
-        for (int c = 0; c < NC; c++) kv[c] = 0.f;
-        return;
-    }
+struct Tile;
+
+template <int D>
+struct Tile<D, NYION_KV_F32> {
+    float4 k[D / 16];         // K row j: dims 16x + 4kq .. +3
+    float4 v[4][D / 64];      // V rows 4kq+r: dims DPL*j .. +DPL
+};
+
+template <int D>
+struct Tile<D, NYION_KV_Q4_20B> {
+    uint32_t khdr;            // f16 d | f16 dmin << 16 of the lane's K group
+    uint32_t k[D / 32];       // D/4 nibbles of K row j
+    uint32_t vhdr[4];
+    uint32_t v[4];            // D/16 nibbles of V row 4kq+r (low 16 bits when D = 64)
+};
+
+// Loads are unconditional (an invalid row reads offset 0 of the pool, which is
+// valid memory) so that the compiler keeps them in flight across the MFMA
+// chain of the previous tile; invalid rows are masked when the tile is consumed.
+template <int D, int KVT>
+__device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const void* vb,
+                                          long long koff, const long long* voff, int j, int kq) {
     if constexpr (KVT == NYION_KV_F32) {
-        const float* row = (const float*)base + off;
+        const float* kr = (const float*)kb + koff;
 #pragma unroll
-        for (int x = 0; x < D / 16; x++) {
-            const float4 t = *(const float4*)(row + 16 * x + 4 * kq);
-            kv[4 * x + 0] = t.x;
-            kv[4 * x + 1] = t.y;
-            kv[4 * x + 2] = t.z;
-            kv[4 * x + 3] = t.w;
+        for (int x = 0; x < D / 16; x++) t.k[x] = *(const float4*)(kr + 16 * x + 4 * kq);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float* vr = (const float*)vb + voff[r] + (D / 16) * j;
+#pragma unroll
+            for (int x = 0; x < D / 64; x++) t.v[r][x] = *(const float4*)(vr + 4 * x);
         }
     } else {
-        const uint8_t* row = (const uint8_t*)base + off;
-        const int e0 = kq * (D / 4);  // first element of this lane
-        const int g = e0 >> 5;
-        const uint32_t hdr = *(const uint32_t*)(row + kQ4GroupBytes * g);
-        const float d = f16_bits_to_f32(hdr), dmin = f16_bits_to_f32(hdr >> 16);
-        const uint32_t* nib = (const uint32_t*)(row + kQ4GroupBytes * g + 4 + ((e0 & 31) >> 1));
+        const int ke0 = kq * (D / 4);
+        const uint8_t* kr = (const uint8_t*)kb + koff + kQ4GroupBytes * (ke0 >> 5);
+        t.khdr = *(const uint32_t*)kr;
+        const uint32_t* kn = (const uint32_t*)(kr + 4 + ((ke0 & 31) >> 1));
 #pragma unroll
-        for (int w = 0; w < D / 32; w++) q4_dequant8(nib[w], d, dmin, kv + 8 * w);
+        for (int w = 0; w < D / 32; w++) t.k[w] = kn[w];
+        const int ve0 = (D / 16) * j;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint8_t* vr = (const uint8_t*)vb + voff[r] + kQ4GroupBytes * (ve0 >> 5);
+            t.vhdr[r] = *(const uint32_t*)vr;
+            const uint8_t* vn = vr + 4 + ((ve0 & 31) >> 1);
+            if constexpr (D == 64)
+                t.v[r] = (uint32_t)(*(const uint16_t*)vn);
+            else
+                t.v[r] = *(const uint32_t*)vn;
+        }
     }
 }
 
-// V operand of lane (col j, quad kq) for one row: DPL = D/16 consecutive dims
-// starting at DPL*j.
 template <int D, int KVT>
-__device__ __forceinline__ void load_v(const void* base, long long off, int j, float* vv) {
-    constexpr int DPL = D / 16;
-    if (off < 0) {
-#pragma unroll
-        for (int t = 0; t < DPL; t++) vv[t] = 0.f;
-        return;
-    }
+__device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
     if constexpr (KVT == NYION_KV_F32) {
-        const float* row = (const float*)base + off + DPL * j;
 #pragma unroll
-        for (int x = 0; x < DPL / 4; x++) {
-            const float4 t = *(const float4*)(row + 4 * x);
-            vv[4 * x + 0] = t.x;
-            vv[4 * x + 1] = t.y;
-            vv[4 * x + 2] = t.z;
-            vv[4 * x + 3] = t.w;
+        for (int x = 0; x < D / 16; x++) {
+            kv[4 * x + 0] = t.k[x].x;
+            kv[4 * x + 1] = t.k[x].y;
+            kv[4 * x + 2] = t.k[x].z;
+            kv[4 * x + 3] = t.k[x].w;
         }
     } else {
-        const uint8_t* row = (const uint8_t*)base + off;
-        const int e0 = DPL * j;
-        const int g = e0 >> 5;
-        const uint32_t hdr = *(const uint32_t*)(row + kQ4GroupBytes * g);
-        const float d = f16_bits_to_f32(hdr), dmin = f16_bits_to_f32(hdr >> 16);
-        const uint8_t* nb = row + kQ4GroupBytes * g + 4 + ((e0 & 31) >> 1);
-        if constexpr (DPL == 8)
-            q4_dequant8(*(const uint32_t*)nb, d, dmin, vv);
-        else
-            q4_dequant4((uint32_t)(*(const uint16_t*)nb), d, dmin, vv);
+        const float d = f16_bits_to_f32(t.khdr), dmin = f16_bits_to_f32(t.khdr >> 16);
+#pragma unroll
+        for (int w = 0; w < D / 32; w++) q4_dequant8(t.k[w], d, dmin, kv + 8 * w);
     }
+}
+
+template <int D, int KVT>
+__device__ __forceinline__ void decode_v(const Tile<D, KVT>& t, int r, float* vv) {
+    if constexpr (KVT == NYION_KV_F32) {
+#pragma unroll
+        for (int x = 0; x < D / 64; x++) {
+            vv[4 * x + 0] = t.v[r][x].x;
+            vv[4 * x + 1] = t.v[r][x].y;
+            vv[4 * x + 2] = t.v[r][x].z;
+            vv[4 * x + 3] = t.v[r][x].w;
+        }
+    } else {
+        const float d = f16_bits_to_f32(t.vhdr[r]), dmin = f16_bits_to_f32(t.vhdr[r] >> 16);
+        if constexpr (D == 64)
+            q4_dequant4(t.v[r], d, dmin, vv);
+        else
+            q4_dequant8(t.v[r], d, dmin, vv);
+    }
+}
+
+// Running state of one wavefront: O (reg r of acc[t] = head 4kq+r, dim
+// DPL*j+t), per-head max (log2) and this lane's share of the denominator.
+template <int D>
+struct State {
+    floatx4 acc[D / 16];
+    float m;
+    float l;
+};
+
+// Rescale threshold of the online softmax, log2 units.  The running max of a
+// head is only moved when a tile's max exceeds it by more than this, so
+// exp2(s - m) <= 2^8 and the O rescale is rare after the first tiles.
+constexpr float kRescaleLog2 = 8.0f;
+
+// One tile: bit i of `mask` (wave-uniform) marks row i of the 16 valid;
+// MASKED = false is the all-valid fast path.
+template <int D, int KVT, bool MASKED>
+__device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t, const float* qv,
+                                             uint32_t mask, int kq, float scale_log2) {
+    constexpr int NC = D / 4;
+    constexpr int DPL = D / 16;
+    float kv[NC];
+    decode_k<D, KVT>(t, kv);
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
+
+    float sv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sv[r] = s[r] * scale_log2;
+        if (MASKED) sv[r] = ((mask >> (4 * kq + r)) & 1u) ? sv[r] : -1e30f;
+    }
+    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    if (__any(mt > st.m + kRescaleLog2)) {  // wave-uniform; first tile always
+        const float mnew = fmaxf(st.m, mt);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+        st.l *= alpha;
+        st.m = mnew;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * kq + r);
+#pragma unroll
+            for (int x = 0; x < DPL; x++) st.acc[x][r] *= ar;
+        }
+    }
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - st.m);
+    st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float vv[DPL];
+        decode_v<D, KVT>(t, r, vv);
+        if (MASKED) {  // masked rows may hold uninitialised slots: keep NaN out
+            const bool ok = (mask >> (4 * kq + r)) & 1u;
+#pragma unroll
+            for (int x = 0; x < DPL; x++) vv[x] = ok ? vv[x] : 0.f;
+        }
+#pragma unroll
+        for (int x = 0; x < DPL; x++)
+            st.acc[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv[x], st.acc[x], 0, 0, 0);
+    }
+}
+
+template <int D, int KVT>
+__device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, const float* qv,
+                                        uint32_t mask, int kq, float scale_log2) {
+    if (mask == 0xffffu)
+        consume_tile<D, KVT, false>(st, t, qv, mask, kq, scale_log2);
+    else if (mask)
+        consume_tile<D, KVT, true>(st, t, qv, mask, kq, scale_log2);
+}
+
+// Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
+// one block; valid rows [vlo, vhi].
+struct AlignedWalk {
+    int base;        // lo & ~15
+    int lo, hi;
+    int bi_first;    // first block index of this wavefront's tiles
+    int tblv;        // lane l: block id of block index bi_first + l (or -1)
+    long long head_off;
+};
+
+template <int D, int KVT>
+__device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const AlignedWalk& w,
+                                                    int tile, int j, int kq, long long& koff,
+                                                    long long* voff) {
+    const int t0 = w.base + 16 * tile;
+    int blk = 0;
+    if (a.tables) blk = __builtin_amdgcn_readlane(w.tblv, (t0 >> a.bt_log2) - w.bi_first);
+    const int vlo = max(w.lo - t0, 0);
+    const int vhi = min(w.hi - t0, 15);
+    uint32_t mask = (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
+    if (blk < 0) {  // block index past the table or block id out of range
+        blk = 0;
+        mask = 0;
+    }
+    // rows of a paged pool are contiguous: the token stride is the row size
+    constexpr int TS = KVT == NYION_KV_F32 ? D : q4_row_bytes(D);
+    const long long base = (long long)blk * a.block_stride + w.head_off +
+                           (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
+    koff = base + j * TS;
+    const long long vbase = base + 4 * kq * TS;
+#pragma unroll
+    for (int r = 0; r < 4; r++) voff[r] = vbase + r * TS;
+    return mask;
+}
+
+// Gather path: virtual indices v0 .. v0+15 (< vend), one table lookup per
+// row.  Invalid rows point at offset 0 and are masked.
+template <int D, int KVT>
+__device__ __forceinline__ uint32_t gather_offsets(const DecodeArgs& a, const Extent& e,
+                                                   const RowMap& m, int b, int kvh, int v0,
+                                                   int vend, bool globals, int j, int kq,
+                                                   long long& koff, long long* voff) {
+    auto off_of = [&](int v) -> long long {
+        if (v >= vend) return -1;
+        const int pos = globals ? v * a.global_stride : virt_to_pos(a, e, b, v);
+        if (pos < 0) return -1;
+        return row_offset(m, pos, kvh);
+    };
+    koff = off_of(v0 + j);
+    const uint32_t mask = (uint32_t)(__ballot(koff >= 0) & 0xffffu);
+    koff = koff < 0 ? 0 : koff;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const long long o = off_of(v0 + 4 * kq + r);
+        voff[r] = o < 0 ? 0 : o;
+    }
+    return mask;
+}
+
+// Walk `n` tiles with the next tile's loads in flight during each MFMA chain.
+// Every step issues exactly one tile of loads (at the end, a repeat of the
+// last tile that is never consumed), so the number of loads in flight is the
+// same on every path and each tile waits only for its own loads.
+template <int D, int KVT, typename Offsets>
+__device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, const float* qv, int n,
+                                           int j, int kq, Offsets offsets) {
+    Tile<D, KVT> ta, tb;
+    long long ko, vo[4];
+    if (n <= 0) return;
+    uint32_t ma = offsets(0, ko, vo);
+    load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
+    for (int i = 0; i < n; i += 2) {
+        uint32_t mb = offsets(min(i + 1, n - 1), ko, vo);
+        load_tile<D, KVT>(tb, a.k, a.v, ko, vo, j, kq);
+        consume<D, KVT>(st, ta, qv, ma, kq, a.scale_log2);
+        ma = offsets(min(i + 2, n - 1), ko, vo);
+        load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
+        if (i + 1 < n) consume<D, KVT>(st, tb, qv, mb, kq, a.scale_log2);
+    }
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// Log-sum-exp merge of the np partials of one (sequence, q head) by one
+// wavefront: lanes over partitions for the weights, lanes over dims for O.
+// The partials come from other workgroups, so they are read with
+// device-coherent loads, 32 partitions' worth issued before any is used.
+template <int D>
+__device__ void merge_head(const DecodeArgs& a, long long slot0, int np, float* out, int lane) {
+    constexpr int X = D / 64;  // dims per lane
+    constexpr int CH = 32;     // partitions per batch of loads
+    const float* mlp = (const float*)(a.ws_ml + slot0);
+    float mx = -INFINITY;
+    for (int p = lane; p < np; p += 64)
+        mx = fmaxf(mx, __hip_atomic_load(mlp + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    mx = wave_max(mx);
+    float lsum = 0.f;
+    float acc[X];
+#pragma unroll
+    for (int x = 0; x < X; x++) acc[x] = 0.f;
+    for (int p0 = 0; p0 < np; p0 += 64) {
+        const int p = p0 + lane;
+        float w = 0.f;
+        if (p < np) {
+            const float m_p = __hip_atomic_load(mlp + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float l_p = __hip_atomic_load(mlp + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            w = m_p == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_p - mx);
+            lsum = __builtin_fmaf(l_p, w, lsum);
+        }
+        const int cnt = min(64, np - p0);
+        for (int q0 = 0; q0 < cnt; q0 += CH) {
+            const float* src = a.ws_acc + (slot0 + p0 + q0) * D + lane;
+            float v[CH][X];
+#pragma unroll
+            for (int q = 0; q < CH; q++)
+#pragma unroll
+                for (int x = 0; x < X; x++)
+                    v[q][x] = (q0 + q < cnt) ? __hip_atomic_load(src + (long long)q * D + 64 * x,
+                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                             : 0.f;
+#pragma unroll
+            for (int q = 0; q < CH; q++) {
+                const float wq = __shfl(w, q0 + q);
+#pragma unroll
+                for (int x = 0; x < X; x++) acc[x] = __builtin_fmaf(wq, v[q][x], acc[x]);
+            }
+        }
+    }
+    lsum = wave_sum(lsum);
+    const float inv = 1.0f / lsum;
+#pragma unroll
+    for (int x = 0; x < X; x++) out[lane + 64 * x] = acc[x] * inv;
 }
 
 // ---------------------------------------------------------------- kernel
 
-template <int D, int KVT>
+template <int D, int KVT, bool ALIGNED>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-    constexpr int NC = D / 4;    // QK MFMAs per tile
-    constexpr int DPL = D / 16;  // PV output tiles (dims per lane per row)
+    constexpr int NC = D / 4;
+    constexpr int DPL = D / 16;
+    __shared__ floatx4 sm_acc[3][DPL][64];
+    __shared__ float sm_m[4][16];
+    __shared__ float sm_l[4][16];
+    __shared__ int sm_last;
 
     const int lane = threadIdx.x & 63;
-    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (p >= a.max_parts) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15;
+    const int kq = lane >> 4;
     const int kvh = blockIdx.y / a.n_hg;
     const int hg = blockIdx.y - kvh * a.n_hg;
     const int b = blockIdx.z;
-
-    const SeqExtent e = seq_extent(a, b);
-    const int j = lane & 15;
-    const int kq = lane >> 4;
+    const int wgp = blockIdx.x;
     const int g_local = min(16, a.group - hg * 16);
     const int head0 = kvh * a.group + hg * 16;
-    if (e.L <= 0) {  // nothing to attend to (ctx_len <= 0 or q_pos < 0): zeros
-        if (p == 0)
-            for (int i = lane; i < g_local * D; i += 64)
+
+    const Extent e = extent<ALIGNED>(a, b);
+    if (e.np == 0) {  // nothing to attend to (ctx_len <= 0 or q_pos < 0): zeros
+        if (wgp == 0)
+            for (int i = threadIdx.x; i < g_local * D; i += 256)
                 a.out[((long long)b * a.n_heads + head0) * D + i] = 0.f;
         return;
     }
-    const int part_begin = p * a.part_tokens;
-    if (part_begin >= e.L) return;  // wave-uniform
-    const int part_end = min(e.L, part_begin + a.part_tokens);
-    const int nparts = (e.L + a.part_tokens - 1) / a.part_tokens;
+    if (wgp >= e.np) return;  // uniform over the workgroup
+
+    // Q operand (B of the QK product): head j, dims by qk_dim.
+    float qv[NC];
+    {
+        const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
+        const bool ok = j < g_local;
+#pragma unroll
+        for (int c = 0; c < NC; c++) qv[c] = ok ? qrow[qk_dim<D, KVT>(c, kq)] : 0.f;
+    }
+
+    State<D> st;
+#pragma unroll
+    for (int x = 0; x < DPL; x++) st.acc[x] = floatx4{0.f, 0.f, 0.f, 0.f};
+    st.m = -INFINITY;
+    st.l = 0.f;
 
     RowMap m;
     m.table = a.tables ? a.tables + (long long)b * a.table_stride : nullptr;
@@ -225,161 +516,153 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     m.num_blocks = a.num_blocks;
     m.table_len = a.table_stride;
 
-    // Q operand (B of the QK product): head j, dims by qk_dim.  Heads past the
-    // group are zero, so their S columns are 0 and never stored.
-    float qv[NC];
-    {
-        const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
-        const bool ok = j < g_local;
-#pragma unroll
-        for (int c = 0; c < NC; c++) qv[c] = ok ? qrow[qk_dim<D, KVT>(c, kq)] : 0.f;
+    const int per_part = 4 * a.tpw;
+    if (ALIGNED && wgp < e.np_main) {
+        const int first = wgp * per_part + wave * a.tpw;
+        const int n = max(0, min(first + a.tpw, e.main_tiles) - first);
+        AlignedWalk w;
+        w.base = e.lo & ~15;
+        w.lo = e.lo;
+        w.hi = e.hi;
+        w.head_off = (long long)kvh * a.head_stride;
+        w.bi_first = (w.base + 16 * first) >> a.bt_log2;
+        w.tblv = 0;
+        if (a.tables && n > 0) {
+            const int bi = w.bi_first + lane;
+            const int bi_last = (w.base + 16 * (first + n) - 1) >> a.bt_log2;
+            int blk = -1;
+            if (bi <= bi_last && bi < a.table_stride) {
+                blk = m.table[bi];
+                if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
+            }
+            w.tblv = blk;
+        }
+        walk_tiles<D, KVT>(st, a, qv, n, j, kq, [&](int i, long long& ko, long long* vo) {
+            return aligned_offsets<D, KVT>(a, w, first + i, j, kq, ko, vo);
+        });
+    } else {
+        // gather: the explicit/virtual position list, or the aligned path's globals
+        const bool globals = ALIGNED;
+        const int vend = globals ? e.n_glob : e.L;
+        const int first = globals ? wave : wgp * per_part + wave * a.tpw;
+        const int step = globals ? 4 : 1;
+        const int ntiles = (vend + 15) / 16;
+        const int n = globals ? max(0, (ntiles - first + 3) / 4)
+                              : max(0, min(first + a.tpw, ntiles) - first);
+        walk_tiles<D, KVT>(st, a, qv, n, j, kq, [&](int i, long long& ko, long long* vo) {
+            return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (first + i * step), vend, globals,
+                                          j, kq, ko, vo);
+        });
     }
 
-    floatx4 acc[DPL];
-#pragma unroll
-    for (int t = 0; t < DPL; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float mrun = -INFINITY;  // running max (log2 domain), uniform over kq
-    float lrun = 0.f;        // this lane's share of the denominator
-
-    for (int t0 = part_begin; t0 < part_end; t0 += 16) {
-        // K row of this lane: virtual token t0 + j.
-        float kv[NC];
-        {
-            const int v = t0 + j;
-            long long off = -1;
-            if (v < part_end) {
-                const int pos = virt_to_pos(a, e, b, v);
-                if (pos >= 0) off = row_offset(m, pos, kvh);
-            }
-            load_k<D, KVT>(a.k, off, kq, kv);
-        }
-        // V rows of this lane: virtual tokens t0 + 4*kq + r.
-        float vv[4][DPL];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int v = t0 + 4 * kq + r;
-            long long off = -1;
-            if (v < part_end) {
-                const int pos = virt_to_pos(a, e, b, v);
-                if (pos >= 0) off = row_offset(m, pos, kvh);
-            }
-            load_v<D, KVT>(a.v, off, j, vv[r]);
-        }
-
-        // S = K . Q^T   (lane: head j, tokens 4*kq + r in reg r)
-        floatx4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
-
-        float sv[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            sv[r] = (t0 + 4 * kq + r < part_end) ? s[r] * a.scale_log2 : -1e30f;
-        float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mnew = fmaxf(mrun, mt);
-        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - mnew);
-        lrun = __builtin_fmaf(lrun, alpha, (pr[0] + pr[1]) + (pr[2] + pr[3]));
-        mrun = mnew;
-
-        // Rescale O: reg r' of this lane holds head 4*kq + r'.
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float ar = __shfl(alpha, 4 * kq + r);
-#pragma unroll
-            for (int t = 0; t < DPL; t++) acc[t][r] *= ar;
-        }
-
-        // O += P . V  (A = P straight from the S registers)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int t = 0; t < DPL; t++)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv[r][t], acc[t], 0, 0, 0);
-    }
-
-    // Denominator per head column: sum the four token quads.
-    float lt = lrun + __shfl_xor(lrun, 16);
+    // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
+    float lt = st.l + __shfl_xor(st.l, 16);
     lt += __shfl_xor(lt, 32);
-
+    if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int hh = 4 * kq + r;  // head (within the 16-group) of acc[.][r]
-        const float lh = __shfl(lt, hh);
-        const float mh = __shfl(mrun, hh);
-        if (hh < g_local) {
+        for (int x = 0; x < DPL; x++) sm_acc[wave - 1][x][lane] = st.acc[x];
+    }
+    if (kq == 0) {
+        sm_m[wave][j] = st.m;
+        sm_l[wave][j] = lt;
+    }
+    __syncthreads();
+    const int slot_base = ((b * a.n_kv_heads + kvh) * a.n_hg + hg);
+    if (wave == 0) {
+        float mh[4], lh[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int hh = 4 * kq + r;
+            float M = fmaxf(fmaxf(sm_m[0][hh], sm_m[1][hh]), fmaxf(sm_m[2][hh], sm_m[3][hh]));
+            float sw[4], L = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float mw = sm_m[w][hh];
+                sw[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+                L = __builtin_fmaf(sm_l[w][hh], sw[w], L);
+            }
+#pragma unroll
+            for (int x = 0; x < DPL; x++) {
+                float v = st.acc[x][r] * sw[0];
+#pragma unroll
+                for (int w = 1; w < 4; w++) v = __builtin_fmaf(sm_acc[w - 1][x][lane][r], sw[w], v);
+                st.acc[x][r] = v;
+            }
+            mh[r] = M;
+            lh[r] = L;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int hh = 4 * kq + r;
+            if (hh >= g_local) continue;
             const long long head = head0 + hh;
-            if (nparts == 1) {
-                const float inv = 1.0f / lh;
+            if (e.np == 1) {
+                const float inv = 1.0f / lh[r];
                 float* o = a.out + ((long long)b * a.n_heads + head) * D + DPL * j;
 #pragma unroll
                 for (int x = 0; x < DPL / 4; x++)
-                    *(float4*)(o + 4 * x) = float4{acc[4 * x + 0][r] * inv, acc[4 * x + 1][r] * inv,
-                                                   acc[4 * x + 2][r] * inv, acc[4 * x + 3][r] * inv};
+                    *(float4*)(o + 4 * x) = float4{st.acc[4 * x + 0][r] * inv, st.acc[4 * x + 1][r] * inv,
+                                                   st.acc[4 * x + 2][r] * inv, st.acc[4 * x + 3][r] * inv};
             } else {
-                const long long slot = ((long long)b * a.n_heads + head) * a.max_parts + p;
+                // device-coherent (write-through) stores: the merging workgroup
+                // may run on another XCD, whose L2 does not see this one's
+                const long long slot = ((long long)b * a.n_heads + head) * a.max_parts + wgp;
                 float* o = a.ws_acc + slot * D + DPL * j;
 #pragma unroll
-                for (int x = 0; x < DPL / 4; x++)
-                    *(float4*)(o + 4 * x) =
-                        float4{acc[4 * x + 0][r], acc[4 * x + 1][r], acc[4 * x + 2][r], acc[4 * x + 3][r]};
-                if (j == 0) a.ws_ml[slot] = float2{mh, lh};
+                for (int x = 0; x < DPL; x++)
+                    __hip_atomic_store(o + x, st.acc[x][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (j == 0) {
+                    float* ml = (float*)(a.ws_ml + slot);
+                    __hip_atomic_store(ml, mh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(ml + 1, lh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
+        if (e.np > 1) {
+            // publish: the write-through stores complete before the arrival is
+            // counted; the last workgroup to arrive merges
+            __builtin_amdgcn_s_waitcnt(0);
+            int old = 0;
+            if (lane == 0)
+                old = __hip_atomic_fetch_add(a.counters + slot_base, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            old = __shfl(old, 0);
+            if (lane == 0) sm_last = (old == e.np - 1);
+        }
     }
+    if (e.np == 1) return;
+    __syncthreads();
+    if (!sm_last) return;
+    for (int hh = wave; hh < g_local; hh += 4) {
+        const long long head = head0 + hh;
+        merge_head<D>(a, ((long long)b * a.n_heads + head) * a.max_parts, e.np,
+                      a.out + ((long long)b * a.n_heads + head) * D, lane);
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.counters + slot_base, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of the split-K partials of one (sequence, q head).
-// 64 threads, thread = dims tid, tid+64.
-template <int D>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
-    const int head = blockIdx.x;
-    const int b = blockIdx.y;
-    const int tid = threadIdx.x;
-    const SeqExtent e = seq_extent(a, b);
-    float* o = a.out + ((long long)b * a.n_heads + head) * D;
-    if (e.L <= 0) return;  // zeros written by decode_kernel
-    const int nparts = (e.L + a.part_tokens - 1) / a.part_tokens;
-    if (nparts <= 1) return;  // written by decode_kernel
-    const long long base = ((long long)b * a.n_heads + head) * a.max_parts;
-    float mx = -INFINITY;
-    for (int p = 0; p < nparts; p++) mx = fmaxf(mx, a.ws_ml[base + p].x);
-    float lsum = 0.f;
-    float accd[D / 64];
-#pragma unroll
-    for (int x = 0; x < D / 64; x++) accd[x] = 0.f;
-    for (int p = 0; p < nparts; p++) {
-        const float2 ml = a.ws_ml[base + p];
-        const float w = __builtin_amdgcn_exp2f(ml.x - mx);
-        lsum = __builtin_fmaf(ml.y, w, lsum);
-        const float* src = a.ws_acc + (base + p) * D;
-#pragma unroll
-        for (int x = 0; x < D / 64; x++) accd[x] = __builtin_fmaf(w, src[tid + 64 * x], accd[x]);
-    }
-    const float inv = 1.0f / lsum;
-#pragma unroll
-    for (int x = 0; x < D / 64; x++) o[tid + 64 * x] = accd[x] * inv;
+__global__ void fill_zero_kernel(int* p, long long n) {
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x)
+        p[i] = 0;
 }
 
 // ---------------------------------------------------------------- host side
 
-static int g_part_override = 0;
+static int g_tpw_override = 0;
 
-static int pick_partition(int batch, int units_per_seq, int max_len) {
-    if (g_part_override > 0) return g_part_override;
-    // Enough wavefronts to keep 256 CUs busy through the tail (about 32 per
-    // CU over the whole grid), but partitions as long as possible so the
-    // partial write-back stays small next to the K/V bytes streamed.
-    const long long token_units = (long long)batch * units_per_seq * (long long)max_len;
-    const long long target = 8192;
-    long long want = token_units / target;
-    int p = 32;
-    while (p < want && p < 4096) p <<= 1;
-    return p;
+// Tiles per wavefront per partition.  Enough workgroups to fill 256 CUs
+// about four deep, each wavefront streaming as many 16-token tiles as that
+// allows (at most 64, one block-table slice per lane), so the partial
+// write-back and merge stay small next to the K/V bytes.
+static int pick_tpw(int batch, int units, int max_len) {
+    if (g_tpw_override > 0) return g_tpw_override;
+    const long long tiles = (long long)batch * units * ((max_len + 15) / 16);
+    const long long target_wg = 1024;
+    int t = 1;
+    while (t < 64 && 4LL * t * target_wg < tiles) t <<= 1;
+    return t;
 }
 
 struct DecodePlan {
@@ -388,16 +671,26 @@ struct DecodePlan {
     size_t ws_bytes;
     int head_dim;
     int kvt;
+    bool aligned;
+    int batch;
 };
 
-static size_t ws_bytes_for(int batch, int n_heads, int head_dim, int max_parts) {
+static size_t ws_layout(int batch, int n_heads, int n_kv_heads, int n_hg, int head_dim,
+                        int max_parts, size_t* ml_off, size_t* ctr_off) {
     if (max_parts <= 1) return 0;
     const size_t slots = (size_t)batch * n_heads * max_parts;
-    return slots * head_dim * sizeof(float) + slots * sizeof(float2) + 256;
+    size_t acc = (slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
+    size_t ml = (slots * sizeof(float2) + 255) & ~(size_t)255;
+    size_t ctr = ((size_t)batch * n_kv_heads * n_hg * sizeof(int) + 255) & ~(size_t)255;
+    if (ml_off) *ml_off = acc;
+    if (ctr_off) *ctr_off = acc + ml;
+    return acc + ml + ctr;
 }
 
+// max_main: host bound on the contiguous main range; globals: whether an
+// extra partition of strided globals may exist.
 static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, int head_dim,
-                       int kvt, int max_len, float scale) {
+                       int kvt, int max_main, bool globals, bool aligned_path, float scale) {
     if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0)
         return set_error(NYION_ERR_INVALID, "decode: batch/heads must be positive");
     if (n_heads % n_kv_heads)
@@ -407,7 +700,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
         return set_error(NYION_ERR_UNSUPPORTED, "decode: head_dim %d (supported: 64, 128)", head_dim);
     if (kvt != NYION_KV_F32 && kvt != NYION_KV_Q4_20B)
         return set_error(NYION_ERR_INVALID, "decode: kv_dtype %d", kvt);
-    if (max_len <= 0) return set_error(NYION_ERR_INVALID, "decode: max_ctx must be positive");
+    if (max_main <= 0) return set_error(NYION_ERR_INVALID, "decode: max_ctx must be positive");
     if (batch > 65535) return set_error(NYION_ERR_UNSUPPORTED, "decode: batch %d > 65535", batch);
     DecodeArgs& a = pl.a;
     a = DecodeArgs{};
@@ -415,48 +708,57 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     a.n_kv_heads = n_kv_heads;
     a.group = n_heads / n_kv_heads;
     a.n_hg = (a.group + 15) / 16;
+    if (n_kv_heads * a.n_hg > 65535) return set_error(NYION_ERR_UNSUPPORTED, "decode: too many heads");
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
-    a.part_tokens = pick_partition(batch, n_kv_heads * a.n_hg, max_len);
-    a.max_parts = (max_len + a.part_tokens - 1) / a.part_tokens;
-    a.max_len = max_len;
+    // the gather path walks the globals too, so its bound includes them
+    const int max_len = aligned_path ? max_main : max_main + (globals ? 128 : 0);
+    a.max_len = max_main;
+    a.tpw = pick_tpw(batch, n_kv_heads * a.n_hg, max_len);
+    const int per_part = 4 * a.tpw;
+    const int tiles = (max_len + 15) / 16 + (aligned_path ? 1 : 0);
+    a.max_parts = (tiles + per_part - 1) / per_part + (aligned_path && globals ? 1 : 0);
     pl.head_dim = head_dim;
     pl.kvt = kvt;
-    pl.grid = dim3((a.max_parts + 3) / 4, n_kv_heads * a.n_hg, batch);
-    pl.ws_bytes = ws_bytes_for(batch, n_heads, head_dim, a.max_parts);
+    pl.aligned = aligned_path;
+    pl.batch = batch;
+    pl.grid = dim3(a.max_parts, n_kv_heads * a.n_hg, batch);
+    pl.ws_bytes = ws_layout(batch, n_heads, n_kv_heads, a.n_hg, head_dim, a.max_parts, nullptr, nullptr);
     return NYION_OK;
 }
 
-static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes, int batch) {
+static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes) {
     if (pl.ws_bytes == 0) return NYION_OK;
     if (!ws || ws_bytes < pl.ws_bytes)
         return set_error(NYION_ERR_WORKSPACE, "decode: workspace %zu bytes < required %zu", ws_bytes,
                          pl.ws_bytes);
-    if (!aligned(ws, 16)) return set_error(NYION_ERR_INVALID, "decode: workspace not 16-byte aligned");
-    const size_t slots = (size_t)batch * pl.a.n_heads * pl.a.max_parts;
+    if (!aligned(ws, 256)) return set_error(NYION_ERR_INVALID, "decode: workspace not 256-byte aligned");
+    size_t ml_off = 0, ctr_off = 0;
+    ws_layout(pl.batch, pl.a.n_heads, pl.a.n_kv_heads, pl.a.n_hg, pl.head_dim, pl.a.max_parts, &ml_off,
+              &ctr_off);
     pl.a.ws_acc = (float*)ws;
-    size_t acc_bytes = (slots * pl.head_dim * sizeof(float) + 255) & ~(size_t)255;
-    pl.a.ws_ml = (float2*)((char*)ws + acc_bytes);
+    pl.a.ws_ml = (float2*)((char*)ws + ml_off);
+    pl.a.counters = (int*)((char*)ws + ctr_off);
     return NYION_OK;
 }
 
-static int launch_plan(const DecodePlan& pl, int batch, hipStream_t stream) {
-    const int D = pl.head_dim;
-#define NYION_DECODE_LAUNCH(DD, KK)                                                        \
-    hipLaunchKernelGGL((decode_kernel<DD, KK>), pl.grid, dim3(256), 0, stream, pl.a);      \
-    if (pl.a.max_parts > 1)                                                                \
-        hipLaunchKernelGGL((decode_merge_kernel<DD>), dim3(pl.a.n_heads, batch), dim3(64), 0, \
-                           stream, pl.a);
-    if (D == 64 && pl.kvt == NYION_KV_F32) {
-        NYION_DECODE_LAUNCH(64, NYION_KV_F32)
-    } else if (D == 64) {
-        NYION_DECODE_LAUNCH(64, NYION_KV_Q4_20B)
-    } else if (pl.kvt == NYION_KV_F32) {
-        NYION_DECODE_LAUNCH(128, NYION_KV_F32)
-    } else {
-        NYION_DECODE_LAUNCH(128, NYION_KV_Q4_20B)
-    }
-#undef NYION_DECODE_LAUNCH
+template <int D, int KVT>
+static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
+    if (pl.aligned)
+        hipLaunchKernelGGL((decode_kernel<D, KVT, true>), pl.grid, dim3(256), 0, stream, pl.a);
+    else
+        hipLaunchKernelGGL((decode_kernel<D, KVT, false>), pl.grid, dim3(256), 0, stream, pl.a);
+}
+
+static int launch_plan(const DecodePlan& pl, hipStream_t stream) {
+    if (pl.head_dim == 64 && pl.kvt == NYION_KV_F32)
+        launch_dk<64, NYION_KV_F32>(pl, stream);
+    else if (pl.head_dim == 64)
+        launch_dk<64, NYION_KV_Q4_20B>(pl, stream);
+    else if (pl.kvt == NYION_KV_F32)
+        launch_dk<128, NYION_KV_F32>(pl, stream);
+    else
+        launch_dk<128, NYION_KV_Q4_20B>(pl, stream);
     return check_launch("decode");
 }
 
@@ -472,6 +774,11 @@ static int check_pool_ptrs(const void* k, const void* v, int kvt) {
     return NYION_OK;
 }
 
+static int window_main_len(int max_ctx, int window) {
+    if (window <= 0) return max_ctx;
+    return (int)((long long)window + 1 < max_ctx ? (long long)window + 1 : max_ctx);
+}
+
 }  // namespace nyion
 
 using namespace nyion;
@@ -479,32 +786,47 @@ using namespace nyion;
 extern "C" {
 
 int nyion_set_decode_partition_tokens(int tokens) {
-    if (tokens != 0 && (tokens < 16 || tokens > 4096 || !is_pow2(tokens)))
-        return set_error(NYION_ERR_INVALID, "partition tokens %d: power of two in [16, 4096] or 0",
-                         tokens);
-    g_part_override = tokens;
+    if (tokens != 0 && (tokens < 64 || tokens > 4096 || !is_pow2(tokens)))
+        return set_error(NYION_ERR_INVALID,
+                         "partition tokens %d: power of two in [64, 4096] (4 wavefronts x 16-token "
+                         "tiles) or 0", tokens);
+    g_tpw_override = tokens / 64;
     return NYION_OK;
 }
 
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len) {
     (void)head_dim;
-    return pick_partition(batch, n_kv_heads, max_len);
-}
-
-static int window_max_len(int max_ctx, int window, int global_stride) {
-    if (window <= 0) return max_ctx;
-    long long L = (long long)window + 1 + (global_stride > 0 ? 128 : 0);
-    if (L > (long long)max_ctx + 128) L = (long long)max_ctx + 128;
-    return (int)L;
+    return 64 * pick_tpw(batch, n_kv_heads, max_len);
 }
 
 size_t nyion_paged_decode_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
                                          int max_ctx, int window, int global_stride) {
     DecodePlan pl;
     if (plan_common(pl, batch, n_heads, n_kv_heads, head_dim, NYION_KV_F32,
-                    window_max_len(max_ctx, window, global_stride), 0.f) != NYION_OK)
+                    window_main_len(max_ctx, window), window > 0 && global_stride > 0, true,
+                    0.f) != NYION_OK)
         return 0;
-    return pl.ws_bytes;
+    // the gather path (block_tokens < 16) may need more partitions
+    DecodePlan pg;
+    if (plan_common(pg, batch, n_heads, n_kv_heads, head_dim, NYION_KV_F32,
+                    window_main_len(max_ctx, window), window > 0 && global_stride > 0, false,
+                    0.f) != NYION_OK)
+        return 0;
+    return pl.ws_bytes > pg.ws_bytes ? pl.ws_bytes : pg.ws_bytes;
+}
+
+int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!d_workspace || workspace_bytes == 0) return NYION_OK;
+    if (!aligned(d_workspace, 4)) return set_error(NYION_ERR_INVALID, "workspace init: alignment");
+    const long long n = (long long)(workspace_bytes / sizeof(int));
+    long long g = (n + 255) / 256;
+    if (g > 4096) g = 4096;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)g), dim3(256), 0, (hipStream_t)stream,
+                       (int*)d_workspace, n);
+    return check_launch("workspace init");
 }
 
 int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
@@ -527,14 +849,17 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
                          block_tokens);
     if (num_blocks <= 0 || max_blocks_per_seq <= 0)
         return set_error(NYION_ERR_INVALID, "paged decode: num_blocks/max_blocks_per_seq");
-    if ((long long)max_ctx > (long long)max_blocks_per_seq * block_tokens)
+    if (max_ctx <= 0 || (long long)max_ctx > (long long)max_blocks_per_seq * block_tokens)
         return set_error(NYION_ERR_INVALID,
-                         "paged decode: max_ctx %d exceeds max_blocks_per_seq*block_tokens", max_ctx);
+                         "paged decode: max_ctx %d must be in [1, max_blocks_per_seq*block_tokens]",
+                         max_ctx);
+    const bool aligned_path = block_tokens >= 16;
     DecodePlan pl;
     if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype,
-                          window_max_len(max_ctx, window, global_stride), scale)) != NYION_OK)
+                          window_main_len(max_ctx, window), window > 0 && global_stride > 0,
+                          aligned_path, scale)) != NYION_OK)
         return rc;
-    if ((rc = attach_workspace(pl, d_workspace, workspace_bytes, batch)) != NYION_OK) return rc;
+    if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
     DecodeArgs& a = pl.a;
     const long long row = row_elems(head_dim, kv_dtype);
     a.q = d_q;
@@ -553,14 +878,14 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
     a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
     a.window = window;
     a.global_stride = global_stride;
-    return launch_plan(pl, batch, (hipStream_t)stream);
+    return launch_plan(pl, (hipStream_t)stream);
 }
 
 size_t nyion_paged_decode_positions_workspace_size(int batch, int n_heads, int n_kv_heads,
                                                    int head_dim, int max_positions) {
     DecodePlan pl;
-    if (plan_common(pl, batch, n_heads, n_kv_heads, head_dim, NYION_KV_F32, max_positions, 0.f) !=
-        NYION_OK)
+    if (plan_common(pl, batch, n_heads, n_kv_heads, head_dim, NYION_KV_F32, max_positions, false,
+                    false, 0.f) != NYION_OK)
         return 0;
     return pl.ws_bytes;
 }
@@ -585,10 +910,10 @@ int nyion_paged_decode_attention_positions(
     if (num_blocks <= 0 || max_blocks_per_seq <= 0 || max_positions <= 0)
         return set_error(NYION_ERR_INVALID, "positions decode: sizes must be positive");
     DecodePlan pl;
-    if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype, max_positions,
-                          scale)) != NYION_OK)
+    if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype, max_positions, false,
+                          false, scale)) != NYION_OK)
         return rc;
-    if ((rc = attach_workspace(pl, d_workspace, workspace_bytes, batch)) != NYION_OK) return rc;
+    if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
     DecodeArgs& a = pl.a;
     const long long row = row_elems(head_dim, kv_dtype);
     a.q = d_q;
@@ -606,7 +931,7 @@ int nyion_paged_decode_attention_positions(
     a.bt_log2 = ilog2(block_tokens);
     a.num_blocks = num_blocks;
     a.mode = MODE_LIST;
-    return launch_plan(pl, batch, (hipStream_t)stream);
+    return launch_plan(pl, (hipStream_t)stream);
 }
 
 int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, float* d_scores,
@@ -627,23 +952,25 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
         return set_error(NYION_ERR_INVALID, "attention node: head counts");
     DecodePlan pl;
     if ((rc = plan_common(pl, 1, (int)n_heads, (int)n_kv_heads, (int)head_dim, kv_dtype,
-                          (int)seq_len, 0.f)) != NYION_OK)
+                          (int)seq_len, false, true, 0.f)) != NYION_OK)
         return rc;
-    // The node's scores buffer (n_heads*kv_stride floats) is the split-K
-    // workspace; without it run one partition per head group.
+    // The node's scores buffer (n_heads*kv_stride floats, the reference's
+    // ScratchBuffers::d_scores) holds the split-K partials; without it, or
+    // when it is too small, use longer partitions until one workgroup covers
+    // the sequence.
     DecodeArgs& a = pl.a;
-    const size_t scores_bytes = d_scores ? (size_t)n_heads * kv_stride * sizeof(float) : 0;
-    if (pl.ws_bytes > scores_bytes) {
-        int p = a.part_tokens;
-        while (p < (1 << 30) && ws_bytes_for(1, (int)n_heads, (int)head_dim,
-                                             (int)((seq_len + p - 1) / p)) > scores_bytes)
-            p <<= 1;
-        a.part_tokens = p;
-        a.max_parts = (int)((seq_len + p - 1) / p);
-        pl.grid = dim3((a.max_parts + 3) / 4, a.n_kv_heads * a.n_hg, 1);
-        pl.ws_bytes = ws_bytes_for(1, (int)n_heads, (int)head_dim, a.max_parts);
+    const size_t scores_bytes =
+        d_scores && aligned(d_scores, 256) ? (size_t)n_heads * kv_stride * sizeof(float) : 0;
+    while (pl.ws_bytes > scores_bytes) {
+        a.tpw *= 2;
+        const int per_part = 4 * a.tpw;
+        const int tiles = ((int)seq_len + 15) / 16 + 1;
+        a.max_parts = (tiles + per_part - 1) / per_part;
+        pl.grid = dim3(a.max_parts, a.n_kv_heads * a.n_hg, 1);
+        pl.ws_bytes = ws_layout(1, a.n_heads, a.n_kv_heads, a.n_hg, (int)head_dim, a.max_parts,
+                                nullptr, nullptr);
     }
-    if ((rc = attach_workspace(pl, d_scores, scores_bytes, 1)) != NYION_OK) return rc;
+    if ((rc = attach_workspace(pl, d_scores, scores_bytes)) != NYION_OK) return rc;
     const long long row = row_elems((int)head_dim, kv_dtype);
     a.q = d_q;
     a.k = d_k;
@@ -657,7 +984,12 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
     a.bt_log2 = 30;
     a.num_blocks = 1;
     a.mode = MODE_FULL;
-    return launch_plan(pl, 1, (hipStream_t)stream);
+    if (pl.ws_bytes) {  // the scores buffer is caller scratch: clear the counters each call
+        const long long n = (long long)a.n_kv_heads * a.n_hg;
+        hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, a.counters, n);
+        if ((rc = check_launch("attention node counters")) != NYION_OK) return rc;
+    }
+    return launch_plan(pl, (hipStream_t)stream);
 }
 
 int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float* d_v_cache,

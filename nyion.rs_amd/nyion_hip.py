@@ -59,6 +59,7 @@ SIGNATURES = {
     "nyion_paged_decode_attention_positions": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
                                                      i32, i32, i32, i32, i32, f32, vp, vp, sz,
                                                      vp]),
+    "nyion_decode_workspace_init": (i32, [vp, sz, vp]),
     "nyion_set_decode_partition_tokens": (i32, [i32]),
     "nyion_get_decode_partition_tokens": (i32, [i32, i32, i32, i32]),
     "nyion_prefill_attention_bf16": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp, vp,
@@ -155,10 +156,12 @@ def decode_workspace_size(batch, n_heads, n_kv_heads, head_dim, max_ctx, window=
 
 
 def alloc_workspace(nbytes: int, device="cuda"):
+    """Decode workspace: zero-filled (the split-K arrival counters start at 0
+    and every call leaves them at 0)."""
     torch = _torch()
     if nbytes <= 0:
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
 
 def paged_decode(q, k_pool, v_pool, block_tables, ctx_lens, out, n_heads, n_kv_heads, head_dim,

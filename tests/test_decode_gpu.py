@@ -104,7 +104,7 @@ def test_paged_variable_batch_and_partitions(gpu):
     pb = W.paged_batch(lens, seed=3, spare_blocks=7)
     ref = W.reference_decode(pb, threads=8)
     try:
-        for p in (16, 32, 128, 1024, 0):
+        for p in (64, 128, 1024, 4096, 0):
             gpu.set_partition_tokens(p)
             assert_close(run_paged(gpu, pb), ref, f"partition {p}")
     finally:
