@@ -16,7 +16,7 @@ The other BASELINE configs are measured in the same run and reported under
 batch), C4 (4-bit KV, 131072 context, window 4096) and C5 (causal prefill,
 TFLOP/s against the bf16 MFMA peak).
 
-roofline: the decode call (decode kernel + split-K merge kernel) timed with
+roofline: the decode call (one decode kernel launch, split-K merge fused) timed with
 HIP events on the stream it is launched on, against 8 TB/s.
 cpu_baseline: the C restatement of ops::attention (oracle/, the reference's
 AVX-512 dot/axpy order, OpenMP over heads) on the host cores, one C2 layer at
@@ -401,7 +401,7 @@ def main():
             "unit": "GB/s",
             "frac": round(c2["achieved_call_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "decode_kernel<64,f32> + decode_merge_kernel<64> (one decode call)",
+            "kernel": "decode_kernel<64,f32,aligned> (one launch per decode call)",
             "bytes_per_launch": c2["bytes_per_layer"],
             "launch_us": round(c2["call_us_event_mean"], 3),
         }

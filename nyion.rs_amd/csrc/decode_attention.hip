@@ -5,10 +5,14 @@
 // (swamp-engine/src/ops.rs:170-278) and ops::attention_sparse (ops.rs:85-168);
 // the header states the position sets.
 //
-// Work decomposition.  A 256-thread workgroup owns one (sequence, kv head,
-// group of up to 16 q heads, split-K partition); its four wavefronts take
-// consecutive runs of 16-token tiles of that partition.  All q heads of a GQA
-// group are processed together, so each K/V byte is read from HBM once.
+// Work decomposition (stream-K).  A segment is one (sequence, kv head, group
+// of up to 16 q heads); its attended positions form a list of 16-token tiles.
+// The segments' tile lists are laid end to end and a grid sized to the
+// resident capacity of the chip cuts that list into equal ranges, one per
+// 256-thread workgroup, whatever the spread of context lengths.  A workgroup
+// walks its range segment by segment; its four wavefronts split each piece.
+// All q heads of a GQA group are processed together, so each K/V byte is read
+// from HBM once.
 //
 // Per 16-token tile a wavefront runs two MFMA chains on
 // v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate):
@@ -30,12 +34,14 @@
 // Softmax.  Online, in the log2 domain, on the S registers: tile max over the
 // 4 registers and the 4 token quads (lane xor 16, 32), rescale, exp2.
 //
-// Split-K.  The four wavefronts of a workgroup merge through LDS.  When a
-// sequence needs several workgroups, each writes one (m, l, O) partial to the
-// workspace with device-coherent (write-through) stores, waits for them, and
-// counts its arrival with an agent-scope atomic; the last workgroup to arrive
-// reads the partials with device-coherent loads, merges them with
-// log-sum-exp, writes the output and resets its counter to 0.  No L2
+// Split-K.  The four wavefronts of a workgroup merge through LDS.  A segment
+// covered by one workgroup is written out directly.  Otherwise each workgroup
+// holding a piece of it writes one (m, l, O) partial to the workspace with
+// device-coherent (write-through) stores, waits for them, and counts its
+// arrival with an agent-scope atomic; the last one to arrive reads the
+// partials with device-coherent loads, merges them with log-sum-exp, writes
+// the output and resets the counter to 0.  Pieces of a segment are held by
+// consecutive workgroups g, so partial slot g + segment is unique.  No L2
 // write-back or invalidate is issued, and one decode call is one launch.
 #include <float.h>
 #include <math.h>
@@ -58,14 +64,15 @@ struct DecodeArgs {
     const int32_t* positions;  // MODE_LIST: [B][pos_stride]
     const int32_t* n_pos;      // MODE_LIST: [B]
     float* out;                // [B][Hq][D]
-    float* ws_acc;             // [(b*Hq + head)*max_parts + p][D]
-    float2* ws_ml;             // [(b*Hq + head)*max_parts + p] = (m log2, l)
-    int* counters;             // [B][Hkv][n_hg], zero between calls
+    float* ws_acc;             // partial slot p: [p][16 heads][D]
+    float2* ws_ml;             // [p][16 heads] = (m log2, l)
+    int* counters;             // [segment], zero between calls
     long long block_stride;
     long long head_stride;
     int table_stride;
     int pos_stride;
     int uniform_len;
+    int batch;  // sequences of this launch (<= kMaxLaunchBatch)
     int n_heads;
     int n_kv_heads;
     int group;  // q heads per kv head
@@ -76,35 +83,31 @@ struct DecodeArgs {
     int window;
     int global_stride;
     int mode;
-    int tpw;        // tiles per wavefront per partition
-    int max_parts;  // workgroup partitions per (sequence, kv head, head group): grid.x
     int max_len;    // host bound on attended positions per sequence
     float scale_log2;  // scale * log2(e)
 };
 
+// Sequences per launch: the per-sequence tile prefix sums live in LDS.
+constexpr int kMaxLaunchBatch = 2048;
+
 // Attended positions of one sequence.
 //  aligned path (FULL/WINDOW, blocks >= 16 tokens): the contiguous range
-//    [lo, hi] walked in 16-aligned tiles from lo & ~15, plus n_glob strided
-//    globals (stride*g) in one extra partition;
+//    [lo, hi] walked in 16-aligned tiles from lo & ~15 (main tiles), then
+//    n_glob strided globals (stride*g) gathered 16 per tile;
 //  gather path: L virtual positions (the same sets, or an explicit list).
 struct Extent {
     int lo, hi, n_glob, L;
     int main_tiles;  // aligned: tiles over [lo & ~15, hi]
-    int np_main;     // partitions over the main tiles (aligned) or all tiles (gather)
-    int np;          // total partitions
+    int tiles;       // all tiles of one segment of this sequence
 };
 
+// len / qp / npos: the sequence's ctx_len, q_pos and list length as loaded.
 template <bool ALIGNED>
-__device__ __forceinline__ Extent extent(const DecodeArgs& a, int b) {
-    Extent e{0, -1, 0, 0, 0, 0, 0};
-    const int per_part = 4 * a.tpw;  // tiles per workgroup partition
-    // per-sequence values are wave-uniform: keep them (and everything derived
-    // from them) in scalar registers so tile loops branch uniformly
+__device__ __forceinline__ Extent seq_extent(const DecodeArgs& a, int len, int qp, int npos) {
+    Extent e{0, -1, 0, 0, 0, 0};
     if (a.mode == MODE_LIST) {
-        e.L = min(max(__builtin_amdgcn_readfirstlane(a.n_pos[b]), 0), a.max_len);
+        e.L = min(max(npos, 0), a.max_len);
     } else {
-        const int len = a.ctx_lens ? __builtin_amdgcn_readfirstlane(a.ctx_lens[b]) : a.uniform_len;
-        const int qp = a.q_pos ? __builtin_amdgcn_readfirstlane(a.q_pos[b]) : len - 1;
         if (len <= 0 || qp < 0) return e;
         const int ve = min(qp, len - 1);  // ops.rs:183
         int lo = 0;
@@ -119,14 +122,32 @@ __device__ __forceinline__ Extent extent(const DecodeArgs& a, int b) {
     if (ALIGNED) {
         if (e.hi < e.lo) return e;
         e.main_tiles = (e.hi - (e.lo & ~15)) / 16 + 1;
-        e.np_main = (e.main_tiles + per_part - 1) / per_part;
-        e.np = min(e.np_main + (e.n_glob > 0 ? 1 : 0), a.max_parts);
+        e.tiles = e.main_tiles + (e.n_glob + 15) / 16;
     } else {
-        const int tiles = (e.L + 15) / 16;
-        e.np_main = (tiles + per_part - 1) / per_part;
-        e.np = min(e.np_main, a.max_parts);
+        e.tiles = (e.L + 15) / 16;
     }
     return e;
+}
+
+// Extent of sequence b as seen by one thread (no uniformity assumed).
+template <bool ALIGNED>
+__device__ __forceinline__ Extent lane_extent(const DecodeArgs& a, int b) {
+    if (a.mode == MODE_LIST) return seq_extent<ALIGNED>(a, 0, 0, a.n_pos[b]);
+    const int len = a.ctx_lens ? a.ctx_lens[b] : a.uniform_len;
+    const int qp = a.q_pos ? a.q_pos[b] : len - 1;
+    return seq_extent<ALIGNED>(a, len, qp, 0);
+}
+
+// Extent of a wave-uniform sequence b: the loaded values are moved to scalar
+// registers so that everything derived from them (tile loop bounds, masks)
+// branches uniformly.
+template <bool ALIGNED>
+__device__ __forceinline__ Extent uniform_extent(const DecodeArgs& a, int b) {
+    if (a.mode == MODE_LIST)
+        return seq_extent<ALIGNED>(a, 0, 0, __builtin_amdgcn_readfirstlane(a.n_pos[b]));
+    const int len = a.ctx_lens ? __builtin_amdgcn_readfirstlane(a.ctx_lens[b]) : a.uniform_len;
+    const int qp = a.q_pos ? __builtin_amdgcn_readfirstlane(a.q_pos[b]) : len - 1;
+    return seq_extent<ALIGNED>(a, len, qp, 0);
 }
 
 // Virtual index -> position, gather path (and the globals of the aligned path).
@@ -399,247 +420,318 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
     }
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
-
-// Log-sum-exp merge of the np partials of one (sequence, q head) by one
-// wavefront: lanes over partitions for the weights, lanes over dims for O.
-// The partials come from other workgroups, so they are read with
-// device-coherent loads, 32 partitions' worth issued before any is used.
+// Log-sum-exp merge of the np partials of one segment by the whole
+// workgroup: one thread per (head, 4-dim quad); partial p of head hh sits at
+// acc0 + (p*16 + hh)*D and ml0[p*16 + hh].  The partials come from other
+// workgroups, so they are read with device-coherent loads, 16 partials'
+// worth (their m, l and O quads) issued before any is used; chunks combine
+// online.
 template <int D>
-__device__ void merge_head(const DecodeArgs& a, long long slot0, int np, float* out, int lane) {
-    constexpr int X = D / 64;  // dims per lane
-    constexpr int CH = 32;     // partitions per batch of loads
-    const float* mlp = (const float*)(a.ws_ml + slot0);
-    float mx = -INFINITY;
-    for (int p = lane; p < np; p += 64)
-        mx = fmaxf(mx, __hip_atomic_load(mlp + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    mx = wave_max(mx);
-    float lsum = 0.f;
-    float acc[X];
-#pragma unroll
-    for (int x = 0; x < X; x++) acc[x] = 0.f;
-    for (int p0 = 0; p0 < np; p0 += 64) {
-        const int p = p0 + lane;
-        float w = 0.f;
-        if (p < np) {
-            const float m_p = __hip_atomic_load(mlp + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float l_p = __hip_atomic_load(mlp + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            w = m_p == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_p - mx);
-            lsum = __builtin_fmaf(l_p, w, lsum);
-        }
-        const int cnt = min(64, np - p0);
-        for (int q0 = 0; q0 < cnt; q0 += CH) {
-            const float* src = a.ws_acc + (slot0 + p0 + q0) * D + lane;
-            float v[CH][X];
-#pragma unroll
-            for (int q = 0; q < CH; q++)
-#pragma unroll
-                for (int x = 0; x < X; x++)
-                    v[q][x] = (q0 + q < cnt) ? __hip_atomic_load(src + (long long)q * D + 64 * x,
-                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                             : 0.f;
+__device__ void merge_segment(const float* acc0, const float2* ml0, int np, int g_local, float* out,
+                              int tid) {
+    constexpr int QPH = D / 4;  // quads per head
+    constexpr int CH = 16;      // partials per batch of loads
+    for (int item = tid; item < g_local * QPH; item += 256) {
+        const int hh = item / QPH;
+        const int dq = item - hh * QPH;
+        float M = -INFINITY, L = 0.f;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int p0 = 0; p0 < np; p0 += CH) {
+            uint64_t mlv[CH], a01[CH], a23[CH];
 #pragma unroll
             for (int q = 0; q < CH; q++) {
-                const float wq = __shfl(w, q0 + q);
-#pragma unroll
-                for (int x = 0; x < X; x++) acc[x] = __builtin_fmaf(wq, v[q][x], acc[x]);
+                if (p0 + q < np) {
+                    const long long e = (long long)(p0 + q) * 16 + hh;
+                    const uint64_t* src = (const uint64_t*)(acc0 + e * D + 4 * dq);
+                    mlv[q] = __hip_atomic_load((const uint64_t*)(ml0 + e), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    a01[q] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    a23[q] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    mlv[q] = (uint64_t)__float_as_uint(-INFINITY);  // m = -inf, l = 0
+                    a01[q] = a23[q] = 0;
+                }
             }
-        }
-    }
-    lsum = wave_sum(lsum);
-    const float inv = 1.0f / lsum;
+            float mc = -INFINITY;
 #pragma unroll
-    for (int x = 0; x < X; x++) out[lane + 64 * x] = acc[x] * inv;
+            for (int q = 0; q < CH; q++) mc = fmaxf(mc, __uint_as_float((uint32_t)mlv[q]));
+            const float mn = fmaxf(M, mc);
+            if (mn == -INFINITY) continue;  // nothing attended so far
+            const float sc = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
+            L *= sc;
+#pragma unroll
+            for (int x = 0; x < 4; x++) o[x] *= sc;
+#pragma unroll
+            for (int q = 0; q < CH; q++) {
+                const float mq = __uint_as_float((uint32_t)mlv[q]);
+                const float w = mq == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mq - mn);
+                L = __builtin_fmaf(w, __uint_as_float((uint32_t)(mlv[q] >> 32)), L);
+                o[0] = __builtin_fmaf(w, __uint_as_float((uint32_t)a01[q]), o[0]);
+                o[1] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a01[q] >> 32)), o[1]);
+                o[2] = __builtin_fmaf(w, __uint_as_float((uint32_t)a23[q]), o[2]);
+                o[3] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a23[q] >> 32)), o[3]);
+            }
+            M = mn;
+        }
+        const float inv = 1.0f / L;
+        *(float4*)(out + hh * D + 4 * dq) = float4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+    }
 }
 
 // ---------------------------------------------------------------- kernel
 
+// Main tiles [first, first + n) of one segment on the aligned path, in runs of
+// at most 64 tiles: lane l holds the block id of the run's l-th block index
+// (with blocks of >= 16 tokens a run of 64 tiles spans at most 64 blocks).
+template <int D, int KVT>
+__device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, const float* qv,
+                                          const Extent& e, const int32_t* table, long long head_off,
+                                          int first, int n, int lane, int j, int kq) {
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        const int f = first + c0;
+        const int nc = min(64, n - c0);
+        AlignedWalk w;
+        w.base = e.lo & ~15;
+        w.lo = e.lo;
+        w.hi = e.hi;
+        w.head_off = head_off;
+        w.bi_first = (w.base + 16 * f) >> a.bt_log2;
+        w.tblv = 0;
+        if (table) {
+            const int bi = w.bi_first + lane;
+            const int bi_last = (w.base + 16 * (f + nc) - 1) >> a.bt_log2;
+            int blk = -1;
+            if (bi <= bi_last && bi < a.table_stride) {
+                blk = table[bi];
+                if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
+            }
+            w.tblv = blk;
+        }
+        walk_tiles<D, KVT>(st, a, qv, nc, j, kq, [&](int i, long long& ko, long long* vo) {
+            return aligned_offsets<D, KVT>(a, w, f + i, j, kq, ko, vo);
+        });
+    }
+}
+
+__device__ __forceinline__ int sload(const int* p) { return __builtin_amdgcn_readfirstlane(*p); }
+
+// Occupancy target, which bounds the registers the compiler may use: three
+// workgroups (12 wavefronts) per CU for head_dim 64, two for packed 4-bit KV
+// at head_dim 128, and one for f32 KV at 128, whose two register-resident
+// 16-token tiles alone take 128 VGPRs per lane.
 template <int D, int KVT, bool ALIGNED>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (KVT == NYION_KV_F32 ? 1 : 2))))
+void decode_kernel(DecodeArgs a) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
     __shared__ floatx4 sm_acc[3][DPL][64];
     __shared__ float sm_m[4][16];
     __shared__ float sm_l[4][16];
+    __shared__ int sm_pref[kMaxLaunchBatch + 1];  // tiles per segment, exclusive prefix
+    __shared__ int sm_wsum[4];
     __shared__ int sm_last;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15;
     const int kq = lane >> 4;
-    const int kvh = blockIdx.y / a.n_hg;
-    const int hg = blockIdx.y - kvh * a.n_hg;
-    const int b = blockIdx.z;
-    const int wgp = blockIdx.x;
-    const int g_local = min(16, a.group - hg * 16);
-    const int head0 = kvh * a.group + hg * 16;
+    const int U = a.n_kv_heads * a.n_hg;  // segments per sequence
 
-    const Extent e = extent<ALIGNED>(a, b);
-    if (e.np == 0) {  // nothing to attend to (ctx_len <= 0 or q_pos < 0): zeros
-        if (wgp == 0)
-            for (int i = threadIdx.x; i < g_local * D; i += 256)
-                a.out[((long long)b * a.n_heads + head0) * D + i] = 0.f;
-        return;
+    // ---- tiles of one segment of each sequence, prefix-summed
+    int carry = 0;
+    if (threadIdx.x == 0) sm_pref[0] = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 256) {
+        const int b = c0 + threadIdx.x;
+        int t = b < a.batch ? lane_extent<ALIGNED>(a, b).tiles : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(t, o);
+            if (lane >= o) t += y;
+        }
+        if (lane == 63) sm_wsum[wave] = t;
+        __syncthreads();
+        int off = carry;
+        for (int w = 0; w < wave; w++) off += sm_wsum[w];
+        if (b < a.batch) sm_pref[b + 1] = off + t;
+        carry += sm_wsum[0] + sm_wsum[1] + sm_wsum[2] + sm_wsum[3];
+        __syncthreads();
     }
-    if (wgp >= e.np) return;  // uniform over the workgroup
+    // the host keeps batch * U * (tiles of the longest segment) below 2^31
+    const int T = __builtin_amdgcn_readfirstlane(carry) * U;
+    const int c = (T + (int)gridDim.x - 1) / (int)gridDim.x;  // tiles per workgroup
+    const int g0 = min((int)blockIdx.x * c, T);
+    const int g1 = min(g0 + c, T);
 
-    // Q operand (B of the QK product): head j, dims by qk_dim.
-    float qv[NC];
+    // sequences with nothing to attend to (ctx_len <= 0, q_pos < 0, empty list)
+    for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
+        if (sload(&sm_pref[b + 1]) != sload(&sm_pref[b])) continue;
+        float* o = a.out + (long long)b * a.n_heads * D;
+        for (int i = threadIdx.x; i < a.n_heads * D; i += 256) o[i] = 0.f;
+    }
+    if (g0 >= g1) return;
+
+    // first sequence of the range: the largest b with U * prefix[b] <= g0
+    int b = 0;
     {
-        const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
-        const bool ok = j < g_local;
-#pragma unroll
-        for (int c = 0; c < NC; c++) qv[c] = ok ? qrow[qk_dim<D, KVT>(c, kq)] : 0.f;
-    }
-
-    State<D> st;
-#pragma unroll
-    for (int x = 0; x < DPL; x++) st.acc[x] = floatx4{0.f, 0.f, 0.f, 0.f};
-    st.m = -INFINITY;
-    st.l = 0.f;
-
-    RowMap m;
-    m.table = a.tables ? a.tables + (long long)b * a.table_stride : nullptr;
-    m.block_stride = a.block_stride;
-    m.head_stride = a.head_stride;
-    m.token_stride = a.token_stride;
-    m.bt_log2 = a.bt_log2;
-    m.num_blocks = a.num_blocks;
-    m.table_len = a.table_stride;
-
-    const int per_part = 4 * a.tpw;
-    if (ALIGNED && wgp < e.np_main) {
-        const int first = wgp * per_part + wave * a.tpw;
-        const int n = max(0, min(first + a.tpw, e.main_tiles) - first);
-        AlignedWalk w;
-        w.base = e.lo & ~15;
-        w.lo = e.lo;
-        w.hi = e.hi;
-        w.head_off = (long long)kvh * a.head_stride;
-        w.bi_first = (w.base + 16 * first) >> a.bt_log2;
-        w.tblv = 0;
-        if (a.tables && n > 0) {
-            const int bi = w.bi_first + lane;
-            const int bi_last = (w.base + 16 * (first + n) - 1) >> a.bt_log2;
-            int blk = -1;
-            if (bi <= bi_last && bi < a.table_stride) {
-                blk = m.table[bi];
-                if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
-            }
-            w.tblv = blk;
+        int hi = a.batch - 1;
+        while (b < hi) {
+            const int mid = (b + hi + 1) >> 1;
+            if (U * sload(&sm_pref[mid]) <= g0) b = mid;
+            else hi = mid - 1;
         }
-        walk_tiles<D, KVT>(st, a, qv, n, j, kq, [&](int i, long long& ko, long long* vo) {
-            return aligned_offsets<D, KVT>(a, w, first + i, j, kq, ko, vo);
-        });
-    } else {
-        // gather: the explicit/virtual position list, or the aligned path's globals
-        const bool globals = ALIGNED;
-        const int vend = globals ? e.n_glob : e.L;
-        const int first = globals ? wave : wgp * per_part + wave * a.tpw;
-        const int step = globals ? 4 : 1;
-        const int ntiles = (vend + 15) / 16;
-        const int n = globals ? max(0, (ntiles - first + 3) / 4)
-                              : max(0, min(first + a.tpw, ntiles) - first);
-        walk_tiles<D, KVT>(st, a, qv, n, j, kq, [&](int i, long long& ko, long long* vo) {
-            return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (first + i * step), vend, globals,
-                                          j, kq, ko, vo);
-        });
     }
 
-    // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
-    float lt = st.l + __shfl_xor(st.l, 16);
-    lt += __shfl_xor(lt, 32);
-    if (wave > 0) {
+    for (int pos = g0; pos < g1;) {
+        while (U * sload(&sm_pref[b + 1]) <= pos) b++;
+        const int pb = sload(&sm_pref[b]);
+        const int Tb = sload(&sm_pref[b + 1]) - pb;
+        const int u = (pos - U * pb) / Tb;
+        const int seg0 = U * pb + u * Tb;  // first global tile of segment (b, u)
+        const int t0 = pos - seg0;
+        const int t1 = min(Tb, t0 + (g1 - pos));
+        pos += t1 - t0;
+
+        const int kvh = u / a.n_hg;
+        const int hg = u - kvh * a.n_hg;
+        const int g_local = min(16, a.group - hg * 16);
+        const int head0 = kvh * a.group + hg * 16;
+        const Extent e = uniform_extent<ALIGNED>(a, b);
+
+        // Q operand (B of the QK product): head j, dims by qk_dim.
+        float qv[NC];
+        {
+            const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
+            const bool ok = j < g_local;
 #pragma unroll
-        for (int x = 0; x < DPL; x++) sm_acc[wave - 1][x][lane] = st.acc[x];
-    }
-    if (kq == 0) {
-        sm_m[wave][j] = st.m;
-        sm_l[wave][j] = lt;
-    }
-    __syncthreads();
-    const int slot_base = ((b * a.n_kv_heads + kvh) * a.n_hg + hg);
-    if (wave == 0) {
-        float mh[4], lh[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int hh = 4 * kq + r;
-            float M = fmaxf(fmaxf(sm_m[0][hh], sm_m[1][hh]), fmaxf(sm_m[2][hh], sm_m[3][hh]));
-            float sw[4], L = 0.f;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float mw = sm_m[w][hh];
-                sw[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-                L = __builtin_fmaf(sm_l[w][hh], sw[w], L);
-            }
-#pragma unroll
-            for (int x = 0; x < DPL; x++) {
-                float v = st.acc[x][r] * sw[0];
-#pragma unroll
-                for (int w = 1; w < 4; w++) v = __builtin_fmaf(sm_acc[w - 1][x][lane][r], sw[w], v);
-                st.acc[x][r] = v;
-            }
-            mh[r] = M;
-            lh[r] = L;
+            for (int cc = 0; cc < NC; cc++) qv[cc] = ok ? qrow[qk_dim<D, KVT>(cc, kq)] : 0.f;
         }
+
+        State<D> st;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int hh = 4 * kq + r;
-            if (hh >= g_local) continue;
-            const long long head = head0 + hh;
-            if (e.np == 1) {
-                const float inv = 1.0f / lh[r];
-                float* o = a.out + ((long long)b * a.n_heads + head) * D + DPL * j;
+        for (int x = 0; x < DPL; x++) st.acc[x] = floatx4{0.f, 0.f, 0.f, 0.f};
+        st.m = -INFINITY;
+        st.l = 0.f;
+
+        RowMap m;
+        m.table = a.tables ? a.tables + (long long)b * a.table_stride : nullptr;
+        m.block_stride = a.block_stride;
+        m.head_stride = a.head_stride;
+        m.token_stride = a.token_stride;
+        m.bt_log2 = a.bt_log2;
+        m.num_blocks = a.num_blocks;
+        m.table_len = a.table_stride;
+
+        // this wavefront's quarter of the piece [t0, t1)
+        const int n = t1 - t0;
+        const int wa = t0 + (wave * n) / 4;
+        const int wb = t0 + ((wave + 1) * n) / 4;
+        if (ALIGNED) {
+            const int mt = e.main_tiles;
+            const int me = min(wb, mt);
+            if (wa < me)
+                walk_main<D, KVT>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa, me - wa,
+                                  lane, j, kq);
+            const int ga = max(wa, mt) - mt;
+            const int gb = wb - mt;
+            walk_tiles<D, KVT>(st, a, qv, gb - ga, j, kq, [&](int i, long long& ko, long long* vo) {
+                return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (ga + i), e.n_glob, true, j, kq,
+                                              ko, vo);
+            });
+        } else {
+            walk_tiles<D, KVT>(st, a, qv, wb - wa, j, kq, [&](int i, long long& ko, long long* vo) {
+                return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (wa + i), e.L, false, j, kq, ko,
+                                              vo);
+            });
+        }
+
+        // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
+        float lt = st.l + __shfl_xor(st.l, 16);
+        lt += __shfl_xor(lt, 32);
+        if (wave > 0) {
 #pragma unroll
-                for (int x = 0; x < DPL / 4; x++)
-                    *(float4*)(o + 4 * x) = float4{st.acc[4 * x + 0][r] * inv, st.acc[4 * x + 1][r] * inv,
-                                                   st.acc[4 * x + 2][r] * inv, st.acc[4 * x + 3][r] * inv};
-            } else {
-                // device-coherent (write-through) stores: the merging workgroup
-                // may run on another XCD, whose L2 does not see this one's
-                const long long slot = ((long long)b * a.n_heads + head) * a.max_parts + wgp;
-                float* o = a.ws_acc + slot * D + DPL * j;
+            for (int x = 0; x < DPL; x++) sm_acc[wave - 1][x][lane] = st.acc[x];
+        }
+        if (kq == 0) {
+            sm_m[wave][j] = st.m;
+            sm_l[wave][j] = lt;
+        }
+        __syncthreads();
+        const bool whole = n == Tb;  // uniform: the segment is this piece
+        const int s = b * U + u;
+        const int slot = (int)blockIdx.x + s;
+        if (wave == 0) {
+            float mh[4], lh[4];
 #pragma unroll
-                for (int x = 0; x < DPL; x++)
-                    __hip_atomic_store(o + x, st.acc[x][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (j == 0) {
-                    float* ml = (float*)(a.ws_ml + slot);
-                    __hip_atomic_store(ml, mh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(ml + 1, lh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int r = 0; r < 4; r++) {
+                const int hh = 4 * kq + r;
+                float M = fmaxf(fmaxf(sm_m[0][hh], sm_m[1][hh]), fmaxf(sm_m[2][hh], sm_m[3][hh]));
+                float sw[4], L = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const float mw = sm_m[w][hh];
+                    sw[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+                    L = __builtin_fmaf(sm_l[w][hh], sw[w], L);
+                }
+#pragma unroll
+                for (int x = 0; x < DPL; x++) {
+                    float v = st.acc[x][r] * sw[0];
+#pragma unroll
+                    for (int w = 1; w < 4; w++) v = __builtin_fmaf(sm_acc[w - 1][x][lane][r], sw[w], v);
+                    st.acc[x][r] = v;
+                }
+                mh[r] = M;
+                lh[r] = L;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int hh = 4 * kq + r;
+                if (hh >= g_local) continue;
+                if (whole) {
+                    const float inv = 1.0f / lh[r];
+                    float* o = a.out + ((long long)b * a.n_heads + head0 + hh) * D + DPL * j;
+#pragma unroll
+                    for (int x = 0; x < DPL / 4; x++)
+                        *(float4*)(o + 4 * x) = float4{st.acc[4 * x + 0][r] * inv, st.acc[4 * x + 1][r] * inv,
+                                                       st.acc[4 * x + 2][r] * inv, st.acc[4 * x + 3][r] * inv};
+                } else {
+                    // device-coherent (write-through) stores: the merging workgroup
+                    // may run on another XCD, whose L2 does not see this one's
+                    float* o = a.ws_acc + ((long long)slot * 16 + hh) * D + DPL * j;
+#pragma unroll
+                    for (int x = 0; x < DPL; x++)
+                        __hip_atomic_store(o + x, st.acc[x][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (j == 0) {
+                        float* ml = (float*)(a.ws_ml + (long long)slot * 16 + hh);
+                        __hip_atomic_store(ml, mh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(ml + 1, lh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
+            if (!whole) {
+                // publish: the write-through stores complete before the arrival is
+                // counted; the last of the segment's pieces to arrive merges
+                __builtin_amdgcn_s_waitcnt(0);
+                int old = 0;
+                if (lane == 0)
+                    old = __hip_atomic_fetch_add(a.counters + s, 1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                old = __shfl(old, 0);
+                const int pieces = (seg0 + Tb - 1) / c - seg0 / c + 1;
+                if (lane == 0) sm_last = (old == pieces - 1);
+            }
         }
-        if (e.np > 1) {
-            // publish: the write-through stores complete before the arrival is
-            // counted; the last workgroup to arrive merges
-            __builtin_amdgcn_s_waitcnt(0);
-            int old = 0;
-            if (lane == 0)
-                old = __hip_atomic_fetch_add(a.counters + slot_base, 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-            old = __shfl(old, 0);
-            if (lane == 0) sm_last = (old == e.np - 1);
+        __syncthreads();  // also: LDS is free for the next piece
+        if (!whole && sm_last) {
+            const int gf = seg0 / c;
+            const int np = (seg0 + Tb - 1) / c - gf + 1;
+            const long long slot0 = (long long)gf + s;
+            merge_segment<D>(a.ws_acc + slot0 * 16 * D, a.ws_ml + slot0 * 16, np, g_local,
+                             a.out + ((long long)b * a.n_heads + head0) * D, threadIdx.x);
+            if (threadIdx.x == 0)
+                __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (e.np == 1) return;
-    __syncthreads();
-    if (!sm_last) return;
-    for (int hh = wave; hh < g_local; hh += 4) {
-        const long long head = head0 + hh;
-        merge_head<D>(a, ((long long)b * a.n_heads + head) * a.max_parts, e.np,
-                      a.out + ((long long)b * a.n_heads + head) * D, lane);
-    }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(a.counters + slot_base, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void fill_zero_kernel(int* p, long long n) {
@@ -650,45 +742,44 @@ __global__ void fill_zero_kernel(int* p, long long n) {
 
 // ---------------------------------------------------------------- host side
 
-static int g_tpw_override = 0;
-
-// Tiles per wavefront per partition.  Enough workgroups to fill 256 CUs
-// about four deep, each wavefront streaming as many 16-token tiles as that
-// allows (at most 64, one block-table slice per lane), so the partial
-// write-back and merge stay small next to the K/V bytes.
-static int pick_tpw(int batch, int units, int max_len) {
-    if (g_tpw_override > 0) return g_tpw_override;
-    const long long tiles = (long long)batch * units * ((max_len + 15) / 16);
-    const long long target_wg = 1024;
-    int t = 1;
-    while (t < 64 && 4LL * t * target_wg < tiles) t <<= 1;
-    return t;
-}
+// Tiles per workgroup the grid is sized for: small enough to spread a short
+// context over many CUs, large enough that each wavefront pipelines a few
+// tiles.  Workspace sizes assume the smallest allowed value, so tuning never
+// outgrows a workspace.
+constexpr int kDefaultWgTiles = 8;
+constexpr int kMinWgTiles = 4;
+constexpr int kMaxGrid = 2048;  // workgroups per launch (partial slots are sized for it)
+static int g_wg_tiles_override = 0;
 
 struct DecodePlan {
-    DecodeArgs a;
-    dim3 grid;
+    DecodeArgs a;      // batch field: set per launch
+    int batch;         // all sequences
+    int chunk;         // sequences per launch
+    int tiles_max;     // bound on the tiles of one segment
+    int grid_bound;    // workgroups per launch at most (sizes the partial slots)
     size_t ws_bytes;
     int head_dim;
     int kvt;
     bool aligned;
-    int batch;
 };
 
-static size_t ws_layout(int batch, int n_heads, int n_kv_heads, int n_hg, int head_dim,
-                        int max_parts, size_t* ml_off, size_t* ctr_off) {
-    if (max_parts <= 1) return 0;
-    const size_t slots = (size_t)batch * n_heads * max_parts;
-    size_t acc = (slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
-    size_t ml = (slots * sizeof(float2) + 255) & ~(size_t)255;
-    size_t ctr = ((size_t)batch * n_kv_heads * n_hg * sizeof(int) + 255) & ~(size_t)255;
+static size_t ws_layout(int slots, int segments, int head_dim, size_t* ml_off, size_t* ctr_off) {
+    const size_t acc = ((size_t)slots * 16 * head_dim * sizeof(float) + 255) & ~(size_t)255;
+    const size_t ml = ((size_t)slots * 16 * sizeof(float2) + 255) & ~(size_t)255;
+    const size_t ctr = ((size_t)segments * sizeof(int) + 255) & ~(size_t)255;
     if (ml_off) *ml_off = acc;
     if (ctr_off) *ctr_off = acc + ml;
     return acc + ml + ctr;
 }
 
-// max_main: host bound on the contiguous main range; globals: whether an
-// extra partition of strided globals may exist.
+static int grid_for(long long tiles, int wg_tiles, int cap) {
+    long long g = (tiles + wg_tiles - 1) / wg_tiles;
+    if (g > cap) g = cap;
+    return g < 1 ? 1 : (int)g;
+}
+
+// max_main: host bound on the contiguous main range; globals: whether
+// strided globals may exist.
 static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, int head_dim,
                        int kvt, int max_main, bool globals, bool aligned_path, float scale) {
     if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0)
@@ -701,29 +792,41 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     if (kvt != NYION_KV_F32 && kvt != NYION_KV_Q4_20B)
         return set_error(NYION_ERR_INVALID, "decode: kv_dtype %d", kvt);
     if (max_main <= 0) return set_error(NYION_ERR_INVALID, "decode: max_ctx must be positive");
-    if (batch > 65535) return set_error(NYION_ERR_UNSUPPORTED, "decode: batch %d > 65535", batch);
     DecodeArgs& a = pl.a;
     a = DecodeArgs{};
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
     a.group = n_heads / n_kv_heads;
     a.n_hg = (a.group + 15) / 16;
-    if (n_kv_heads * a.n_hg > 65535) return set_error(NYION_ERR_UNSUPPORTED, "decode: too many heads");
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
-    // the gather path walks the globals too, so its bound includes them
-    const int max_len = aligned_path ? max_main : max_main + (globals ? 128 : 0);
     a.max_len = max_main;
-    a.tpw = pick_tpw(batch, n_kv_heads * a.n_hg, max_len);
-    const int per_part = 4 * a.tpw;
-    const int tiles = (max_len + 15) / 16 + (aligned_path ? 1 : 0);
-    a.max_parts = (tiles + per_part - 1) / per_part + (aligned_path && globals ? 1 : 0);
+    const long long units = (long long)n_kv_heads * a.n_hg;
+    // aligned: main tiles <= max_main/16 + 2, globals (<= 128) <= 8 tiles;
+    // gather: the globals are part of the list
+    const long long tiles = aligned_path ? max_main / 16 + 2 + (globals ? 8 : 0)
+                                         : ((long long)max_main + (globals ? 128 : 0) + 15) / 16;
+    const long long per_seq = units * tiles;
+    if (per_seq >= (1LL << 31))
+        return set_error(NYION_ERR_UNSUPPORTED, "decode: %lld tiles per sequence", per_seq);
+    long long chunk = ((1LL << 31) - 1) / per_seq;
+    if (chunk > kMaxLaunchBatch) chunk = kMaxLaunchBatch;
+    if (chunk > batch) chunk = batch;
+    pl.batch = batch;
+    pl.chunk = (int)chunk;
+    pl.tiles_max = (int)tiles;
     pl.head_dim = head_dim;
     pl.kvt = kvt;
     pl.aligned = aligned_path;
-    pl.batch = batch;
-    pl.grid = dim3(a.max_parts, n_kv_heads * a.n_hg, batch);
-    pl.ws_bytes = ws_layout(batch, n_heads, n_kv_heads, a.n_hg, head_dim, a.max_parts, nullptr, nullptr);
+    pl.grid_bound = grid_for(chunk * per_seq, kMinWgTiles, kMaxGrid);
+    // one sequence over at most one workgroup per segment: no partials
+    if (batch == 1 && pl.grid_bound <= units) {
+        pl.grid_bound = (int)units;
+        pl.ws_bytes = 0;
+    } else {
+        pl.ws_bytes = ws_layout(pl.grid_bound + (int)(chunk * units), (int)(chunk * units), head_dim,
+                                nullptr, nullptr);
+    }
     return NYION_OK;
 }
 
@@ -733,32 +836,74 @@ static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes) {
         return set_error(NYION_ERR_WORKSPACE, "decode: workspace %zu bytes < required %zu", ws_bytes,
                          pl.ws_bytes);
     if (!aligned(ws, 256)) return set_error(NYION_ERR_INVALID, "decode: workspace not 256-byte aligned");
+    const int units = pl.a.n_kv_heads * pl.a.n_hg;
     size_t ml_off = 0, ctr_off = 0;
-    ws_layout(pl.batch, pl.a.n_heads, pl.a.n_kv_heads, pl.a.n_hg, pl.head_dim, pl.a.max_parts, &ml_off,
-              &ctr_off);
+    ws_layout(pl.grid_bound + pl.chunk * units, pl.chunk * units, pl.head_dim, &ml_off, &ctr_off);
     pl.a.ws_acc = (float*)ws;
     pl.a.ws_ml = (float2*)((char*)ws + ml_off);
     pl.a.counters = (int*)((char*)ws + ctr_off);
     return NYION_OK;
 }
 
-template <int D, int KVT>
+// Workgroups of one kernel instance resident on the whole device.
+template <int D, int KVT, bool AL>
+static int resident_capacity() {
+    static int cap = 0;
+    if (cap == 0) {
+        int per_cu = 0, cus = 0, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL>, 256, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            (void)hipGetLastError();
+            return 256;
+        }
+        cap = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    }
+    return cap;
+}
+
+template <int D, int KVT, bool AL>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
+    const int units = pl.a.n_kv_heads * pl.a.n_hg;
+    const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
+    const int cap = resident_capacity<D, KVT, AL>();
+    for (int b0 = 0; b0 < pl.batch; b0 += pl.chunk) {
+        const int nb = pl.batch - b0 < pl.chunk ? pl.batch - b0 : pl.chunk;
+        DecodeArgs a = pl.a;
+        a.batch = nb;
+        const long long qo = (long long)b0 * a.n_heads * D;
+        a.q += qo;
+        a.out += qo;
+        if (a.tables) a.tables += (long long)b0 * a.table_stride;
+        if (a.ctx_lens) a.ctx_lens += b0;
+        if (a.q_pos) a.q_pos += b0;
+        if (a.positions) a.positions += (long long)b0 * a.pos_stride;
+        if (a.n_pos) a.n_pos += b0;
+        int grid = grid_for((long long)nb * units * pl.tiles_max, wg_tiles, cap);
+        if (grid > pl.grid_bound) grid = pl.grid_bound;
+        if (pl.ws_bytes == 0 || (nb == 1 && grid <= units)) grid = units;  // whole segments
+        hipLaunchKernelGGL((decode_kernel<D, KVT, AL>), dim3(grid), dim3(256), 0, stream, a);
+    }
+}
+
+template <int D, int KVT>
+static void launch_dkt(const DecodePlan& pl, hipStream_t stream) {
     if (pl.aligned)
-        hipLaunchKernelGGL((decode_kernel<D, KVT, true>), pl.grid, dim3(256), 0, stream, pl.a);
+        launch_dk<D, KVT, true>(pl, stream);
     else
-        hipLaunchKernelGGL((decode_kernel<D, KVT, false>), pl.grid, dim3(256), 0, stream, pl.a);
+        launch_dk<D, KVT, false>(pl, stream);
 }
 
 static int launch_plan(const DecodePlan& pl, hipStream_t stream) {
     if (pl.head_dim == 64 && pl.kvt == NYION_KV_F32)
-        launch_dk<64, NYION_KV_F32>(pl, stream);
+        launch_dkt<64, NYION_KV_F32>(pl, stream);
     else if (pl.head_dim == 64)
-        launch_dk<64, NYION_KV_Q4_20B>(pl, stream);
+        launch_dkt<64, NYION_KV_Q4_20B>(pl, stream);
     else if (pl.kvt == NYION_KV_F32)
-        launch_dk<128, NYION_KV_F32>(pl, stream);
+        launch_dkt<128, NYION_KV_F32>(pl, stream);
     else
-        launch_dk<128, NYION_KV_Q4_20B>(pl, stream);
+        launch_dkt<128, NYION_KV_Q4_20B>(pl, stream);
     return check_launch("decode");
 }
 
@@ -786,17 +931,25 @@ using namespace nyion;
 extern "C" {
 
 int nyion_set_decode_partition_tokens(int tokens) {
-    if (tokens != 0 && (tokens < 64 || tokens > 4096 || !is_pow2(tokens)))
+    if (tokens != 0 && (tokens < 16 * kMinWgTiles || tokens > 4096 || !is_pow2(tokens)))
         return set_error(NYION_ERR_INVALID,
-                         "partition tokens %d: power of two in [64, 4096] (4 wavefronts x 16-token "
-                         "tiles) or 0", tokens);
-    g_tpw_override = tokens / 64;
+                         "partition tokens %d: power of two in [%d, 4096] or 0", tokens,
+                         16 * kMinWgTiles);
+    g_wg_tiles_override = tokens / 16;
     return NYION_OK;
 }
 
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len) {
-    (void)head_dim;
-    return 64 * pick_tpw(batch, n_kv_heads, max_len);
+    if (batch <= 0 || n_kv_heads <= 0 || max_len <= 0) return 0;
+    const long long tiles = (long long)batch * n_kv_heads * (max_len / 16 + 2);
+    const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
+    int cap = kMaxGrid;
+    if (require_device() == NYION_OK)
+        cap = head_dim == 128 ? resident_capacity<128, NYION_KV_F32, true>()
+                              : resident_capacity<64, NYION_KV_F32, true>();
+    clear_error();
+    const int grid = grid_for(tiles, wg_tiles, cap);
+    return (int)(16 * ((tiles + grid - 1) / grid));
 }
 
 size_t nyion_paged_decode_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
@@ -955,21 +1108,17 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
                           (int)seq_len, false, true, 0.f)) != NYION_OK)
         return rc;
     // The node's scores buffer (n_heads*kv_stride floats, the reference's
-    // ScratchBuffers::d_scores) holds the split-K partials; without it, or
-    // when it is too small, use longer partitions until one workgroup covers
-    // the sequence.
+    // ScratchBuffers::d_scores) holds the split-K partials when it is large
+    // enough; otherwise one workgroup covers each head group.
     DecodeArgs& a = pl.a;
     const size_t scores_bytes =
         d_scores && aligned(d_scores, 256) ? (size_t)n_heads * kv_stride * sizeof(float) : 0;
-    while (pl.ws_bytes > scores_bytes) {
-        a.tpw *= 2;
-        const int per_part = 4 * a.tpw;
-        const int tiles = ((int)seq_len + 15) / 16 + 1;
-        a.max_parts = (tiles + per_part - 1) / per_part;
-        pl.grid = dim3(a.max_parts, a.n_kv_heads * a.n_hg, 1);
-        pl.ws_bytes = ws_layout(1, a.n_heads, a.n_kv_heads, a.n_hg, (int)head_dim, a.max_parts,
-                                nullptr, nullptr);
+    const int units = a.n_kv_heads * a.n_hg;
+    while (pl.ws_bytes > scores_bytes && pl.grid_bound > units) {
+        pl.grid_bound = pl.grid_bound / 2 > units ? pl.grid_bound / 2 : units;
+        pl.ws_bytes = ws_layout(pl.grid_bound + units, units, (int)head_dim, nullptr, nullptr);
     }
+    if (pl.ws_bytes > scores_bytes) pl.ws_bytes = 0;  // whole segments: grid = units
     if ((rc = attach_workspace(pl, d_scores, scores_bytes)) != NYION_OK) return rc;
     const long long row = row_elems((int)head_dim, kv_dtype);
     a.q = d_q;
