@@ -73,17 +73,34 @@ def timed(fn, steps, warmup, torch):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def event_times(fn, reps, torch):
-    """Per-call device durations (ms) from HIP events on the current stream."""
+def event_mean(fn, reps, torch):
+    """Mean device time per call (ms): HIP events on the launching stream
+    around `reps` back-to-back calls (per-call event pairs would add the
+    event records' own cost to every call)."""
     st = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
-    for i, (a, b) in enumerate(evs):
-        a.record(st)
-        fn(i)
-        b.record(st)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn(0)
     torch.cuda.synchronize()
-    return np.array([a.elapsed_time(b) for a, b in evs])
+    a.record(st)
+    for i in range(reps):
+        fn(i)
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def pmc_traffic(workload):
+    """HBM bytes per launch of the decode kernel for `workload`, from the
+    calibrated FETCH_SIZE + WRITE_SIZE passes summarised under profiles/."""
+    path = os.path.join(ROOT, "profiles", "decode_hbm_traffic_pmc.txt")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == workload:
+                return float(f[2])
+    except OSError:
+        pass
+    return None
 
 
 def paged_tables(rng, n_seqs, nblk, total):
@@ -128,9 +145,8 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
 
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
     ms = timed(step, steps, warmup, torch)
-    # roofline: per decode call, HIP events on the launching stream
-    per = event_times(lambda i: layer_call(i % R, i % L), steps * 4, torch)
-    us_call = float(np.mean(per) * 1e3)
+    # roofline: decode calls timed with HIP events on the launching stream
+    us_call = event_mean(lambda i: layer_call(i % R, i % L), steps * L, torch) * 1e3
     achieved = bytes_layer / (us_call * 1e-6) / 1e9
     return {
         "ms_per_step": ms,
@@ -138,8 +154,6 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
         "gbs": L * bytes_layer / (ms * 1e-3) / 1e9,
         "bytes_per_layer": bytes_layer,
         "call_us_event_mean": us_call,
-        "call_us_event_p10_p90": [float(np.percentile(per, 10) * 1e3),
-                                  float(np.percentile(per, 90) * 1e3)],
         "achieved_call_gbs": achieved,
         "partition_tokens": nh.partition_tokens(1, Hkv, D, ctx),
         "workspace_bytes": ws_bytes,
@@ -212,9 +226,8 @@ def bench_c1(nh, torch, steps, warmup):
         nh.attention_node(q, k, v, out, 32, 4, 128, 64, 128, scores=scores)
 
     ms = timed(call, steps * 10, warmup, torch)
-    per = event_times(call, steps * 4, torch)
-    return {"us_per_layer": ms * 1e3, "call_us_event_mean": float(np.mean(per) * 1e3),
-            "bytes_per_layer": 278528}
+    us = event_mean(call, steps * 4, torch) * 1e3
+    return {"us_per_layer": ms * 1e3, "call_us_event_mean": us, "bytes_per_layer": 278528}
 
 
 def bench_c3(nh, torch, steps, warmup, seed=0):
@@ -247,11 +260,13 @@ def bench_c3(nh, torch, steps, warmup, seed=0):
     toks = int(lens.sum())
     nbytes = 2 * toks * Hkv * D * 4 + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
     ms = timed(call, steps, warmup, torch)
-    per = event_times(call, steps, torch)
-    us = float(np.mean(per) * 1e3)
+    us = event_mean(call, steps, torch) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"us_per_layer": us, "us_per_layer_wall": ms * 1e3, "bytes": nbytes, "tokens": toks,
             "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": pmc_traffic("c3")},
             "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
 
 
@@ -289,8 +304,7 @@ def bench_c4(nh, torch, steps, warmup, seed=0):
         n_pos = w + (128 if stride else 0)
         nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4 + B * (n_pos // bt + 8) * 4
         ms = timed(call, steps, warmup, torch)
-        per = event_times(call, steps, torch)
-        us = float(np.mean(per) * 1e3)
+        us = event_mean(call, steps, torch) * 1e3
         res[f"stride{stride}"] = {"us_per_layer": us, "us_per_layer_wall": ms * 1e3,
                                   "bytes_packed": nbytes,
                                   "gbs_packed": nbytes / (us * 1e-6) / 1e9}
@@ -319,8 +333,7 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
 
     s = max(3, steps // 5)
     ms = timed(attn, s, max(1, warmup // 5), torch)
-    per = event_times(attn, s, torch)
-    us = float(np.mean(per) * 1e3)
+    us = event_mean(attn, s, torch) * 1e3
     ms_kv = timed(attn_kv, s, 1, torch)
     tf = flops / (us * 1e-6) / 1e12
     return {"us": us, "us_wall": ms * 1e3, "us_with_kv_write": ms_kv * 1e3, "flops": flops,
@@ -400,7 +413,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(c2["achieved_call_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("c2"),
             "kernel": "decode_kernel<64,f32,aligned> (one launch per decode call)",
             "bytes_per_launch": c2["bytes_per_layer"],
             "launch_us": round(c2["call_us_event_mean"], 3),

@@ -110,7 +110,7 @@ int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float
  * head_dim in {64, 128}; n_heads % n_kv_heads == 0.
  * d_workspace: >= nyion_paged_decode_workspace_size(...) bytes (256-byte
  * aligned), or NULL when that size is 0.  It holds the split-K partials and
- * per-(sequence, kv head) arrival counters: it must be zero-filled before its
+ * per-(sequence, kv head, head group) arrival counters: it must be zero-filled before its
  * first use (nyion_decode_workspace_init, or any zeroing) and is left with
  * the counters at zero by every call.  Calls that run concurrently need
  * separate workspaces. */
@@ -143,9 +143,13 @@ int nyion_paged_decode_attention_positions(
  * recorded into a HIP graph).  Needed once before first use. */
 int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion_stream_t stream);
 
-/* Split-K partition length in tokens per workgroup (4 wavefronts x 16-token
- * tiles x tiles per wavefront: a power of two in 64..4096) used by the decode
- * entry points; 0 restores the automatic choice.  Process-wide; for tuning. */
+/* Decode work split.  The decode grid cuts the concatenated 16-token tile
+ * lists of all (sequence, kv head, head group) segments into equal ranges, one
+ * per workgroup; the grid is sized for `tokens` per workgroup (a power of two
+ * in 64..4096; 0 restores the default, 256) and capped at the workgroups the
+ * device holds resident.  Process-wide; for tuning.  The getter returns the
+ * tokens per workgroup the current setting gives for `batch` sequences of
+ * max_len tokens. */
 int nyion_set_decode_partition_tokens(int tokens);
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len);
 

@@ -178,8 +178,8 @@ struct Tile;
 
 template <int D>
 struct Tile<D, NYION_KV_F32> {
-    float4 k[D / 16];         // K row j: dims 16x + 4kq .. +3
-    float4 v[4][D / 64];      // V rows 4kq+r: dims DPL*j .. +DPL
+    floatx4 k[D / 16];        // K row j: dims 16x + 4kq .. +3
+    floatx4 v[4][D / 64];     // V rows 4kq+r: dims DPL*j .. +DPL
 };
 
 template <int D>
@@ -199,30 +199,32 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
     if constexpr (KVT == NYION_KV_F32) {
         const float* kr = (const float*)kb + koff;
 #pragma unroll
-        for (int x = 0; x < D / 16; x++) t.k[x] = *(const float4*)(kr + 16 * x + 4 * kq);
+        for (int x = 0; x < D / 16; x++)
+            t.k[x] = __builtin_nontemporal_load((const floatx4*)(kr + 16 * x + 4 * kq));
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const float* vr = (const float*)vb + voff[r] + (D / 16) * j;
 #pragma unroll
-            for (int x = 0; x < D / 64; x++) t.v[r][x] = *(const float4*)(vr + 4 * x);
+            for (int x = 0; x < D / 64; x++)
+                t.v[r][x] = __builtin_nontemporal_load((const floatx4*)(vr + 4 * x));
         }
     } else {
         const int ke0 = kq * (D / 4);
         const uint8_t* kr = (const uint8_t*)kb + koff + kQ4GroupBytes * (ke0 >> 5);
-        t.khdr = *(const uint32_t*)kr;
+        t.khdr = __builtin_nontemporal_load((const uint32_t*)kr);
         const uint32_t* kn = (const uint32_t*)(kr + 4 + ((ke0 & 31) >> 1));
 #pragma unroll
-        for (int w = 0; w < D / 32; w++) t.k[w] = kn[w];
+        for (int w = 0; w < D / 32; w++) t.k[w] = __builtin_nontemporal_load(kn + w);
         const int ve0 = (D / 16) * j;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint8_t* vr = (const uint8_t*)vb + voff[r] + kQ4GroupBytes * (ve0 >> 5);
-            t.vhdr[r] = *(const uint32_t*)vr;
+            t.vhdr[r] = __builtin_nontemporal_load((const uint32_t*)vr);
             const uint8_t* vn = vr + 4 + ((ve0 & 31) >> 1);
             if constexpr (D == 64)
-                t.v[r] = (uint32_t)(*(const uint16_t*)vn);
+                t.v[r] = (uint32_t)__builtin_nontemporal_load((const uint16_t*)vn);
             else
-                t.v[r] = *(const uint32_t*)vn;
+                t.v[r] = __builtin_nontemporal_load((const uint32_t*)vn);
         }
     }
 }
@@ -515,13 +517,14 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
 
 __device__ __forceinline__ int sload(const int* p) { return __builtin_amdgcn_readfirstlane(*p); }
 
-// Occupancy target, which bounds the registers the compiler may use: three
-// workgroups (12 wavefronts) per CU for head_dim 64, two for packed 4-bit KV
-// at head_dim 128, and one for f32 KV at 128, whose two register-resident
-// 16-token tiles alone take 128 VGPRs per lane.
+// Occupancy target, which bounds the registers the compiler may use: two
+// workgroups (8 wavefronts) per CU, except f32 KV at head_dim 128, whose two
+// register-resident 16-token tiles alone take 128 VGPRs per lane (one).  Two
+// tiles of loads in flight per wavefront at this occupancy keep ~32 MB of
+// reads outstanding, more than HBM latency x bandwidth.
 template <int D, int KVT, bool ALIGNED>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (KVT == NYION_KV_F32 ? 1 : 2))))
+__attribute__((amdgpu_waves_per_eu((D == 128 && KVT == NYION_KV_F32) ? 1 : 2)))
 void decode_kernel(DecodeArgs a) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
@@ -746,7 +749,7 @@ __global__ void fill_zero_kernel(int* p, long long n) {
 // context over many CUs, large enough that each wavefront pipelines a few
 // tiles.  Workspace sizes assume the smallest allowed value, so tuning never
 // outgrows a workspace.
-constexpr int kDefaultWgTiles = 8;
+constexpr int kDefaultWgTiles = 16;
 constexpr int kMinWgTiles = 4;
 constexpr int kMaxGrid = 2048;  // workgroups per launch (partial slots are sized for it)
 static int g_wg_tiles_override = 0;
