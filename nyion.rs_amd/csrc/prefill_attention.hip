@@ -8,20 +8,30 @@
 // Work decomposition.  A 256-thread workgroup owns one kv head and four
 // (q head, 32-row block) pairs that read the same K/V: for GQA 4:1 these are
 // the four q heads of the group on the same 32 rows, so every K/V tile staged
-// in LDS feeds four wavefronts.  Row blocks are issued longest-first.
+// in LDS feeds four wavefronts.  Workgroups are numbered so that each XCD
+// (workgroup id mod 8) takes a contiguous run of the (kv head, row block)
+// list: with 8 kv heads every XCD's L2 holds the K/V of one head.  Within a
+// head, row blocks are issued longest-first.
 //
 // Per 64-key tile:
 //   K tile  [64][D] bf16 -> LDS, 16-byte chunks XOR-swizzled by key row
-//   V tile  [64][D] bf16 -> LDS transposed to V^T [D][64] (key pairs packed
-//           into 32-bit words, 8-byte chunks XOR-swizzled by dim row)
+//   V tile  [64][D] bf16 -> LDS as fp16, transposed to V^T [D][64] (key
+//           pairs packed into 32-bit words, 8-byte chunks XOR-swizzled by
+//           dim row)
 //   S^T[64 keys][32 rows] = K . Q^T      v_mfma_f32_32x32x16_bf16, Q^T from
 //                                        registers (loaded once)
-//   online softmax per row (rows are lanes; 32 keys per lane per half)
-//   O[32 rows][D] += P . V               A = P converted in registers from
-//                                        the S^T accumulators (no shuffles),
-//                                        as bf16 hi + lo (two MFMAs), B = V^T
-//                                        from LDS
-// The next tile's global loads are issued before the current tile's MFMAs.
+//   online softmax per row (rows are lanes; 32 keys per lane per half), the
+//   running max moved only when a tile exceeds it by 2^8
+//   O[32 rows][D] += P . V               v_mfma_f32_32x32x16_f16, A = P in
+//                                        fp16 converted in registers from the
+//                                        S^T accumulators, B = V^T from LDS
+// LDS holds two tiles: the next tile is written from registers (its global
+// loads were issued a whole tile earlier) while the current one is consumed,
+// with one barrier per tile.
+//
+// fp16 for P and V keeps 11 significant bits (p <= 2^8 after the lazy max),
+// so the P.V product stays within the f32 reference's tolerance; V must lie
+// within the fp16 range (|v| <= 65504).
 #include <math.h>
 
 #include "common.hpp"
@@ -31,6 +41,8 @@ namespace nyion {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 int kv_write_impl(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
                   int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
@@ -51,56 +63,130 @@ struct PrefillArgs {
     int hw;        // q heads per workgroup (min(group, 4))
     int rb_per_wg; // 32-row blocks per workgroup (4 / hw)
     int n_rbg;     // row-block groups
+    int n_items;   // kv heads x head subsets x row-block groups
     int causal;
     float scale_log2;
 };
 
 constexpr int BN = 64;  // keys per tile
+constexpr float kPrefillRescaleLog2 = 8.0f;
 
+// LDS tiles, padded by 16 bytes per row so that every lane's reads are one
+// base address plus compile-time offsets (no per-read address registers):
+//   K   [BN][D] bf16, row stride D*2+16 bytes;
+//   V^T [D][BN] fp16, row stride BN*2+16 bytes.  Within each 16-key group the
+//       keys sit in the order 0-3, 8-11, 4-7, 12-15, which is the order of
+//       the PV k-step's B operand (lane half h holds keys 4h..4h+3 and
+//       8+4h..8+4h+3), so one 16-byte read fetches it.
 template <int D>
-struct PrefillSmem {
-    // K tile: [BN][D] bf16, chunk c of key i at (c ^ (i % (D/8)))
-    uint4 k[BN * D / 8];
-    // V^T tile: [D][BN] bf16 as words; 8-byte chunk q of dim row r at q ^ ((r>>1)&15)
-    uint32_t vt[D * BN / 2];
+struct PrefillLds {
+    static constexpr int KROW = D * 2 + 16;   // bytes
+    static constexpr int VROW = BN * 2 + 16;  // bytes
+    static constexpr int KBYTES = BN * KROW;
+    static constexpr int VBYTES = D * VROW;
+    static constexpr int BUF = KBYTES + VBYTES;
+};
+
+// Position of key w (0..15) of a 16-key group in V^T row order.
+__device__ __forceinline__ int vt_pos(int w) {
+    return (w & 3) | (((w >> 3) & 1) << 2) | (((w >> 2) & 1) << 3);
+}
+
+__device__ __forceinline__ uint32_t bf16_to_f16_bits(uint32_t b) {
+    const _Float16 h = (_Float16)__uint_as_float(b << 16);
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// One tile's K and V in registers between its global loads and its LDS
+// stores (K chunk u: key (tid+256u) / (D/8); V unit u: key pair and 8 dims).
+template <int D>
+struct TileStage {
+    static constexpr int KLOADS = BN * (D / 8) / 256;
+    static constexpr int VUNITS = (BN / 2) * (D / 8) / 256;
+    u32x4 k[KLOADS];
+    u32x4 v0[VUNITS];
+    u32x4 v1[VUNITS];
 };
 
 template <int D>
-__device__ __forceinline__ int k_chunk_index(int key, int c) {
-    return key * (D / 8) + (c ^ (key % (D / 8)));
+__device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kbase,
+                                           const uint16_t* vbase, long long tok_stride, int n,
+                                           int kt, int tid) {
+    constexpr int CPR = D / 8;
+#pragma unroll
+    for (int u = 0; u < TileStage<D>::KLOADS; u++) {
+        const int id = tid + 256 * u;
+        const int t = min(kt + id / CPR, n - 1);  // keys past n: finite values, masked
+        st.k[u] = *(const u32x4*)(kbase + t * tok_stride + 8 * (id % CPR));
+    }
+#pragma unroll
+    for (int u = 0; u < TileStage<D>::VUNITS; u++) {
+        const int id = tid + 256 * u;
+        const int t = kt + 2 * (id % (BN / 2));
+        const int dc = id / (BN / 2);
+        st.v0[u] = t < n ? *(const u32x4*)(vbase + t * tok_stride + 8 * dc) : u32x4{0, 0, 0, 0};
+        st.v1[u] = t + 1 < n ? *(const u32x4*)(vbase + (t + 1) * tok_stride + 8 * dc)
+                             : u32x4{0, 0, 0, 0};
+    }
 }
 
-// Word index of keys (4*qc + 2*half .. +1) in V^T row r.
-__device__ __forceinline__ int vt_word(int r, int qc, int half) {
-    return r * (BN / 2) + ((qc ^ ((r >> 1) & 15)) << 1) + half;
+
+template <int D>
+__device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned char* base, int tid) {
+    using L = PrefillLds<D>;
+    constexpr int CPR = D / 8;
+#pragma unroll
+    for (int u = 0; u < TileStage<D>::KLOADS; u++) {
+        const int id = tid + 256 * u;
+        *(u32x4*)(base + (id / CPR) * L::KROW + 16 * (id % CPR)) = st.k[u];
+    }
+    unsigned char* vt = base + L::KBYTES;
+#pragma unroll
+    for (int u = 0; u < TileStage<D>::VUNITS; u++) {
+        const int id = tid + 256 * u;
+        const int key = 2 * (id % (BN / 2));
+        const int dc = id / (BN / 2);
+        const int col = (key & ~15) + vt_pos(key & 15);  // even: keys key, key+1
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            // dim 8dc+e: low half from key, high half from key+1
+            const uint32_t x0 = st.v0[u][e >> 1], x1 = st.v1[u][e >> 1];
+            const uint32_t lo = bf16_to_f16_bits((e & 1) ? (x0 >> 16) : (x0 & 0xffffu));
+            const uint32_t hi = bf16_to_f16_bits((e & 1) ? (x1 >> 16) : (x1 & 0xffffu));
+            *(uint32_t*)(vt + (8 * dc + e) * L::VROW + 2 * col) = lo | (hi << 16);
+        }
+    }
 }
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
-    constexpr int CPR = D / 8;              // 16-byte chunks per row
-    constexpr int KLOADS = BN * CPR / 256;  // K chunks per thread per tile
-    constexpr int VUNITS = (BN / 2) * (D / 8) / 256;  // (key pair, 8 dims) units per thread
-    constexpr int DT = D / 32;              // output dim tiles
-    constexpr int KS = D / 16;              // k-steps of the S product
+    using L = PrefillLds<D>;
+    constexpr int DT = D / 32;  // output dim tiles
+    constexpr int KS = D / 16;  // k-steps of the S product
 
-    __shared__ PrefillSmem<D> sm;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * L::BUF];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31;   // row (S^T col) / dim within tile (O col)
     const int h = lane >> 5;   // half
 
-    // workgroup -> (kv head, head subset, row-block group)
+    // workgroup -> work item: XCD x = id % 8 takes items [x*per, (x+1)*per)
+    const int per = (a.n_items + 7) / 8;
+    const int item = ((int)blockIdx.x & 7) * per + ((int)blockIdx.x >> 3);
+    if (item >= a.n_items) return;
+    const int p = item / a.n_rbg;                         // kv head * subsets + subset
+    const int rbg = a.n_rbg - 1 - (item - p * a.n_rbg);  // longest first
     const int subsets = a.group / a.hw;
-    const int rbg = a.n_rbg - 1 - (int)blockIdx.x;  // longest first
-    const int g = blockIdx.y / subsets;
-    const int hs = blockIdx.y - g * subsets;
+    const int g = p / subsets;
+    const int hs = p - g * subsets;
     const int head = g * a.group + hs * a.hw + (wave % a.hw);
     const int row0 = (rbg * a.rb_per_wg + wave / a.hw) * 32;
     const int wg_row_end = min(a.n, (rbg + 1) * a.rb_per_wg * 32);
     const int key_end = a.causal ? wg_row_end : a.n;
     const int n_tiles = (key_end + BN - 1) / BN;
+    const int lim = a.causal ? min(row0 + j, a.n - 1) : a.n - 1;  // last key of this lane's row
 
     // Q^T operand (B of S^T = K.Q^T): row row0+j, dims 16s + 8h .. +7
     bf16x8 qreg[KS];
@@ -118,148 +204,100 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     floatx16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; t++) o[t] = floatx16{};
-    float mrun = -INFINITY;
+    float mrun = -1e30f;  // finite: exp2(s - mrun) of a masked s is 0, never NaN
     float lrun = 0.f;
 
-    // global -> register staging of one tile
-    uint4 kst[KLOADS];
-    uint4 vst[VUNITS][2];
-    auto load_tile = [&](int kt) {
-#pragma unroll
-        for (int u = 0; u < KLOADS; u++) {
-            const int id = tid + 256 * u;
-            const int key = id / CPR, c = id % CPR;
-            const int t = kt + key;
-            kst[u] = t < a.n ? *(const uint4*)(a.k + ((long long)t * a.n_kv_heads + g) * D + 8 * c)
-                             : uint4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int u = 0; u < VUNITS; u++) {
-            const int id = tid + 256 * u;
-            const int kp = id % (BN / 2), dc = id / (BN / 2);
-            const int t = kt + 2 * kp;
-            vst[u][0] = t < a.n ? *(const uint4*)(a.v + ((long long)t * a.n_kv_heads + g) * D + 8 * dc)
-                                : uint4{0, 0, 0, 0};
-            vst[u][1] = t + 1 < a.n
-                            ? *(const uint4*)(a.v + ((long long)(t + 1) * a.n_kv_heads + g) * D + 8 * dc)
-                            : uint4{0, 0, 0, 0};
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int u = 0; u < KLOADS; u++) {
-            const int id = tid + 256 * u;
-            const int key = id / CPR, c = id % CPR;
-            sm.k[k_chunk_index<D>(key, c)] = kst[u];
-        }
-#pragma unroll
-        for (int u = 0; u < VUNITS; u++) {
-            const int id = tid + 256 * u;
-            const int kp = id % (BN / 2), dc = id / (BN / 2);
-            const uint32_t* a0 = (const uint32_t*)&vst[u][0];
-            const uint32_t* a1 = (const uint32_t*)&vst[u][1];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // dims 8dc+e: low half from key 2kp, high half from key 2kp+1
-                const uint32_t lo = (e & 1) ? (a0[e >> 1] >> 16) : (a0[e >> 1] & 0xffffu);
-                const uint32_t hi = (e & 1) ? (a1[e >> 1] >> 16) : (a1[e >> 1] & 0xffffu);
-                const int r = 8 * dc + e;
-                const int key = 2 * kp;
-                sm.vt[vt_word(r, key >> 2, (key >> 1) & 1)] = lo | (hi << 16);
-            }
-        }
-    };
+    // Per-thread roles in staging a tile (fixed for the whole loop).
+    //   K: chunk id = tid + 256u -> key id / CPR, chunk id % CPR
+    //   V: unit id = tid + 256u -> key pair id % (BN/2), dim chunk id / (BN/2)
+    const uint16_t* kbase = a.k + (long long)g * D;
+    const uint16_t* vbase = a.v + (long long)g * D;
+    const long long tok_stride = (long long)a.n_kv_heads * D;
+    TileStage<D> stg;
 
-    if (n_tiles > 0) load_tile(0);
-    for (int it = 0; it < n_tiles; it++) {
-        const int kt = it * BN;
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (it + 1 < n_tiles) load_tile(kt + BN);
-
-        // S^T for the two 32-key halves of the tile
-        floatx16 st[2];
+    // One 32-key half kb of the tile in buffer `buf`: S^T, online softmax,
+    // O += P.V over its two 16-key k-steps.
+    auto consume_half = [&](int buf, int kt, int kb, bool masked) {
+        const unsigned char* base = lds + buf * L::BUF;
+        // K rows kb*32 + j, chunk 2s + h
+        const unsigned char* kp = base + (kb * 32 + j) * L::KROW + 16 * h;
+        floatx16 st = floatx16{};
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            st[kb] = floatx16{};
-            const int key = kb * 32 + j;
-#pragma unroll
-            for (int s = 0; s < KS; s++) {
-                const bf16x8 kf = __builtin_bit_cast(bf16x8, sm.k[k_chunk_index<D>(key, 2 * s + h)]);
-                st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qreg[s], st[kb], 0, 0, 0);
-            }
+        for (int s = 0; s < KS; s++) {
+            const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
+            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qreg[s], st, 0, 0, 0);
         }
-
         // scale + mask; lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
-        const int row = row0 + j;
-        const bool need_mask = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[r] *= a.scale_log2;
+        if (masked) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                st[r] = key <= lim ? st[r] : -INFINITY;
+            }
+        }
         float mt = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float s = st[kb][r] * a.scale_log2;
-                if (need_mask) {
-                    const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (key >= a.n || (a.causal && key > row)) s = -INFINITY;
-                }
-                st[kb][r] = s;
-                mt = fmaxf(mt, s);
-            }
+        for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        // rows past the end (row >= n) see only -inf in the causal mask when
-        // row0+j exceeds every key; keep their max finite
-        const float mnew = fmaxf(fmaxf(mrun, mt), -1e30f);
-        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-        mrun = mnew;
-        float psum = 0.f;
-        // A operands of the PV product, k-step t = 2kb + half.  P is split
-        // into bf16 hi + lo parts (p - hi is exact in f32), so the PV product
-        // carries ~16 significant bits of p instead of 8.
-        bf16x8 pa[4], pl[4];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int t2 = 0; t2 < 2; t2++) {
-                bf16x8 pk, pr;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float p = __builtin_amdgcn_exp2f(st[kb][8 * t2 + e] - mnew);
-                    psum += p;
-                    const __bf16 hi = (__bf16)p;
-                    pk[e] = hi;
-                    pr[e] = (__bf16)(p - (float)hi);
-                }
-                pa[2 * kb + t2] = pk;
-                pl[2 * kb + t2] = pr;
-            }
-        lrun = __builtin_fmaf(lrun, alpha, psum);
-
-        // rescale O rows whose max moved (O reg r of this lane is row 8(r/4)+4h+r%4)
-        if (__any(alpha != 1.0f)) {
+        // the running max moves only when some row's max exceeds it by more
+        // than 2^8, so most halves skip the O rescale (p stays <= 2^8)
+        if (__any(mt > mrun + kPrefillRescaleLog2)) {
+            const float mnew = fmaxf(mrun, mt);
+            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
+                // O reg r of this lane is row 8(r/4) + 4h + r%4
                 const float ar = __shfl(alpha, 8 * (r >> 2) + 4 * h + (r & 3));
 #pragma unroll
                 for (int t = 0; t < DT; t++) o[t][r] *= ar;
             }
         }
-
-        // O += P . V
+        // A operands of the PV product: k-step t2 of this half holds keys
+        // 16t2 + 8(e/4) + 4h + e%4 (e = 0..7) of the half
+        halfx8 pa[2];
+        float psum = 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float pv = __builtin_amdgcn_exp2f(st[8 * t2 + e] - mrun);
+                psum += pv;
+                pa[t2][e] = (_Float16)pv;
+            }
+        lrun += psum;
+        // B operands: V^T row 32dt + j, the 8 keys of k-step t = 2kb + t2
+        const unsigned char* vp = base + L::KBYTES + j * L::VROW + 16 * h + 64 * kb;
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
-                const int r = 32 * dt + j;  // V^T row (dim)
-                const uint2 w0 = *(const uint2*)&sm.vt[vt_word(r, 4 * t + h, 0)];
-                const uint2 w1 = *(const uint2*)&sm.vt[vt_word(r, 4 * t + 2 + h, 0)];
-                const uint4 w = uint4{w0.x, w0.y, w1.x, w1.y};
-                const bf16x8 vb = __builtin_bit_cast(bf16x8, w);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t], vb, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl[t], vb, o[dt], 0, 0, 0);
+                const halfx8 vb =
+                    __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb, o[dt], 0, 0, 0);
             }
+    };
+
+    stage_load<D>(stg, kbase, vbase, tok_stride, a.n, 0, tid);
+    stage_store<D>(stg, lds, tid);
+    __syncthreads();
+    if (n_tiles > 1) stage_load<D>(stg, kbase, vbase, tok_stride, a.n, BN, tid);
+    for (int it = 0; it < n_tiles; it++) {
+        const int kt = it * BN;
+        const int cur = it & 1;
+        const bool masked = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0);
+        consume_half(cur, kt, 0, masked);
+        consume_half(cur, kt, 1, masked);
+        // stage the next tile into the other buffer (last read one tile ago,
+        // before the previous barrier) and start loading the one after
+        if (it + 1 < n_tiles) {
+            stage_store<D>(stg, lds + (cur ^ 1) * L::BUF, tid);
+            if (it + 2 < n_tiles) stage_load<D>(stg, kbase, vbase, tok_stride, a.n, kt + 2 * BN, tid);
         }
+        __syncthreads();
     }
 
     // epilogue: divide by the row sums and store
@@ -279,6 +317,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 }  // namespace nyion
+
+
+
+
 
 using namespace nyion;
 
@@ -316,12 +358,13 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
     a.rb_per_wg = 4 / hw;
     const int rows_per_wg = 32 * a.rb_per_wg;
     a.n_rbg = (n + rows_per_wg - 1) / rows_per_wg;
+    const long long items = (long long)n_kv_heads * (group / hw) * a.n_rbg;
+    if (items > (1LL << 30)) return set_error(NYION_ERR_UNSUPPORTED, "prefill: %lld work items", items);
+    a.n_items = (int)items;
     a.causal = causal ? 1 : 0;
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
-    if ((long long)n_kv_heads * (group / hw) > 65535)
-        return set_error(NYION_ERR_UNSUPPORTED, "prefill: too many heads");
-    dim3 grid(a.n_rbg, n_kv_heads * (group / hw));
+    dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
     if (head_dim == 128)
         hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);
