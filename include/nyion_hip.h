@@ -124,6 +124,26 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
                                  int max_ctx, float scale, float* d_out, void* d_workspace,
                                  size_t workspace_bytes, nyion_stream_t stream);
 
+/* Tracked decode: the executor's Full decode call, ops::attention_tracked
+ * (ops.rs:283-401, called at executor.rs:742-749).  Same arguments and
+ * output as nyion_paged_decode_attention, plus
+ *   d_importance [batch][importance_stride] f64: importance[b][t] +=
+ *     sum over q heads of the normalised probability of position t (f32
+ *     probabilities accumulated in f64), for every attended t; other
+ *     entries are left as they are.  importance_stride >= max_ctx.
+ *   d_scores [batch][n_heads][scores_stride] f32 scratch, scores_stride >=
+ *     max_ctx + 2: receives the scaled scores (log2 units) of the attended
+ *     positions and, in its last two entries per row, the head's softmax
+ *     max and denominator.
+ * Two launches on `stream` (the decode, then the importance sum). */
+int nyion_paged_decode_attention_tracked(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, double* d_importance,
+    int importance_stride, nyion_stream_t stream);
+
 /* Decode over explicit position lists (ops::attention_fugu, ops.rs:445-541,
  * whose list is the sparse set plus DSPark positions; also the Mojo
  * sparse_attention_q4 FFI, swamp-gpu/src/mojo.rs:5).  Softmax over exactly

@@ -67,6 +67,8 @@ struct DecodeArgs {
     float* ws_acc;             // partial slot p: [p][16 heads][D]
     float2* ws_ml;             // [p][16 heads] = (m log2, l)
     int* counters;             // [segment], zero between calls
+    float* scores;             // tracked decode: [B][Hq][scores_stride] scaled scores (log2)
+    int scores_stride;         // >= attended positions + 2; the row ends hold (m, l)
     long long block_stride;
     long long head_stride;
     int table_stride;
@@ -280,10 +282,12 @@ struct State {
 constexpr float kRescaleLog2 = 8.0f;
 
 // One tile: bit i of `mask` (wave-uniform) marks row i of the 16 valid;
-// MASKED = false is the all-valid fast path.
-template <int D, int KVT, bool MASKED>
+// MASKED = false is the all-valid fast path.  TRACK: also store the scaled
+// scores of this lane's head (rows 4kq+r, at positions pos[r]) into srow.
+template <int D, int KVT, bool MASKED, bool TRACK>
 __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t, const float* qv,
-                                             uint32_t mask, int kq, float scale_log2) {
+                                             uint32_t mask, int kq, float scale_log2, float* srow,
+                                             const int* pos) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
     float kv[NC];
@@ -297,6 +301,11 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
     for (int r = 0; r < 4; r++) {
         sv[r] = s[r] * scale_log2;
         if (MASKED) sv[r] = ((mask >> (4 * kq + r)) & 1u) ? sv[r] : -1e30f;
+    }
+    if (TRACK && srow) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if ((mask >> (4 * kq + r)) & 1u) srow[pos[r]] = sv[r];
     }
     float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mt = fmaxf(mt, __shfl_xor(mt, 16));
@@ -332,13 +341,14 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
     }
 }
 
-template <int D, int KVT>
+template <int D, int KVT, bool TRACK>
 __device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, const float* qv,
-                                        uint32_t mask, int kq, float scale_log2) {
+                                        uint32_t mask, int kq, float scale_log2, float* srow,
+                                        const int* pos) {
     if (mask == 0xffffu)
-        consume_tile<D, KVT, false>(st, t, qv, mask, kq, scale_log2);
+        consume_tile<D, KVT, false, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos);
     else if (mask)
-        consume_tile<D, KVT, true>(st, t, qv, mask, kq, scale_log2);
+        consume_tile<D, KVT, true, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos);
 }
 
 // Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
@@ -354,8 +364,10 @@ struct AlignedWalk {
 template <int D, int KVT>
 __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const AlignedWalk& w,
                                                     int tile, int j, int kq, long long& koff,
-                                                    long long* voff) {
+                                                    long long* voff, int* pos) {
     const int t0 = w.base + 16 * tile;
+#pragma unroll
+    for (int r = 0; r < 4; r++) pos[r] = t0 + 4 * kq + r;
     int blk = 0;
     if (a.tables) blk = __builtin_amdgcn_readlane(w.tblv, (t0 >> a.bt_log2) - w.bi_first);
     const int vlo = max(w.lo - t0, 0);
@@ -382,19 +394,19 @@ template <int D, int KVT>
 __device__ __forceinline__ uint32_t gather_offsets(const DecodeArgs& a, const Extent& e,
                                                    const RowMap& m, int b, int kvh, int v0,
                                                    int vend, bool globals, int j, int kq,
-                                                   long long& koff, long long* voff) {
-    auto off_of = [&](int v) -> long long {
+                                                   long long& koff, long long* voff, int* pos) {
+    auto pos_of = [&](int v) -> int {
         if (v >= vend) return -1;
-        const int pos = globals ? v * a.global_stride : virt_to_pos(a, e, b, v);
-        if (pos < 0) return -1;
-        return row_offset(m, pos, kvh);
+        return globals ? v * a.global_stride : virt_to_pos(a, e, b, v);
     };
-    koff = off_of(v0 + j);
+    auto off_of = [&](int p) -> long long { return p < 0 ? -1 : row_offset(m, p, kvh); };
+    koff = off_of(pos_of(v0 + j));
     const uint32_t mask = (uint32_t)(__ballot(koff >= 0) & 0xffffu);
     koff = koff < 0 ? 0 : koff;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const long long o = off_of(v0 + 4 * kq + r);
+        pos[r] = pos_of(v0 + 4 * kq + r);
+        const long long o = off_of(pos[r]);
         voff[r] = o < 0 ? 0 : o;
     }
     return mask;
@@ -404,21 +416,22 @@ __device__ __forceinline__ uint32_t gather_offsets(const DecodeArgs& a, const Ex
 // Every step issues exactly one tile of loads (at the end, a repeat of the
 // last tile that is never consumed), so the number of loads in flight is the
 // same on every path and each tile waits only for its own loads.
-template <int D, int KVT, typename Offsets>
+template <int D, int KVT, bool TRACK, typename Offsets>
 __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, const float* qv, int n,
-                                           int j, int kq, Offsets offsets) {
+                                           int j, int kq, float* srow, Offsets offsets) {
     Tile<D, KVT> ta, tb;
     long long ko, vo[4];
+    int pa[4], pb[4];  // positions of this lane's score rows (used when TRACK)
     if (n <= 0) return;
-    uint32_t ma = offsets(0, ko, vo);
+    uint32_t ma = offsets(0, ko, vo, pa);
     load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
     for (int i = 0; i < n; i += 2) {
-        uint32_t mb = offsets(min(i + 1, n - 1), ko, vo);
+        uint32_t mb = offsets(min(i + 1, n - 1), ko, vo, pb);
         load_tile<D, KVT>(tb, a.k, a.v, ko, vo, j, kq);
-        consume<D, KVT>(st, ta, qv, ma, kq, a.scale_log2);
-        ma = offsets(min(i + 2, n - 1), ko, vo);
+        consume<D, KVT, TRACK>(st, ta, qv, ma, kq, a.scale_log2, srow, pa);
+        ma = offsets(min(i + 2, n - 1), ko, vo, pa);
         load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
-        if (i + 1 < n) consume<D, KVT>(st, tb, qv, mb, kq, a.scale_log2);
+        if (i + 1 < n) consume<D, KVT, TRACK>(st, tb, qv, mb, kq, a.scale_log2, srow, pb);
     }
 }
 
@@ -430,7 +443,7 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
 // online.
 template <int D>
 __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int g_local, float* out,
-                              int tid) {
+                              int tid, float* score_rows, int scores_stride) {
     constexpr int QPH = D / 4;  // quads per head
     constexpr int CH = 16;      // partials per batch of loads
     for (int item = tid; item < g_local * QPH; item += 256) {
@@ -477,6 +490,11 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
         }
         const float inv = 1.0f / L;
         *(float4*)(out + hh * D + 4 * dq) = float4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        if (score_rows && dq == 0) {  // final (m, l) of the head: end of its score row
+            float* sr = score_rows + (long long)hh * scores_stride;
+            sr[scores_stride - 2] = M;
+            sr[scores_stride - 1] = L;
+        }
     }
 }
 
@@ -485,10 +503,10 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
 // Main tiles [first, first + n) of one segment on the aligned path, in runs of
 // at most 64 tiles: lane l holds the block id of the run's l-th block index
 // (with blocks of >= 16 tokens a run of 64 tiles spans at most 64 blocks).
-template <int D, int KVT>
+template <int D, int KVT, bool TRACK>
 __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, const float* qv,
                                           const Extent& e, const int32_t* table, long long head_off,
-                                          int first, int n, int lane, int j, int kq) {
+                                          int first, int n, int lane, int j, int kq, float* srow) {
     for (int c0 = 0; c0 < n; c0 += 64) {
         const int f = first + c0;
         const int nc = min(64, n - c0);
@@ -509,9 +527,10 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
             }
             w.tblv = blk;
         }
-        walk_tiles<D, KVT>(st, a, qv, nc, j, kq, [&](int i, long long& ko, long long* vo) {
-            return aligned_offsets<D, KVT>(a, w, f + i, j, kq, ko, vo);
-        });
+        walk_tiles<D, KVT, TRACK>(st, a, qv, nc, j, kq, srow,
+                                  [&](int i, long long& ko, long long* vo, int* pos) {
+                                      return aligned_offsets<D, KVT>(a, w, f + i, j, kq, ko, vo, pos);
+                                  });
     }
 }
 
@@ -522,7 +541,7 @@ __device__ __forceinline__ int sload(const int* p) { return __builtin_amdgcn_rea
 // register-resident 16-token tiles alone take 128 VGPRs per lane (one).  Two
 // tiles of loads in flight per wavefront at this occupancy keep ~32 MB of
 // reads outstanding, more than HBM latency x bandwidth.
-template <int D, int KVT, bool ALIGNED>
+template <int D, int KVT, bool ALIGNED, bool TRACK>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu((D == 128 && KVT == NYION_KV_F32) ? 1 : 2)))
 void decode_kernel(DecodeArgs a) {
@@ -616,6 +635,11 @@ void decode_kernel(DecodeArgs a) {
         st.m = -INFINITY;
         st.l = 0.f;
 
+        // TRACK: this lane's head's row of the score buffer (pad heads: none)
+        float* srow = nullptr;
+        if (TRACK && j < g_local)
+            srow = a.scores + ((long long)b * a.n_heads + head0 + j) * a.scores_stride;
+
         RowMap m;
         m.table = a.tables ? a.tables + (long long)b * a.table_stride : nullptr;
         m.block_stride = a.block_stride;
@@ -633,19 +657,22 @@ void decode_kernel(DecodeArgs a) {
             const int mt = e.main_tiles;
             const int me = min(wb, mt);
             if (wa < me)
-                walk_main<D, KVT>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa, me - wa,
-                                  lane, j, kq);
+                walk_main<D, KVT, TRACK>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa,
+                                         me - wa, lane, j, kq, srow);
             const int ga = max(wa, mt) - mt;
             const int gb = wb - mt;
-            walk_tiles<D, KVT>(st, a, qv, gb - ga, j, kq, [&](int i, long long& ko, long long* vo) {
-                return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (ga + i), e.n_glob, true, j, kq,
-                                              ko, vo);
-            });
+            walk_tiles<D, KVT, TRACK>(st, a, qv, gb - ga, j, kq, srow,
+                                      [&](int i, long long& ko, long long* vo, int* pos) {
+                                          return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (ga + i),
+                                                                        e.n_glob, true, j, kq, ko, vo,
+                                                                        pos);
+                                      });
         } else {
-            walk_tiles<D, KVT>(st, a, qv, wb - wa, j, kq, [&](int i, long long& ko, long long* vo) {
-                return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (wa + i), e.L, false, j, kq, ko,
-                                              vo);
-            });
+            walk_tiles<D, KVT, TRACK>(st, a, qv, wb - wa, j, kq, srow,
+                                      [&](int i, long long& ko, long long* vo, int* pos) {
+                                          return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (wa + i),
+                                                                        e.L, false, j, kq, ko, vo, pos);
+                                      });
         }
 
         // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
@@ -690,6 +717,11 @@ void decode_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; r++) {
                 const int hh = 4 * kq + r;
                 if (hh >= g_local) continue;
+                if (TRACK && whole && j == 0) {  // final (m, l) of the head: row end
+                    float* sr = a.scores + ((long long)b * a.n_heads + head0 + hh) * a.scores_stride;
+                    sr[a.scores_stride - 2] = mh[r];
+                    sr[a.scores_stride - 1] = lh[r];
+                }
                 if (whole) {
                     const float inv = 1.0f / lh[r];
                     float* o = a.out + ((long long)b * a.n_heads + head0 + hh) * D + DPL * j;
@@ -730,10 +762,33 @@ void decode_kernel(DecodeArgs a) {
             const int np = (seg0 + Tb - 1) / c - gf + 1;
             const long long slot0 = (long long)gf + s;
             merge_segment<D>(a.ws_acc + slot0 * 16 * D, a.ws_ml + slot0 * 16, np, g_local,
-                             a.out + ((long long)b * a.n_heads + head0) * D, threadIdx.x);
+                             a.out + ((long long)b * a.n_heads + head0) * D, threadIdx.x,
+                             TRACK ? a.scores + ((long long)b * a.n_heads + head0) * a.scores_stride
+                                   : nullptr,
+                             a.scores_stride);
             if (threadIdx.x == 0)
                 __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+}
+
+// Tracked decode, second pass: importance[b][t] += sum over q heads of the
+// normalised probability of position t (ops::attention_tracked,
+// ops.rs:303-368: p in f32, accumulated in f64), for every attended t.
+__global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    for (int b = blockIdx.y; b < a.batch; b += gridDim.y) {
+        const Extent e = lane_extent<true>(a, b);
+        const bool in_window = t >= e.lo && t <= e.hi;
+        const bool global = e.n_glob > 0 && t % a.global_stride == 0 && t / a.global_stride < e.n_glob;
+        if (!in_window && !global) continue;
+        double acc = 0.0;
+        const float* row = a.scores + (long long)b * a.n_heads * a.scores_stride;
+        for (int h = 0; h < a.n_heads; h++, row += a.scores_stride) {
+            const float m = row[a.scores_stride - 2], l = row[a.scores_stride - 1];
+            acc += (double)(__builtin_amdgcn_exp2f(row[t] - m) / l);
+        }
+        imp[(long long)b * imp_stride + t] += acc;
     }
 }
 
@@ -764,6 +819,7 @@ struct DecodePlan {
     int head_dim;
     int kvt;
     bool aligned;
+    bool track;
 };
 
 static size_t ws_layout(int slots, int segments, int head_dim, size_t* ml_off, size_t* ctr_off) {
@@ -821,6 +877,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     pl.head_dim = head_dim;
     pl.kvt = kvt;
     pl.aligned = aligned_path;
+    pl.track = false;
     pl.grid_bound = grid_for(chunk * per_seq, kMinWgTiles, kMaxGrid);
     // one sequence over at most one workgroup per segment: no partials
     if (batch == 1 && pl.grid_bound <= units) {
@@ -849,14 +906,14 @@ static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes) {
 }
 
 // Workgroups of one kernel instance resident on the whole device.
-template <int D, int KVT, bool AL>
+template <int D, int KVT, bool AL, bool TR>
 static int resident_capacity() {
     static int cap = 0;
     if (cap == 0) {
         int per_cu = 0, cus = 0, dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL>, 256, 0) !=
-                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL, TR>, 256,
+                                                         0) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
             (void)hipGetLastError();
             return 256;
@@ -866,11 +923,11 @@ static int resident_capacity() {
     return cap;
 }
 
-template <int D, int KVT, bool AL>
+template <int D, int KVT, bool AL, bool TR>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
     const int units = pl.a.n_kv_heads * pl.a.n_hg;
     const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
-    const int cap = resident_capacity<D, KVT, AL>();
+    const int cap = resident_capacity<D, KVT, AL, TR>();
     for (int b0 = 0; b0 < pl.batch; b0 += pl.chunk) {
         const int nb = pl.batch - b0 < pl.chunk ? pl.batch - b0 : pl.chunk;
         DecodeArgs a = pl.a;
@@ -883,19 +940,26 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
         if (a.q_pos) a.q_pos += b0;
         if (a.positions) a.positions += (long long)b0 * a.pos_stride;
         if (a.n_pos) a.n_pos += b0;
+        if (a.scores) a.scores += (long long)b0 * a.n_heads * a.scores_stride;
         int grid = grid_for((long long)nb * units * pl.tiles_max, wg_tiles, cap);
         if (grid > pl.grid_bound) grid = pl.grid_bound;
         if (pl.ws_bytes == 0 || (nb == 1 && grid <= units)) grid = units;  // whole segments
-        hipLaunchKernelGGL((decode_kernel<D, KVT, AL>), dim3(grid), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR>), dim3(grid), dim3(256), 0, stream, a);
     }
 }
 
 template <int D, int KVT>
 static void launch_dkt(const DecodePlan& pl, hipStream_t stream) {
-    if (pl.aligned)
-        launch_dk<D, KVT, true>(pl, stream);
-    else
-        launch_dk<D, KVT, false>(pl, stream);
+    if (pl.track) {
+        if (pl.aligned)
+            launch_dk<D, KVT, true, true>(pl, stream);
+        else
+            launch_dk<D, KVT, false, true>(pl, stream);
+    } else if (pl.aligned) {
+        launch_dk<D, KVT, true, false>(pl, stream);
+    } else {
+        launch_dk<D, KVT, false, false>(pl, stream);
+    }
 }
 
 static int launch_plan(const DecodePlan& pl, hipStream_t stream) {
@@ -948,8 +1012,8 @@ int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, i
     const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
     int cap = kMaxGrid;
     if (require_device() == NYION_OK)
-        cap = head_dim == 128 ? resident_capacity<128, NYION_KV_F32, true>()
-                              : resident_capacity<64, NYION_KV_F32, true>();
+        cap = head_dim == 128 ? resident_capacity<128, NYION_KV_F32, true, false>()
+                              : resident_capacity<64, NYION_KV_F32, true, false>();
     clear_error();
     const int grid = grid_for(tiles, wg_tiles, cap);
     return (int)(16 * ((tiles + grid - 1) / grid));
@@ -985,13 +1049,18 @@ int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion
     return check_launch("workspace init");
 }
 
-int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
-                                 const int32_t* block_tables, int max_blocks_per_seq,
-                                 const int32_t* ctx_lens, const int32_t* q_pos, int batch,
-                                 int n_heads, int n_kv_heads, int head_dim, int block_tokens,
-                                 int num_blocks, int kv_dtype, int window, int global_stride,
-                                 int max_ctx, float scale, float* d_out, void* d_workspace,
-                                 size_t workspace_bytes, nyion_stream_t stream) {
+}  // extern "C"
+
+// Shared body of the paged decode entry points; scores/imp non-null selects
+// the tracked form.
+static int paged_decode_common(const float* d_q, const void* k_pool, const void* v_pool,
+                               const int32_t* block_tables, int max_blocks_per_seq,
+                               const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                               int n_heads, int n_kv_heads, int head_dim, int block_tokens,
+                               int num_blocks, int kv_dtype, int window, int global_stride,
+                               int max_ctx, float scale, float* d_out, void* d_workspace,
+                               size_t workspace_bytes, float* d_scores, int scores_stride,
+                               double* d_importance, int importance_stride, hipStream_t stream) {
     clear_error();
     int rc;
     if ((rc = require_device()) != NYION_OK) return rc;
@@ -1009,6 +1078,18 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
         return set_error(NYION_ERR_INVALID,
                          "paged decode: max_ctx %d must be in [1, max_blocks_per_seq*block_tokens]",
                          max_ctx);
+    const bool track = d_scores != nullptr;
+    if (track) {
+        if (!d_importance)
+            return set_error(NYION_ERR_INVALID, "tracked decode: null importance");
+        if ((long long)scores_stride < (long long)max_ctx + 2 || importance_stride < max_ctx)
+            return set_error(NYION_ERR_INVALID,
+                             "tracked decode: scores_stride %d must be >= max_ctx + 2 and "
+                             "importance_stride %d >= max_ctx (%d)",
+                             scores_stride, importance_stride, max_ctx);
+        if (!aligned(d_scores, 4) || !aligned(d_importance, 8))
+            return set_error(NYION_ERR_INVALID, "tracked decode: buffer alignment");
+    }
     const bool aligned_path = block_tokens >= 16;
     DecodePlan pl;
     if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype,
@@ -1016,6 +1097,7 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
                           aligned_path, scale)) != NYION_OK)
         return rc;
     if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
+    pl.track = track;
     DecodeArgs& a = pl.a;
     const long long row = row_elems(head_dim, kv_dtype);
     a.q = d_q;
@@ -1034,7 +1116,49 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
     a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
     a.window = window;
     a.global_stride = global_stride;
-    return launch_plan(pl, (hipStream_t)stream);
+    a.scores = d_scores;
+    a.scores_stride = scores_stride;
+    if ((rc = launch_plan(pl, stream)) != NYION_OK || !track) return rc;
+    DecodeArgs ia = a;
+    ia.batch = batch;
+    const unsigned gy = batch < 65535 ? (unsigned)batch : 65535u;
+    hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((max_ctx + 255) / 256), gy), dim3(256), 0,
+                       stream, ia, d_importance, importance_stride);
+    return check_launch("decode importance");
+}
+
+extern "C" {
+
+int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_tables, int max_blocks_per_seq,
+                                 const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                 int n_heads, int n_kv_heads, int head_dim, int block_tokens,
+                                 int num_blocks, int kv_dtype, int window, int global_stride,
+                                 int max_ctx, float scale, float* d_out, void* d_workspace,
+                                 size_t workspace_bytes, nyion_stream_t stream) {
+    return paged_decode_common(d_q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                               q_pos, batch, n_heads, n_kv_heads, head_dim, block_tokens,
+                               num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
+                               d_workspace, workspace_bytes, nullptr, 0, nullptr, 0,
+                               (hipStream_t)stream);
+}
+
+int nyion_paged_decode_attention_tracked(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, double* d_importance,
+    int importance_stride, nyion_stream_t stream) {
+    if (!d_scores) {
+        clear_error();
+        return set_error(NYION_ERR_INVALID, "tracked decode: null scores buffer");
+    }
+    return paged_decode_common(d_q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                               q_pos, batch, n_heads, n_kv_heads, head_dim, block_tokens,
+                               num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
+                               d_workspace, workspace_bytes, d_scores, scores_stride, d_importance,
+                               importance_stride, (hipStream_t)stream);
 }
 
 size_t nyion_paged_decode_positions_workspace_size(int batch, int n_heads, int n_kv_heads,

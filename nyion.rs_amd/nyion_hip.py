@@ -55,6 +55,9 @@ SIGNATURES = {
     "nyion_paged_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "nyion_paged_decode_attention": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32,
                                            i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
+    "nyion_paged_decode_attention_tracked": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32,
+                                                   i32, i32, i32, i32, i32, i32, f32, vp, vp, sz,
+                                                   vp, i32, vp, i32, vp]),
     "nyion_paged_decode_positions_workspace_size": (sz, [i32, i32, i32, i32, i32]),
     "nyion_paged_decode_attention_positions": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
                                                      i32, i32, i32, i32, i32, f32, vp, vp, sz,
@@ -183,6 +186,32 @@ def paged_decode(q, k_pool, v_pool, block_tables, ctx_lens, out, n_heads, n_kv_h
         ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens, num_blocks, kv_dtype, window,
         global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes, stream_handle(stream))
     check(rc, "nyion_paged_decode_attention")
+    return workspace
+
+
+def paged_decode_tracked(q, k_pool, v_pool, block_tables, ctx_lens, out, importance, n_heads,
+                         n_kv_heads, head_dim, block_tokens, kv_dtype=KV_F32, window=0,
+                         global_stride=0, max_ctx=None, q_pos=None, scale=0.0, workspace=None,
+                         scores=None, stream=None):
+    """paged_decode plus importance [B][>= max_ctx] f64 (accumulated), the tracked
+    form of the executor's Full decode call.  scores: optional f32 scratch
+    [B][Hq][>= max_ctx + 2]."""
+    torch = _torch()
+    B = q.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if scores is None:
+        scores = torch.empty((B, n_heads, max_ctx + 2), dtype=torch.float32, device=q.device)
+    rc = load().nyion_paged_decode_attention_tracked(
+        ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1], ptr(ctx_lens),
+        ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens, k_pool.shape[0], kv_dtype,
+        window, global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes, ptr(scores),
+        scores.shape[-1], ptr(importance), importance.shape[-1], stream_handle(stream))
+    check(rc, "nyion_paged_decode_attention_tracked")
     return workspace
 
 

@@ -117,6 +117,70 @@ def test_paged_q_pos(gpu):
     assert_close(run_paged(gpu, pb, q_pos=q_pos), W.reference_decode(pb, q_pos=q_pos), "q_pos")
 
 
+# ---------------------------------------------------------------- tracked (A2)
+
+def run_tracked(gpu, pb, q_pos=None, window=0, global_stride=0, init=None, stride_pad=5):
+    q = to_dev(pb.q)
+    kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    qp = None if q_pos is None else to_dev(np.asarray(q_pos, np.int32))
+    out = torch.full_like(q, float("nan"))
+    max_ctx = int(pb.ctx_lens.max())
+    imp0 = np.zeros((pb.batch, max_ctx + stride_pad)) if init is None else init
+    imp = torch.from_numpy(imp0.copy()).cuda()
+    gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out, imp, pb.n_heads, pb.n_kv_heads,
+                             pb.head_dim, pb.block_tokens, kv_dtype=pb.kv_dtype, window=window,
+                             global_stride=global_stride, q_pos=qp)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), imp.cpu().numpy()
+
+
+def test_tracked_importance_matches_oracle(gpu):
+    """ops::attention_tracked: outputs and importance[t] = sum_h p_h[t] (f64),
+    accumulated onto the caller's array, untouched past valid_end."""
+    pb = W.paged_batch([300, 4096, 1, 2000], seed=7)
+    q_pos = [250, 4095, 0, 1500]
+    rng = np.random.default_rng(3)
+    init = rng.random((pb.batch, 4096 + 3))
+    out, imp = run_tracked(gpu, pb, q_pos=q_pos, init=init, stride_pad=3)
+    assert_close(out, W.reference_decode(pb, q_pos=q_pos), "tracked out")
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        ref_out, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, q_pos[b],
+                                            pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                                            importance=True)
+        got = imp[b] - init[b]
+        ve = min(q_pos[b], L - 1)
+        assert np.max(np.abs(got[:L] - ref_imp)) <= 1e-4 * pb.n_heads, f"importance b={b}"
+        assert np.all(got[ve + 1:] == 0.0), f"importance past valid_end b={b}"
+        assert abs(got.sum() - pb.n_heads) <= 1e-3, f"importance sum b={b}"
+
+
+def test_tracked_split_and_window(gpu):
+    """Tracked form with split-K partials (small partitions), and with a
+    window: probabilities of the attended set sum to n_heads per sequence."""
+    pb = W.paged_batch([5000, 700], seed=8)
+    try:
+        gpu.set_partition_tokens(64)
+        out, imp = run_tracked(gpu, pb)
+    finally:
+        gpu.set_partition_tokens(0)
+    assert_close(out, W.reference_decode(pb), "tracked split")
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, L - 1, pb.n_heads,
+                                      pb.n_kv_heads, pb.head_dim, importance=True)
+        assert np.max(np.abs(imp[b][:L] - ref_imp)) <= 1e-4 * pb.n_heads
+    out, imp = run_tracked(gpu, pb, window=512, global_stride=64)
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        pos = oracle.sparse_positions(L, L - 1, 512, 64)
+        mask = np.zeros(imp.shape[1], bool)
+        mask[pos] = True
+        assert abs(imp[b][mask].sum() - pb.n_heads) <= 1e-3
+        assert np.all(imp[b][~mask] == 0.0)
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd", [(8, 8, 64), (16, 8, 64), (32, 8, 128), (64, 4, 64),
                                              (32, 1, 128), (40, 2, 64)])
 def test_paged_head_shapes(gpu, n_heads, n_kv, hd):
