@@ -159,6 +159,74 @@ int nyion_paged_decode_attention_positions(
     int num_blocks, int kv_dtype, float scale, float* d_out, void* d_workspace,
     size_t workspace_bytes, nyion_stream_t stream);
 
+/* ------------------------------------------ per-layer ring and Fugu policy */
+
+/* Sliding-window KV rings of the GPU decode path: PerLayerGpuState
+ * (swamp-engine/src/scheduler.rs:36-178).  One ring of `window` slots per
+ * layer, [n_kv_heads][window][head_dim] f32 on the device, zero-filled.
+ *   upload_kv (upload_kv_async, scheduler.rs:103-117): host k, v
+ *     [n_kv_heads][head_dim] of token `pos` -> slot pos % window;
+ *   attention (execute_attention_async + sync, scheduler.rs:119-178): host q
+ *     [n_heads][head_dim] -> host out, the Attention node over
+ *     min(seq_len, window) slots; returns when out is written.
+ * Unlike the reference (one f16 ring shared by every layer), each layer has
+ * its own f32 ring.  Calls on one state are not thread-safe. */
+void* nyion_layer_state_create(int window, int n_heads, int n_kv_heads, int head_dim,
+                               int n_layers);
+int   nyion_layer_state_upload_kv(void* state, int layer, const float* h_k, const float* h_v,
+                                  int pos);
+int   nyion_layer_state_attention(void* state, int layer, const float* h_q, float* h_out,
+                                  int pos, int seq_len);
+int   nyion_layer_state_sync(void* state);
+void  nyion_layer_state_destroy(void* state);
+
+/* FuguOrchestrator::decide_attention (swamp-engine/src/fugu.rs:129-170):
+ * the attention variant of one step (host function, no device needed).
+ * Fields are those of SystemSnapshot (fugu.rs:64-73) and FuguOrchestrator
+ * (fugu.rs:79-117) that the decision reads. */
+typedef struct nyion_system_snapshot {
+    int64_t seq_len;
+    double  dspark_accept_rate;
+    int32_t is_prefill;
+    int32_t predictive_throttle;
+} nyion_system_snapshot;
+typedef struct nyion_fugu_config {
+    int64_t sparse_attention_threshold; /* 512 */
+    int32_t sparse_window;              /* 256 */
+    int32_t sparse_random_samples;      /* 32 */
+    int32_t n_heads;
+    int32_t head_dim;
+} nyion_fugu_config;
+enum nyion_attention_kind {
+    NYION_ATTN_FULL = 0,          /* attention_tracked: nyion_paged_decode_attention_tracked */
+    NYION_ATTN_SPARSE = 1,        /* attention_sparse: window, global stride 64 */
+    NYION_ATTN_SPARSE_DSPARK = 2  /* attention_fugu: nyion_fugu_positions + _positions decode */
+};
+typedef struct nyion_attention_strategy {
+    int32_t kind;
+    int32_t window;
+    int32_t num_random;
+    int32_t sentinel_stride;
+    int32_t num_dspark;
+    int32_t _pad;
+} nyion_attention_strategy;
+/* FuguOrchestrator::new defaults (fugu.rs:103-117). */
+int nyion_fugu_config_default(int n_heads, int head_dim, nyion_fugu_config* cfg);
+int nyion_fugu_decide_attention(const nyion_system_snapshot* state, const nyion_fugu_config* cfg,
+                                nyion_attention_strategy* out);
+
+/* The attention_fugu position set (ops.rs:463-484), built on the device for
+ * nyion_paged_decode_attention_positions: per sequence, sentinels
+ * sentinel_stride*g (g < min(window_start/sentinel_stride, 128)), the window
+ * [window_start, valid_end], then each DSPark position <= valid_end not
+ * already present, in input order.  d_dspark [batch][dspark_stride] int32
+ * (n_dspark used per row); d_positions [batch][max_positions], with
+ * max_positions >= 128 + window + 1 + n_dspark; d_n_positions [batch]. */
+int nyion_fugu_positions(const int32_t* d_ctx_lens, const int32_t* d_q_pos, int batch, int window,
+                         int sentinel_stride, const int32_t* d_dspark, int n_dspark,
+                         int dspark_stride, int32_t* d_positions, int max_positions,
+                         int32_t* d_n_positions, nyion_stream_t stream);
+
 /* Zero-fills a decode workspace on `stream` (a fill kernel, so it may be
  * recorded into a HIP graph).  Needed once before first use. */
 int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion_stream_t stream);

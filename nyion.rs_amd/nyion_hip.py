@@ -42,6 +42,25 @@ class Allocation(C.Structure):
 
 vp, i32, u32, i64, f32, sz = C.c_void_p, C.c_int, C.c_uint32, C.c_int64, C.c_float, C.c_size_t
 
+
+class SystemSnapshot(C.Structure):
+    _fields_ = [("seq_len", C.c_int64), ("dspark_accept_rate", C.c_double),
+                ("is_prefill", C.c_int32), ("predictive_throttle", C.c_int32)]
+
+
+class FuguConfig(C.Structure):
+    _fields_ = [("sparse_attention_threshold", C.c_int64), ("sparse_window", C.c_int32),
+                ("sparse_random_samples", C.c_int32), ("n_heads", C.c_int32),
+                ("head_dim", C.c_int32)]
+
+
+class AttentionStrategy(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("window", C.c_int32), ("num_random", C.c_int32),
+                ("sentinel_stride", C.c_int32), ("num_dspark", C.c_int32), ("_pad", C.c_int32)]
+
+
+ATTN_FULL, ATTN_SPARSE, ATTN_SPARSE_DSPARK = 0, 1, 2
+
 # name -> (restype, argtypes); the full list of symbols the header declares.
 SIGNATURES = {
     "nyion_last_error": (C.c_char_p, []),
@@ -63,6 +82,15 @@ SIGNATURES = {
                                                      i32, i32, i32, i32, i32, f32, vp, vp, sz,
                                                      vp]),
     "nyion_decode_workspace_init": (i32, [vp, sz, vp]),
+    "nyion_layer_state_create": (vp, [i32, i32, i32, i32, i32]),
+    "nyion_layer_state_upload_kv": (i32, [vp, i32, vp, vp, i32]),
+    "nyion_layer_state_attention": (i32, [vp, i32, vp, vp, i32, i32]),
+    "nyion_layer_state_sync": (i32, [vp]),
+    "nyion_layer_state_destroy": (None, [vp]),
+    "nyion_fugu_config_default": (i32, [i32, i32, C.POINTER(FuguConfig)]),
+    "nyion_fugu_decide_attention": (i32, [C.POINTER(SystemSnapshot), C.POINTER(FuguConfig),
+                                          C.POINTER(AttentionStrategy)]),
+    "nyion_fugu_positions": (i32, [vp, vp, i32, i32, i32, vp, i32, i32, vp, i32, vp, vp]),
     "nyion_set_decode_partition_tokens": (i32, [i32]),
     "nyion_get_decode_partition_tokens": (i32, [i32, i32, i32, i32]),
     "nyion_prefill_attention_bf16": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp, vp,
@@ -232,6 +260,65 @@ def paged_decode_positions(q, k_pool, v_pool, block_tables, positions, n_positio
         stream_handle(stream))
     check(rc, "nyion_paged_decode_attention_positions")
     return workspace
+
+
+def fugu_decide_attention(seq_len, n_heads, head_dim, is_prefill=False, predictive_throttle=False,
+                          dspark_accept_rate=0.0, cfg=None) -> AttentionStrategy:
+    """FuguOrchestrator::decide_attention (host; no device needed)."""
+    if cfg is None:
+        cfg = FuguConfig()
+        check(load().nyion_fugu_config_default(n_heads, head_dim, C.byref(cfg)), "fugu config")
+    snap = SystemSnapshot(seq_len, dspark_accept_rate, int(is_prefill), int(predictive_throttle))
+    out = AttentionStrategy()
+    check(load().nyion_fugu_decide_attention(C.byref(snap), C.byref(cfg), C.byref(out)),
+          "fugu decide")
+    return out
+
+
+def fugu_positions(ctx_lens, window, sentinel_stride, dspark, positions, n_positions, q_pos=None,
+                   stream=None):
+    """Device A4 position sets: dspark [B][n] int32 -> positions [B][max], n_positions [B]."""
+    B = ctx_lens.shape[0]
+    nd = 0 if dspark is None else dspark.shape[1]
+    rc = load().nyion_fugu_positions(ptr(ctx_lens), ptr(q_pos), B, window, sentinel_stride,
+                                     ptr(dspark), nd, nd, ptr(positions), positions.shape[1],
+                                     ptr(n_positions), stream_handle(stream))
+    check(rc, "nyion_fugu_positions")
+
+
+class LayerState:
+    """PerLayerGpuState: per-layer sliding-window rings on the device, host q/k/v/out."""
+
+    def __init__(self, window, n_heads, n_kv_heads, head_dim, n_layers):
+        self.h = load().nyion_layer_state_create(window, n_heads, n_kv_heads, head_dim, n_layers)
+        if not self.h:
+            raise NyionError(-1, last_error())
+
+    def upload_kv(self, layer, k, v, pos):
+        import numpy as np
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        check(load().nyion_layer_state_upload_kv(self.h, layer, k.ctypes.data, v.ctypes.data, pos),
+              "layer_state_upload_kv")
+
+    def attention(self, layer, q, pos, seq_len):
+        import numpy as np
+        q = np.ascontiguousarray(q, np.float32)
+        out = np.empty_like(q)
+        check(load().nyion_layer_state_attention(self.h, layer, q.ctypes.data, out.ctypes.data,
+                                                 pos, seq_len), "layer_state_attention")
+        return out
+
+    def close(self):
+        if self.h:
+            load().nyion_layer_state_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def set_partition_tokens(tokens: int) -> None:
