@@ -131,25 +131,23 @@ __device__ __forceinline__ Extent seq_extent(const DecodeArgs& a, int len, int q
     return e;
 }
 
+// The per-sequence values an extent needs: (ctx_len, q_pos), or the list
+// length in MODE_LIST (as len).
+__device__ __forceinline__ int2 seq_values(const DecodeArgs& a, int b) {
+    if (a.mode == MODE_LIST) return int2{a.n_pos[b], 0};
+    const int len = a.ctx_lens ? a.ctx_lens[b] : a.uniform_len;
+    return int2{len, a.q_pos ? a.q_pos[b] : len - 1};
+}
+
+template <bool ALIGNED>
+__device__ __forceinline__ Extent extent_of(const DecodeArgs& a, int2 v) {
+    return a.mode == MODE_LIST ? seq_extent<ALIGNED>(a, 0, 0, v.x) : seq_extent<ALIGNED>(a, v.x, v.y, 0);
+}
+
 // Extent of sequence b as seen by one thread (no uniformity assumed).
 template <bool ALIGNED>
 __device__ __forceinline__ Extent lane_extent(const DecodeArgs& a, int b) {
-    if (a.mode == MODE_LIST) return seq_extent<ALIGNED>(a, 0, 0, a.n_pos[b]);
-    const int len = a.ctx_lens ? a.ctx_lens[b] : a.uniform_len;
-    const int qp = a.q_pos ? a.q_pos[b] : len - 1;
-    return seq_extent<ALIGNED>(a, len, qp, 0);
-}
-
-// Extent of a wave-uniform sequence b: the loaded values are moved to scalar
-// registers so that everything derived from them (tile loop bounds, masks)
-// branches uniformly.
-template <bool ALIGNED>
-__device__ __forceinline__ Extent uniform_extent(const DecodeArgs& a, int b) {
-    if (a.mode == MODE_LIST)
-        return seq_extent<ALIGNED>(a, 0, 0, __builtin_amdgcn_readfirstlane(a.n_pos[b]));
-    const int len = a.ctx_lens ? __builtin_amdgcn_readfirstlane(a.ctx_lens[b]) : a.uniform_len;
-    const int qp = a.q_pos ? __builtin_amdgcn_readfirstlane(a.q_pos[b]) : len - 1;
-    return seq_extent<ALIGNED>(a, len, qp, 0);
+    return extent_of<ALIGNED>(a, seq_values(a, b));
 }
 
 // Virtual index -> position, gather path (and the globals of the aligned path).
@@ -435,67 +433,111 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
     }
 }
 
+// Online log-sum-exp merge state of one (head, 4-dim quad).
+struct MergeAcc {
+    float m, l, o[4];
+};
+
+__device__ __forceinline__ void merge_into(MergeAcc& x, float m, float l, const float* o) {
+    const float mn = fmaxf(x.m, m);
+    if (mn == -INFINITY) return;  // nothing attended on either side
+    const float sx = x.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x.m - mn);
+    const float sy = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+    x.l = __builtin_fmaf(l, sy, x.l * sx);
+#pragma unroll
+    for (int i = 0; i < 4; i++) x.o[i] = __builtin_fmaf(o[i], sy, x.o[i] * sx);
+    x.m = mn;
+}
+
 // Log-sum-exp merge of the np partials of one segment by the whole
-// workgroup: one thread per (head, 4-dim quad); partial p of head hh sits at
-// acc0 + (p*16 + hh)*D and ml0[p*16 + hh].  The partials come from other
-// workgroups, so they are read with device-coherent loads, 16 partials'
-// worth (their m, l and O quads) issued before any is used; chunks combine
-// online.
+// workgroup.  Partial p of head hh sits at acc0 + (p*16 + hh)*D and
+// ml0[p*16 + hh].  A thread owns one (head, 4-dim quad) item; when there are
+// fewer items than threads, R replicas of each item take partials
+// r, r+R, ... and combine through LDS, so up to 16*R partials need one
+// round of loads.  The partials come from other workgroups, so they are read
+// with device-coherent loads, 16 partials' worth (m, l and O quads) issued
+// before any is used.  `lds` holds 6 floats per thread; the function begins
+// and ends with a barrier.
 template <int D>
 __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int g_local, float* out,
-                              int tid, float* score_rows, int scores_stride) {
+                              int tid, float* score_rows, int scores_stride, float* lds) {
     constexpr int QPH = D / 4;  // quads per head
     constexpr int CH = 16;      // partials per batch of loads
-    for (int item = tid; item < g_local * QPH; item += 256) {
+    const int items = g_local * QPH;
+    const int R = items >= 256 ? 1 : 256 / items;
+    const int nthr = items >= 256 ? 256 : R * items;
+    const int r = tid / (items >= 256 ? 256 : items);
+    __syncthreads();
+    for (int base = 0; base < items; base += 256) {
+        const int item = items >= 256 ? base + tid : tid % items;
+        const bool active = tid < nthr && item < items;
+        MergeAcc x{-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f}};
         const int hh = item / QPH;
         const int dq = item - hh * QPH;
-        float M = -INFINITY, L = 0.f;
-        float o[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int p0 = 0; p0 < np; p0 += CH) {
-            uint64_t mlv[CH], a01[CH], a23[CH];
+        if (active) {
+            for (int p0 = r; p0 < np; p0 += CH * R) {
+                uint64_t mlv[CH], a01[CH], a23[CH];
 #pragma unroll
-            for (int q = 0; q < CH; q++) {
-                if (p0 + q < np) {
-                    const long long e = (long long)(p0 + q) * 16 + hh;
-                    const uint64_t* src = (const uint64_t*)(acc0 + e * D + 4 * dq);
-                    mlv[q] = __hip_atomic_load((const uint64_t*)(ml0 + e), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                    a01[q] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    a23[q] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    mlv[q] = (uint64_t)__float_as_uint(-INFINITY);  // m = -inf, l = 0
-                    a01[q] = a23[q] = 0;
+                for (int q = 0; q < CH; q++) {
+                    const int pq = p0 + q * R;
+                    if (pq < np) {
+                        const long long e = (long long)pq * 16 + hh;
+                        const uint64_t* src = (const uint64_t*)(acc0 + e * D + 4 * dq);
+                        mlv[q] = __hip_atomic_load((const uint64_t*)(ml0 + e), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                        a01[q] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        a23[q] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        mlv[q] = (uint64_t)__float_as_uint(-INFINITY);  // m = -inf, l = 0
+                        a01[q] = a23[q] = 0;
+                    }
                 }
+                float mc = -INFINITY;
+#pragma unroll
+                for (int q = 0; q < CH; q++) mc = fmaxf(mc, __uint_as_float((uint32_t)mlv[q]));
+                MergeAcc c{mc, 0.f, {0.f, 0.f, 0.f, 0.f}};
+                if (mc != -INFINITY) {
+#pragma unroll
+                    for (int q = 0; q < CH; q++) {
+                        const float mq = __uint_as_float((uint32_t)mlv[q]);
+                        const float w = mq == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mq - mc);
+                        c.l = __builtin_fmaf(w, __uint_as_float((uint32_t)(mlv[q] >> 32)), c.l);
+                        c.o[0] = __builtin_fmaf(w, __uint_as_float((uint32_t)a01[q]), c.o[0]);
+                        c.o[1] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a01[q] >> 32)), c.o[1]);
+                        c.o[2] = __builtin_fmaf(w, __uint_as_float((uint32_t)a23[q]), c.o[2]);
+                        c.o[3] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a23[q] >> 32)), c.o[3]);
+                    }
+                }
+                merge_into(x, c.m, c.l, c.o);
             }
-            float mc = -INFINITY;
-#pragma unroll
-            for (int q = 0; q < CH; q++) mc = fmaxf(mc, __uint_as_float((uint32_t)mlv[q]));
-            const float mn = fmaxf(M, mc);
-            if (mn == -INFINITY) continue;  // nothing attended so far
-            const float sc = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
-            L *= sc;
-#pragma unroll
-            for (int x = 0; x < 4; x++) o[x] *= sc;
-#pragma unroll
-            for (int q = 0; q < CH; q++) {
-                const float mq = __uint_as_float((uint32_t)mlv[q]);
-                const float w = mq == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mq - mn);
-                L = __builtin_fmaf(w, __uint_as_float((uint32_t)(mlv[q] >> 32)), L);
-                o[0] = __builtin_fmaf(w, __uint_as_float((uint32_t)a01[q]), o[0]);
-                o[1] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a01[q] >> 32)), o[1]);
-                o[2] = __builtin_fmaf(w, __uint_as_float((uint32_t)a23[q]), o[2]);
-                o[3] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a23[q] >> 32)), o[3]);
-            }
-            M = mn;
         }
-        const float inv = 1.0f / L;
-        *(float4*)(out + hh * D + 4 * dq) = float4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
-        if (score_rows && dq == 0) {  // final (m, l) of the head: end of its score row
-            float* sr = score_rows + (long long)hh * scores_stride;
-            sr[scores_stride - 2] = M;
-            sr[scores_stride - 1] = L;
+        if (R > 1) {  // replicas -> replica 0 through LDS
+            if (active) {
+                float* d = lds + 6 * tid;
+                d[0] = x.m;
+                d[1] = x.l;
+#pragma unroll
+                for (int i = 0; i < 4; i++) d[2 + i] = x.o[i];
+            }
+            __syncthreads();
+            if (active && r == 0)
+                for (int k = 1; k < R; k++) {
+                    const float* d = lds + 6 * (k * items + item);
+                    merge_into(x, d[0], d[1], d + 2);
+                }
+        }
+        if (active && r == 0) {
+            const float inv = 1.0f / x.l;
+            *(float4*)(out + hh * D + 4 * dq) =
+                float4{x.o[0] * inv, x.o[1] * inv, x.o[2] * inv, x.o[3] * inv};
+            if (score_rows && dq == 0) {  // final (m, l) of the head: end of its score row
+                float* sr = score_rows + (long long)hh * scores_stride;
+                sr[scores_stride - 2] = x.m;
+                sr[scores_stride - 1] = x.l;
+            }
         }
     }
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------- kernel
@@ -551,6 +593,7 @@ void decode_kernel(DecodeArgs a) {
     __shared__ float sm_m[4][16];
     __shared__ float sm_l[4][16];
     __shared__ int sm_pref[kMaxLaunchBatch + 1];  // tiles per segment, exclusive prefix
+    __shared__ int2 sm_seq[kMaxLaunchBatch];       // (ctx_len, q_pos) or (list length, 0)
     __shared__ int sm_wsum[4];
     __shared__ int sm_last;
 
@@ -565,7 +608,12 @@ void decode_kernel(DecodeArgs a) {
     if (threadIdx.x == 0) sm_pref[0] = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 256) {
         const int b = c0 + threadIdx.x;
-        int t = b < a.batch ? lane_extent<ALIGNED>(a, b).tiles : 0;
+        int t = 0;
+        if (b < a.batch) {
+            const int2 v = seq_values(a, b);
+            sm_seq[b] = v;
+            t = extent_of<ALIGNED>(a, v).tiles;
+        }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int y = __shfl_up(t, o);
@@ -618,7 +666,9 @@ void decode_kernel(DecodeArgs a) {
         const int hg = u - kvh * a.n_hg;
         const int g_local = min(16, a.group - hg * 16);
         const int head0 = kvh * a.group + hg * 16;
-        const Extent e = uniform_extent<ALIGNED>(a, b);
+        // the sequence's values from LDS, in scalar registers, so that tile
+        // loop bounds and masks derived from them branch uniformly
+        const Extent e = extent_of<ALIGNED>(a, int2{sload(&sm_seq[b].x), sload(&sm_seq[b].y)});
 
         // Q operand (B of the QK product): head j, dims by qk_dim.
         float qv[NC];
@@ -765,7 +815,7 @@ void decode_kernel(DecodeArgs a) {
                              a.out + ((long long)b * a.n_heads + head0) * D, threadIdx.x,
                              TRACK ? a.scores + ((long long)b * a.n_heads + head0) * a.scores_stride
                                    : nullptr,
-                             a.scores_stride);
+                             a.scores_stride, (float*)&sm_acc[0][0][0]);
             if (threadIdx.x == 0)
                 __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

@@ -217,6 +217,33 @@ def paged_decode(q, k_pool, v_pool, block_tables, ctx_lens, out, n_heads, n_kv_h
     return workspace
 
 
+def prepare_paged_decode(q, k_pool, v_pool, block_tables, ctx_lens, out, n_heads, n_kv_heads,
+                         head_dim, block_tokens, max_ctx, kv_dtype=KV_F32, window=0,
+                         global_stride=0, q_pos=None, scale=0.0, workspace=None, stream=None):
+    """paged_decode with every argument resolved once: returns a no-argument
+    callable that only crosses the C ABI (what a compiled caller pays), for
+    loops that launch many decode calls."""
+    B = q.shape[0]
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    fn = load().nyion_paged_decode_attention
+    args = (ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1],
+            ptr(ctx_lens), ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens,
+            k_pool.shape[0], kv_dtype, window, global_stride, max_ctx, scale, ptr(out),
+            ptr(workspace), ws_bytes, stream_handle(stream))
+    keep = (q, k_pool, v_pool, block_tables, ctx_lens, out, q_pos, workspace)
+
+    def call():
+        rc = fn(*args)
+        if rc != 0:
+            check(rc, "nyion_paged_decode_attention")
+
+    call.keep = keep
+    return call
+
+
 def paged_decode_tracked(q, k_pool, v_pool, block_tables, ctx_lens, out, importance, n_heads,
                          n_kv_heads, head_dim, block_tokens, kv_dtype=KV_F32, window=0,
                          global_stride=0, max_ctx=None, q_pos=None, scale=0.0, workspace=None,
