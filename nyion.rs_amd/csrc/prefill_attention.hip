@@ -92,9 +92,12 @@ __device__ __forceinline__ int vt_pos(int w) {
     return (w & 3) | (((w >> 3) & 1) << 2) | (((w >> 2) & 1) << 3);
 }
 
-__device__ __forceinline__ uint32_t bf16_to_f16_bits(uint32_t b) {
-    const _Float16 h = (_Float16)__uint_as_float(b << 16);
-    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+
+// Two f32 -> one word of two fp16 (lo in the low half), round to nearest
+// even; one v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, halfx2{(_Float16)lo, (_Float16)hi});
 }
 
 // One tile's K and V in registers between its global loads and its LDS
@@ -108,28 +111,45 @@ struct TileStage {
     u32x4 v1[VUNITS];
 };
 
+// Loads of tile kt.  Offsets are 32-bit element offsets from the tile's
+// first token (the host keeps n * n_kv_heads * head_dim below 2^31), so a
+// full tile costs one per-thread base plus constant steps; only a tile
+// that reaches past n clamps or zeroes rows.
 template <int D>
 __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kbase,
-                                           const uint16_t* vbase, long long tok_stride, int n,
-                                           int kt, int tid) {
+                                           const uint16_t* vbase, int tok_stride, int n, int kt,
+                                           int tid) {
     constexpr int CPR = D / 8;
+    const uint16_t* kp = kbase + (long long)kt * tok_stride;
+    const uint16_t* vp = vbase + (long long)kt * tok_stride;
+    const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);            // chunk u adds u*256/CPR keys
+    const int v_off = 2 * (tid % (BN / 2)) * tok_stride + 8 * (tid / (BN / 2));  // unit u adds 64 dims
+    if (kt + BN <= n) {
+#pragma unroll
+        for (int u = 0; u < TileStage<D>::KLOADS; u++)
+            st.k[u] = *(const u32x4*)(kp + k_off + u * (256 / CPR) * tok_stride);
+#pragma unroll
+        for (int u = 0; u < TileStage<D>::VUNITS; u++) {
+            st.v0[u] = *(const u32x4*)(vp + v_off + 64 * u);
+            st.v1[u] = *(const u32x4*)(vp + v_off + 64 * u + tok_stride);
+        }
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < TileStage<D>::KLOADS; u++) {
-        const int id = tid + 256 * u;
-        const int t = min(kt + id / CPR, n - 1);  // keys past n: finite values, masked
-        st.k[u] = *(const u32x4*)(kbase + t * tok_stride + 8 * (id % CPR));
+        const int key = tid / CPR + u * (256 / CPR);
+        const int t = min(kt + key, n - 1);  // keys past n: finite values, masked
+        st.k[u] = *(const u32x4*)(kbase + (long long)t * tok_stride + 8 * (tid % CPR));
     }
 #pragma unroll
     for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-        const int id = tid + 256 * u;
-        const int t = kt + 2 * (id % (BN / 2));
-        const int dc = id / (BN / 2);
-        st.v0[u] = t < n ? *(const u32x4*)(vbase + t * tok_stride + 8 * dc) : u32x4{0, 0, 0, 0};
-        st.v1[u] = t + 1 < n ? *(const u32x4*)(vbase + (t + 1) * tok_stride + 8 * dc)
+        const int t = kt + 2 * (tid % (BN / 2));
+        const int dc = tid / (BN / 2) + u * (256 / (BN / 2));
+        st.v0[u] = t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + 8 * dc) : u32x4{0, 0, 0, 0};
+        st.v1[u] = t + 1 < n ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + 8 * dc)
                              : u32x4{0, 0, 0, 0};
     }
 }
-
 
 template <int D>
 __device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned char* base, int tid) {
@@ -150,10 +170,12 @@ __device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned cha
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             // dim 8dc+e: low half from key, high half from key+1
+            // bf16 -> f32 is a 16-bit shift (or mask for the high half); bf16
+            // values in the fp16 range convert to fp16 exactly
             const uint32_t x0 = st.v0[u][e >> 1], x1 = st.v1[u][e >> 1];
-            const uint32_t lo = bf16_to_f16_bits((e & 1) ? (x0 >> 16) : (x0 & 0xffffu));
-            const uint32_t hi = bf16_to_f16_bits((e & 1) ? (x1 >> 16) : (x1 & 0xffffu));
-            *(uint32_t*)(vt + (8 * dc + e) * L::VROW + 2 * col) = lo | (hi << 16);
+            const float lo = __uint_as_float((e & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
+            const float hi = __uint_as_float((e & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
+            *(uint32_t*)(vt + (8 * dc + e) * L::VROW + 2 * col) = pack_f16x2(lo, hi);
         }
     }
 }
@@ -212,7 +234,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     //   V: unit id = tid + 256u -> key pair id % (BN/2), dim chunk id / (BN/2)
     const uint16_t* kbase = a.k + (long long)g * D;
     const uint16_t* vbase = a.v + (long long)g * D;
-    const long long tok_stride = (long long)a.n_kv_heads * D;
+    const int tok_stride = a.n_kv_heads * D;
     TileStage<D> stg;
 
     // One 32-key half kb of the tile in buffer `buf`: S^T, online softmax,
@@ -227,9 +249,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
             st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qreg[s], st, 0, 0, 0);
         }
-        // scale + mask; lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
-#pragma unroll
-        for (int r = 0; r < 16; r++) st[r] *= a.scale_log2;
+        // mask (raw scores); lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
         if (masked) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
@@ -240,9 +260,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        // the running max moves only when some row's max exceeds it by more
-        // than 2^8, so most halves skip the O rescale (p stays <= 2^8)
+        mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;  // scale > 0: max commutes
+        // the running max (log2 units, scaled) moves only when some row's max
+        // exceeds it by more than 2^8, so most halves skip the O rescale
         if (__any(mt > mrun + kPrefillRescaleLog2)) {
             const float mnew = fmaxf(mrun, mt);
             const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
@@ -256,17 +276,24 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                 for (int t = 0; t < DT; t++) o[t][r] *= ar;
             }
         }
-        // A operands of the PV product: k-step t2 of this half holds keys
-        // 16t2 + 8(e/4) + 4h + e%4 (e = 0..7) of the half
+        // p = exp2(s*scale - m), one FMA + one exp per score, converted to
+        // fp16 pairs; the row sum adds the same fp16 values the PV product
+        // uses (v_dot2 against (1, 1)).  A operands of the PV product: k-step
+        // t2 of this half holds keys 16t2 + 8(e/4) + 4h + e%4 (e = 0..7).
         halfx8 pa[2];
+        const halfx2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
         float psum = 0.f;
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float pv = __builtin_amdgcn_exp2f(st[8 * t2 + e] - mrun);
-                psum += pv;
-                pa[t2][e] = (_Float16)pv;
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e], a.scale_log2, -mrun));
+                const float p1 =
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e + 1], a.scale_log2, -mrun));
+                const halfx2 pp = {(_Float16)p0, (_Float16)p1};
+                psum = __builtin_amdgcn_fdot2(pp, one2, psum, false);
+                pa[t2][e] = pp[0];
+                pa[t2][e + 1] = pp[1];
             }
         lrun += psum;
         // B operands: V^T row 32dt + j, the 8 keys of k-step t = 2kb + t2
@@ -340,6 +367,9 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: head_dim %d (supported: 64, 128)", head_dim);
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
         return set_error(NYION_ERR_INVALID, "prefill: q/k/v/out must be 16-byte aligned");
+    if ((long long)n * n_kv_heads * head_dim >= (1LL << 31) ||
+        (long long)n * n_heads * head_dim >= (1LL << 40))
+        return set_error(NYION_ERR_UNSUPPORTED, "prefill: chunk of %d tokens too large", n);
     const int group = n_heads / n_kv_heads;
     const int hw = group < 4 ? group : 4;
     if (4 % hw || group % hw)
