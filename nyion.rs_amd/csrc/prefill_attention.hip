@@ -239,16 +239,21 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 
     // One 32-key half kb of the tile in buffer `buf`: S^T, online softmax,
     // O += P.V over its two 16-key k-steps.
-    auto consume_half = [&](int buf, int kt, int kb, bool masked) {
-        const unsigned char* base = lds + buf * L::BUF;
-        // K rows kb*32 + j, chunk 2s + h
-        const unsigned char* kp = base + (kb * 32 + j) * L::KROW + 16 * h;
+    // S^T of 32-key half kb of the tile in buffer `buf` (K rows kb*32 + j,
+    // chunk 2s + h)
+    auto scores_half = [&](int buf, int kb) {
+        const unsigned char* kp = lds + buf * L::BUF + (kb * 32 + j) * L::KROW + 16 * h;
         floatx16 st = floatx16{};
 #pragma unroll
         for (int s = 0; s < KS; s++) {
             const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
             st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qreg[s], st, 0, 0, 0);
         }
+        return st;
+    };
+    // Online softmax of half kb and O += P.V over its two 16-key k-steps.
+    auto consume_half = [&](floatx16 st, int buf, int kt, int kb, bool masked) {
+        const unsigned char* base = lds + buf * L::BUF;
         // mask (raw scores); lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
         if (masked) {
 #pragma unroll
@@ -316,8 +321,12 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         const int kt = it * BN;
         const int cur = it & 1;
         const bool masked = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0);
-        consume_half(cur, kt, 0, masked);
-        consume_half(cur, kt, 1, masked);
+        // both halves' S first: the second chain of MFMAs has no dependence
+        // on the first half's softmax, so the two overlap
+        const floatx16 s0 = scores_half(cur, 0);
+        const floatx16 s1 = scores_half(cur, 1);
+        consume_half(s0, cur, kt, 0, masked);
+        consume_half(s1, cur, kt, 1, masked);
         // stage the next tile into the other buffer (last read one tile ago,
         // before the previous barrier) and start loading the one after
         if (it + 1 < n_tiles) {
