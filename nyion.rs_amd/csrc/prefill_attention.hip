@@ -5,10 +5,10 @@
 // row i attends to keys [0, i].  Here one kernel computes all rows of a chunk
 // as a flash-attention style pass: bf16 q, k, v in, fp32 accumulate, f32 out.
 //
-// Work decomposition.  A 256-thread workgroup owns one kv head and four
-// (q head, 32-row block) pairs that read the same K/V: for GQA 4:1 these are
-// the four q heads of the group on the same 32 rows, so every K/V tile staged
-// in LDS feeds four wavefronts.  Workgroups are numbered so that each XCD
+// Work decomposition.  A workgroup owns one kv head and eight (four at
+// head_dim 64) (q head, 32-row block) pairs that read the same K/V: for GQA
+// 4:1 these are the four q heads of the group on 64 rows, so every K/V tile
+// staged in LDS feeds eight wavefronts.  Workgroups are numbered so that each XCD
 // (workgroup id mod 8) takes a contiguous run of the (kv head, row block)
 // list: with 8 kv heads every XCD's L2 holds the K/V of one head.  Within a
 // head, row blocks are issued longest-first.
@@ -69,6 +69,14 @@ struct PrefillArgs {
 };
 
 constexpr int BN = 64;  // keys per tile
+
+// Threads per workgroup: eight wavefronts at head_dim 128 (two per SIMD, one
+// workgroup per CU), so each K/V tile staged in LDS feeds eight
+// (q head, 32-row) pairs; four at head_dim 64.
+template <int D>
+constexpr int prefill_threads() {
+    return D == 128 ? 512 : 256;
+}
 constexpr float kPrefillRescaleLog2 = 8.0f;
 
 // LDS tiles, padded by 16 bytes per row so that every lane's reads are one
@@ -101,11 +109,12 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 }
 
 // One tile's K and V in registers between its global loads and its LDS
-// stores (K chunk u: key (tid+256u) / (D/8); V unit u: key pair and 8 dims).
+// stores (K chunk u: key (tid+NT*u) / (D/8); V unit u: key pair and 8 dims).
 template <int D>
 struct TileStage {
-    static constexpr int KLOADS = BN * (D / 8) / 256;
-    static constexpr int VUNITS = (BN / 2) * (D / 8) / 256;
+    static constexpr int NT = prefill_threads<D>();
+    static constexpr int KLOADS = BN * (D / 8) / NT;
+    static constexpr int VUNITS = (BN / 2) * (D / 8) / NT;
     u32x4 k[KLOADS];
     u32x4 v0[VUNITS];
     u32x4 v1[VUNITS];
@@ -122,29 +131,29 @@ __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kba
     constexpr int CPR = D / 8;
     const uint16_t* kp = kbase + (long long)kt * tok_stride;
     const uint16_t* vp = vbase + (long long)kt * tok_stride;
-    const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);            // chunk u adds u*256/CPR keys
-    const int v_off = 2 * (tid % (BN / 2)) * tok_stride + 8 * (tid / (BN / 2));  // unit u adds 64 dims
+    const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);            // chunk u adds u*NT/CPR keys
+    const int v_off = 2 * (tid % (BN / 2)) * tok_stride + 8 * (tid / (BN / 2));  // unit u adds NT/4 dims
     if (kt + BN <= n) {
 #pragma unroll
         for (int u = 0; u < TileStage<D>::KLOADS; u++)
-            st.k[u] = *(const u32x4*)(kp + k_off + u * (256 / CPR) * tok_stride);
+            st.k[u] = *(const u32x4*)(kp + k_off + u * (TileStage<D>::NT / CPR) * tok_stride);
 #pragma unroll
         for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-            st.v0[u] = *(const u32x4*)(vp + v_off + 64 * u);
-            st.v1[u] = *(const u32x4*)(vp + v_off + 64 * u + tok_stride);
+            st.v0[u] = *(const u32x4*)(vp + v_off + 8 * (TileStage<D>::NT / (BN / 2)) * u);
+            st.v1[u] = *(const u32x4*)(vp + v_off + 8 * (TileStage<D>::NT / (BN / 2)) * u + tok_stride);
         }
         return;
     }
 #pragma unroll
     for (int u = 0; u < TileStage<D>::KLOADS; u++) {
-        const int key = tid / CPR + u * (256 / CPR);
+        const int key = tid / CPR + u * (TileStage<D>::NT / CPR);
         const int t = min(kt + key, n - 1);  // keys past n: finite values, masked
         st.k[u] = *(const u32x4*)(kbase + (long long)t * tok_stride + 8 * (tid % CPR));
     }
 #pragma unroll
     for (int u = 0; u < TileStage<D>::VUNITS; u++) {
         const int t = kt + 2 * (tid % (BN / 2));
-        const int dc = tid / (BN / 2) + u * (256 / (BN / 2));
+        const int dc = tid / (BN / 2) + u * (TileStage<D>::NT / (BN / 2));
         st.v0[u] = t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + 8 * dc) : u32x4{0, 0, 0, 0};
         st.v1[u] = t + 1 < n ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + 8 * dc)
                              : u32x4{0, 0, 0, 0};
@@ -157,13 +166,13 @@ __device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned cha
     constexpr int CPR = D / 8;
 #pragma unroll
     for (int u = 0; u < TileStage<D>::KLOADS; u++) {
-        const int id = tid + 256 * u;
+        const int id = tid + TileStage<D>::NT * u;
         *(u32x4*)(base + (id / CPR) * L::KROW + 16 * (id % CPR)) = st.k[u];
     }
     unsigned char* vt = base + L::KBYTES;
 #pragma unroll
     for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-        const int id = tid + 256 * u;
+        const int id = tid + TileStage<D>::NT * u;
         const int key = 2 * (id % (BN / 2));
         const int dc = id / (BN / 2);
         const int col = (key & ~15) + vt_pos(key & 15);  // even: keys key, key+1
@@ -181,7 +190,8 @@ __device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned cha
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) void prefill_kernel(
+    PrefillArgs a) {
     using L = PrefillLds<D>;
     constexpr int DT = D / 32;  // output dim tiles
     constexpr int KS = D / 16;  // k-steps of the S product
@@ -230,8 +240,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     float lrun = 0.f;
 
     // Per-thread roles in staging a tile (fixed for the whole loop).
-    //   K: chunk id = tid + 256u -> key id / CPR, chunk id % CPR
-    //   V: unit id = tid + 256u -> key pair id % (BN/2), dim chunk id / (BN/2)
+    //   K: chunk id = tid + NT*u -> key id / CPR, chunk id % CPR
+    //   V: unit id = tid + NT*u -> key pair id % (BN/2), dim chunk id / (BN/2)
     const uint16_t* kbase = a.k + (long long)g * D;
     const uint16_t* vbase = a.v + (long long)g * D;
     const int tok_stride = a.n_kv_heads * D;
@@ -381,6 +391,7 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: chunk of %d tokens too large", n);
     const int group = n_heads / n_kv_heads;
     const int hw = group < 4 ? group : 4;
+    const int waves = (head_dim == 128 ? 512 : 256) / 64;
     if (4 % hw || group % hw)
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: GQA group %d (need 1, 2 or a multiple of 4)",
                          group);
@@ -394,7 +405,7 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
     a.n_kv_heads = n_kv_heads;
     a.group = group;
     a.hw = hw;
-    a.rb_per_wg = 4 / hw;
+    a.rb_per_wg = waves / hw;
     const int rows_per_wg = 32 * a.rb_per_wg;
     a.n_rbg = (n + rows_per_wg - 1) / rows_per_wg;
     const long long items = (long long)n_kv_heads * (group / hw) * a.n_rbg;
@@ -406,9 +417,9 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
     dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
     if (head_dim == 128)
-        hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(prefill_threads<128>()), 0, st, a);
     else
-        hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(prefill_threads<64>()), 0, st, a);
     if ((rc = check_launch("prefill")) != NYION_OK) return rc;
     if (k_pool || v_pool) {
         if (!k_pool || !v_pool || !block_table)
