@@ -276,6 +276,24 @@ int nyion_kv_append_batch(void* k_pool, void* v_pool, const int32_t* block_table
                           int block_tokens, int num_blocks, int n_kv_heads, int head_dim,
                           int kv_dtype, const float* k, const float* v, nyion_stream_t stream);
 
+/* RoPE table of init_rope_lut (swamp-engine/src/ops.rs:20-37): d_lut
+ * [max_ctx][head_dim/2][2] f32 = (cos, sin) of m * 10000^(-2k/head_dim),
+ * computed on the host with the C library's powf/cosf/sinf (what the
+ * reference's f32::powf/cos/sin call) and copied; returns when copied. */
+int nyion_rope_lut_init(float* d_lut, int head_dim, int max_ctx, nyion_stream_t stream);
+
+/* Decode-step QKV epilogue in one launch: apply_rope_ufc (ops.rs:40-64) on
+ * q [batch][n_heads][D] (in place) and k [batch][n_kv_heads][D] at
+ * positions[b] (table row min(pos, max_ctx-1)), then the rotated k and v
+ * written into the paged pools at positions[b] (the save of executor.rs:
+ * 699-702, Q4-20B quantised as nyion_kv_write does).  k and v are not
+ * modified. */
+int nyion_rope_kv_append(float* d_q, const float* d_k, const float* d_v, const float* d_lut,
+                         int max_ctx, const int32_t* positions, int batch, int n_heads,
+                         int n_kv_heads, int head_dim, void* k_pool, void* v_pool,
+                         const int32_t* block_tables, int max_blocks_per_seq, int block_tokens,
+                         int num_blocks, int kv_dtype, nyion_stream_t stream);
+
 /* Debug/validation kernels sharing the decode kernels' index and unpack code:
  * gather tokens [0, n_tokens) of one sequence into [n_kv_heads][n_tokens][D]
  * f32 (dequantising Q4), and row-wise Q4-20B dequantise / quantise. */

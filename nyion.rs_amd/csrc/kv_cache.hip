@@ -13,6 +13,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <vector>
+
 #include "common.hpp"
 
 namespace nyion {
@@ -145,6 +147,80 @@ __global__ void kv_write_q4_kernel(WriteArgs a) {
         uint32_t* dv = (uint32_t*)((uint8_t*)a.v_pool + off + kQ4GroupBytes * g);
 #pragma unroll
         for (int t = 0; t < 5; t++) dv[t] = w[t];
+    }
+}
+
+// ------------------------------------------------------------- RoPE
+
+// apply_rotation_pair (swamp-engine/src/ops.rs:67-79): x*cos - y*sin,
+// x*sin + y*cos, each product rounded before the add (no contraction).
+__device__ __forceinline__ float2 rope_pair(float x, float y, float2 cs) {
+    return float2{x * cs.x - y * cs.y, x * cs.y + y * cs.x};
+}
+
+struct RopeArgs {
+    float* q;              // [B][Hq][D], rotated in place
+    const float* k;        // [B][Hkv][D] (before RoPE)
+    const float2* lut;     // [max_ctx][D/2] (cos, sin)
+    int max_ctx;
+    int n_heads;
+    WriteArgs w;           // k: unused (rotated on the fly), v: source of V rows
+};
+
+// One launch for the decode-step QKV epilogue.  Items [0, nq): one q pair
+// (b, head, k) each; items [nq, nq + nkv): one K/V unit each -- a pair (f32
+// pools) or a 32-element group (Q4-20B pools) of (b, kv head).
+template <int KVT>
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a, long long nq, long long nkv) {
+    const int D = a.w.head_dim;
+    const int half = D / 2;
+    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < nq + nkv; i += (long long)gridDim.x * 256) {
+        if (i < nq) {
+            const int k = (int)(i % half);
+            const long long row = i / half;  // b * Hq + head
+            const int b = (int)(row / a.n_heads);
+            const int pos = a.w.positions[b];
+            if (pos < 0) continue;
+            const float2 cs = a.lut[(long long)min(pos, a.max_ctx - 1) * half + k];
+            float* qp = a.q + row * D + 2 * k;
+            const float2 r = rope_pair(qp[0], qp[1], cs);
+            qp[0] = r.x;
+            qp[1] = r.y;
+            continue;
+        }
+        const long long j = i - nq;
+        const int units = KVT == NYION_KV_F32 ? half : (D + 31) / 32;
+        const int u = (int)(j % units);
+        const int h = (int)((j / units) % a.w.n_kv_heads);
+        const int b = (int)(j / ((long long)units * a.w.n_kv_heads));
+        const int pos = a.w.positions[b];
+        const long long off = write_row_offset(a.w, b, h);
+        if (pos < 0 || off < 0) continue;
+        const float2* cs = a.lut + (long long)min(pos, a.max_ctx - 1) * half;
+        const long long src = ((long long)b * a.w.n_kv_heads + h) * D;
+        if constexpr (KVT == NYION_KV_F32) {
+            const float2 r = rope_pair(a.k[src + 2 * u], a.k[src + 2 * u + 1], cs[u]);
+            *(float2*)((float*)a.w.k_pool + off + 2 * u) = r;
+            *(float2*)((float*)a.w.v_pool + off + 2 * u) = *(const float2*)(a.w.v + src + 2 * u);
+        } else {
+            const int len = min(32, D - 32 * u);
+            float kb[32];
+            for (int e = 0; e < len; e += 2) {
+                const float2 r = rope_pair(a.k[src + 32 * u + e], a.k[src + 32 * u + e + 1],
+                                           cs[16 * u + e / 2]);
+                kb[e] = r.x;
+                kb[e + 1] = r.y;
+            }
+            uint32_t w[5];
+            q4_quantize_group(kb, len, w);
+            uint32_t* dk = (uint32_t*)((uint8_t*)a.w.k_pool + off + kQ4GroupBytes * u);
+#pragma unroll
+            for (int t = 0; t < 5; t++) dk[t] = w[t];
+            q4_quantize_group(a.w.v + src + 32 * u, len, w);
+            uint32_t* dv = (uint32_t*)((uint8_t*)a.w.v_pool + off + kQ4GroupBytes * u);
+#pragma unroll
+            for (int t = 0; t < 5; t++) dv[t] = w[t];
+        }
     }
 }
 
@@ -427,6 +503,70 @@ int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out
     hipLaunchKernelGGL(q4_dequant_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
                        in, (long long)n_rows, head_dim, out);
     return check_launch("q4 dequant");
+}
+
+int nyion_rope_lut_init(float* d_lut, int head_dim, int max_ctx, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!d_lut || head_dim <= 0 || head_dim % 2 || max_ctx <= 0)
+        return set_error(NYION_ERR_INVALID, "rope lut: head_dim %d max_ctx %d", head_dim, max_ctx);
+    const int half = head_dim / 2;
+    // init_rope_lut (ops.rs:20-37) on the host with the C library's
+    // powf/cosf/sinf, as the reference computes it, then one copy
+    std::vector<float> lut((size_t)max_ctx * half * 2);
+    for (int m = 0; m < max_ctx; m++)
+        for (int k = 0; k < half; k++) {
+            const float freq = 1.0f / powf(10000.0f, (float)(2 * k) / (float)head_dim);
+            const float angle = (float)m * freq;
+            lut[((size_t)m * half + k) * 2] = cosf(angle);
+            lut[((size_t)m * half + k) * 2 + 1] = sinf(angle);
+        }
+    NYION_CHECK_HIP(hipMemcpyAsync(d_lut, lut.data(), lut.size() * sizeof(float),
+                                   hipMemcpyHostToDevice, (hipStream_t)stream));
+    NYION_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return NYION_OK;
+}
+
+int nyion_rope_kv_append(float* d_q, const float* d_k, const float* d_v, const float* d_lut,
+                         int max_ctx, const int32_t* positions, int batch, int n_heads,
+                         int n_kv_heads, int head_dim, void* k_pool, void* v_pool,
+                         const int32_t* block_tables, int max_blocks_per_seq, int block_tokens,
+                         int num_blocks, int kv_dtype, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    RopeArgs a{};
+    if ((rc = fill_write_args(a.w, k_pool, v_pool, block_tokens, num_blocks, n_kv_heads, head_dim,
+                              kv_dtype)) != NYION_OK)
+        return rc;
+    if (!d_q || !d_k || !d_v || !d_lut || !positions || !block_tables || batch <= 0 ||
+        n_heads <= 0 || max_blocks_per_seq <= 0 || max_ctx <= 0 || head_dim % 2)
+        return set_error(NYION_ERR_INVALID, "rope kv append: null argument or bad size");
+    if (!aligned(d_q, 8) || !aligned(d_k, 8) || !aligned(d_v, 8) || !aligned(d_lut, 8))
+        return set_error(NYION_ERR_INVALID, "rope kv append: buffers must be 8-byte aligned");
+    a.q = d_q;
+    a.k = d_k;
+    a.lut = (const float2*)d_lut;
+    a.max_ctx = max_ctx;
+    a.n_heads = n_heads;
+    a.w.tables = block_tables;
+    a.w.positions = positions;
+    a.w.v = d_v;
+    a.w.table_stride = max_blocks_per_seq;
+    a.w.rows = batch;
+    a.w.per_seq = 1;
+    const long long nq = (long long)batch * n_heads * (head_dim / 2);
+    const long long units = kv_dtype == NYION_KV_F32 ? head_dim / 2 : (head_dim + 31) / 32;
+    const long long nkv = (long long)batch * n_kv_heads * units;
+    const dim3 grid(grid_for(nq + nkv, 256));
+    if (kv_dtype == NYION_KV_F32)
+        hipLaunchKernelGGL(rope_kv_append_kernel<NYION_KV_F32>, grid, dim3(256), 0,
+                           (hipStream_t)stream, a, nq, nkv);
+    else
+        hipLaunchKernelGGL(rope_kv_append_kernel<NYION_KV_Q4_20B>, grid, dim3(256), 0,
+                           (hipStream_t)stream, a, nq, nkv);
+    return check_launch("rope kv append");
 }
 
 int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* out,

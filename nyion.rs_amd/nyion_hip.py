@@ -99,6 +99,9 @@ SIGNATURES = {
     "nyion_kv_append_batch": (i32, [vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, vp, vp,
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
+    "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
+                                   i32, i32, i32, vp]),
     "nyion_q4_dequant": (i32, [vp, i64, i32, vp, vp]),
     "nyion_q4_quantize": (i32, [vp, i64, i32, vp, vp]),
     "nyion_hma_create": (vp, [sz, sz]),
@@ -392,6 +395,25 @@ def kv_append_batch(k_pool, v_pool, block_tables, positions, block_tokens, n_kv_
                                       block_tokens, k_pool.shape[0], n_kv_heads, head_dim,
                                       kv_dtype, ptr(k), ptr(v), stream_handle(stream))
     check(rc, "nyion_kv_append_batch")
+
+
+def rope_lut(head_dim, max_ctx, device="cuda", stream=None):
+    """Device RoPE table [max_ctx][head_dim/2][2] f32 (init_rope_lut)."""
+    torch = _torch()
+    lut = torch.empty((max_ctx, head_dim // 2, 2), dtype=torch.float32, device=device)
+    check(load().nyion_rope_lut_init(ptr(lut), head_dim, max_ctx, stream_handle(stream)),
+          "nyion_rope_lut_init")
+    return lut
+
+
+def rope_kv_append(q, k, v, lut, positions, k_pool, v_pool, block_tables, n_heads, n_kv_heads,
+                   head_dim, block_tokens, kv_dtype=KV_F32, stream=None):
+    """RoPE on q (in place) and k, then k/v of each sequence into the pools."""
+    rc = load().nyion_rope_kv_append(
+        ptr(q), ptr(k), ptr(v), ptr(lut), lut.shape[0], ptr(positions), q.shape[0], n_heads,
+        n_kv_heads, head_dim, ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1],
+        block_tokens, k_pool.shape[0], kv_dtype, stream_handle(stream))
+    check(rc, "nyion_rope_kv_append")
 
 
 def kv_gather(pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dtype, n_tokens, out,

@@ -633,3 +633,40 @@ int orc_stokes_read(const void* p, float* keys, float* values, float* scores) {
     if (scores) memcpy(scores, c->scores, sizeof(float) * (size_t)c->n);
     return c->n;
 }
+
+/* ------------------------------------------------------------------------
+ * RoPE (swamp-engine/src/ops.rs:11, 20-37, 40-79)
+ * --------------------------------------------------------------------- */
+void orc_rope_lut(int head_dim, int max_ctx, float* lut) {
+    const int half = head_dim / 2;
+    for (int m = 0; m < max_ctx; m++)
+        for (int k = 0; k < half; k++) {
+            /* ops.rs:30-33: freq = 1 / theta^(2k/D); angle = m * freq (f32) */
+            float freq = 1.0f / powf(10000.0f, (float)(2 * k) / (float)head_dim);
+            float angle = (float)m * freq;
+            lut[((size_t)m * half + k) * 2] = cosf(angle);
+            lut[((size_t)m * half + k) * 2 + 1] = sinf(angle);
+        }
+}
+
+static void rope_rows(float* x, int rows, int head_dim, const float* cs) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < rows; h++) {
+        float* v = x + (size_t)h * head_dim;
+        for (int k = 0; k < half; k++) {
+            /* ops.rs:70-78 */
+            float a = v[2 * k], b = v[2 * k + 1];
+            float c = cs[2 * k], s = cs[2 * k + 1];
+            v[2 * k] = a * c - b * s;
+            v[2 * k + 1] = a * s + b * c;
+        }
+    }
+}
+
+void orc_apply_rope(float* q, float* k, int pos, int n_heads, int n_kv_heads, int head_dim,
+                    int max_ctx, const float* lut) {
+    if (pos > max_ctx - 1) pos = max_ctx - 1; /* ops.rs:53 */
+    const float* cs = lut + (size_t)pos * (head_dim / 2) * 2;
+    rope_rows(q, n_heads, head_dim, cs);
+    rope_rows(k, n_kv_heads, head_dim, cs);
+}

@@ -26,6 +26,10 @@
  *                                              swamp-kernels/src/lib.rs:629-684
  *                                              + integer pipeline by hand
  *   orc_stokes_*                             : eviction-by-construction
+ *   orc_rope_lut / orc_apply_rope            : float64 cos/sin of the same
+ *                                              angles within f32 rounding,
+ *                                              pos 0 identity, rotation
+ *                                              preserves pair norms
  * Bit-parity of attention outputs with the Rust binary (glibc expf order,
  * rayon scheduling of the importance sum) is unpinned and not required:
  * attention parity is at tolerance.
@@ -106,6 +110,13 @@ int orc_attention_rows(float* out, const float* q, int64_t q_row_stride,
                        int64_t out_row_stride, const orc_kv_layout* kv,
                        const int32_t* rows, int n_rows, int n_heads,
                        int n_kv_heads, int head_dim, int nthreads);
+
+/* RoPE: init_rope_lut (swamp-engine/src/ops.rs:20-37) into lut
+ * [max_ctx][head_dim/2][2], and apply_rope_ufc (ops.rs:40-79) on one
+ * token's q [n_heads][D] and k [n_kv_heads][D] in place. */
+void orc_rope_lut(int head_dim, int max_ctx, float* lut);
+void orc_apply_rope(float* q, float* k, int pos, int n_heads, int n_kv_heads, int head_dim,
+                    int max_ctx, const float* lut);
 
 /* swamp-kernels C-ABI restatements */
 int32_t orc_exp_q16_16(int32_t x_fixed);

@@ -54,6 +54,9 @@ def lib():
         L = C.CDLL(LIB_PATH)
         f32p = C.POINTER(C.c_float)
         i32p = C.POINTER(C.c_int32)
+        L.orc_rope_lut.argtypes = [C.c_int, C.c_int, C.c_void_p]
+        L.orc_apply_rope.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                     C.c_int, C.c_void_p]
         L.orc_dot_avx512_order.restype = C.c_float
         L.orc_dot_avx512_order.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
         L.orc_weighted_sum.argtypes = [C.c_void_p, C.c_void_p, C.c_float, C.c_int]
@@ -220,6 +223,23 @@ def fugu_positions(seq_len: int, q_pos: int, window: int, sentinel_stride: int,
 
 def q4_row_bytes(head_dim: int) -> int:
     return ((head_dim + 31) // 32) * 20
+
+
+def rope_lut(head_dim: int, max_ctx: int) -> np.ndarray:
+    """init_rope_lut: [max_ctx][head_dim/2][2] f32 (cos, sin)."""
+    out = np.empty((max_ctx, head_dim // 2, 2), dtype=np.float32)
+    lib().orc_rope_lut(head_dim, max_ctx, out.ctypes.data)
+    return out
+
+
+def apply_rope(q: np.ndarray, k: np.ndarray, pos: int, max_ctx: int, lut: np.ndarray):
+    """apply_rope_ufc on copies of one token's q [Hq][D], k [Hkv][D]."""
+    q = np.array(q, dtype=np.float32, copy=True, order="C")
+    k = np.array(k, dtype=np.float32, copy=True, order="C")
+    lut = np.ascontiguousarray(lut, dtype=np.float32)
+    lib().orc_apply_rope(q.ctypes.data, k.ctypes.data, pos, q.shape[0], k.shape[0], q.shape[1],
+                         max_ctx, lut.ctypes.data)
+    return q, k
 
 
 def q4_quantize_rows(x: np.ndarray) -> np.ndarray:

@@ -131,3 +131,42 @@ def test_paged_gather_matches_table_arithmetic(gpu):
     t = np.arange(777)
     exp = pb.k_pool[pb.tables[0][t // 16], :, t % 16].transpose(1, 0, 2)
     assert np.array_equal(out.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_kv_append_bit_exact(gpu, hd):
+    """Decode-step epilogue: RoPE on q and k (apply_rope_ufc) and the save of
+    the rotated k and of v, against the oracle's table and rotation,
+    bit-exactly (f32 products rounded before the add on both sides); a
+    position past max_ctx uses the table's last row."""
+    rng = np.random.default_rng(6)
+    B, hq, hkv, bt, max_ctx = 5, 16, 4, 16, 600
+    pos = np.array([0, 15, 16, 599, 700], np.int32)
+    tables = rng.permutation(B * 64).astype(np.int32).reshape(B, 64)
+    q = rng.standard_normal((B, hq, hd), dtype=np.float32)
+    k = rng.standard_normal((B, hkv, hd), dtype=np.float32)
+    v = rng.standard_normal((B, hkv, hd), dtype=np.float32)
+    lut_ref = oracle.rope_lut(hd, max_ctx)
+    lut = gpu.rope_lut(hd, max_ctx)
+    assert np.array_equal(lut.cpu().numpy().view(np.uint32), lut_ref.view(np.uint32))
+    for kv_dtype in (oracle.KV_F32, oracle.KV_Q4):
+        rb = hd if kv_dtype == oracle.KV_F32 else oracle.q4_row_bytes(hd)
+        dt = torch.float32 if kv_dtype == oracle.KV_F32 else torch.uint8
+        kp = torch.zeros((B * 64, hkv, bt, rb), dtype=dt, device="cuda")
+        vp = torch.zeros_like(kp)
+        dq = to_dev(q)
+        gpu.rope_kv_append(dq, to_dev(k), to_dev(v), lut, to_dev(pos), kp, vp, to_dev(tables),
+                           hq, hkv, hd, bt, kv_dtype)
+        torch.cuda.synchronize()
+        got_q, kh, vh = dq.cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy()
+        for b in range(B):
+            rq, rk = oracle.apply_rope(q[b], k[b], int(pos[b]), max_ctx, lut_ref)
+            assert np.array_equal(got_q[b].view(np.uint32), rq.view(np.uint32)), f"q b={b}"
+            krow = kh[tables[b, pos[b] // bt], :, pos[b] % bt]
+            vrow = vh[tables[b, pos[b] // bt], :, pos[b] % bt]
+            if kv_dtype == oracle.KV_F32:
+                assert np.array_equal(krow.view(np.uint32), rk.view(np.uint32)), f"k b={b}"
+                assert np.array_equal(vrow, v[b])
+            else:
+                assert np.array_equal(krow, oracle.q4_quantize_rows(rk)), f"k q4 b={b}"
+                assert np.array_equal(vrow, oracle.q4_quantize_rows(v[b]))

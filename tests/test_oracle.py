@@ -426,3 +426,45 @@ def test_stokes_evicts_first_minimum():
     L.orc_stokes_append(c, 0, key.ctypes.data, key.ctypes.data, float("nan"))
     assert L.orc_stokes_append(c, 0, key.ctypes.data, key.ctypes.data, 2.0) == -1
     L.orc_stokes_free(c)
+
+
+# ---------------------------------------------------------------- RoPE
+
+def test_rope_lut_against_float64():
+    """init_rope_lut (ops.rs:20-37): cos/sin of m * 10000^(-2k/D) with the
+    angle formed in f32; checked against float64 trigonometry of the exact
+    angle, within the f32 rounding of freq (powf, divide) and of m * freq."""
+    D, M = 128, 4096
+    lut = oracle.rope_lut(D, M).astype(np.float64)
+    k = np.arange(D // 2)
+    exact = np.arange(M)[:, None] * np.power(10000.0, -2.0 * k / D)[None, :]
+    tol = 2e-7 + np.abs(exact) * 3.6e-7
+    assert np.all(np.abs(lut[..., 0] - np.cos(exact)) < tol)
+    assert np.all(np.abs(lut[..., 1] - np.sin(exact)) < tol)
+    assert np.all(lut[0, :, 0] == 1.0) and np.all(lut[0, :, 1] == 0.0)
+    # k = 0: freq is exactly 1, the angle is m itself
+    assert np.max(np.abs(lut[:, 0, 0] - np.cos(np.arange(M)))) < 2e-7
+
+
+def test_apply_rope_rotation():
+    """apply_rope_ufc: pos 0 is the identity; pairs keep their norm; the
+    result matches a float64 rotation by the table's (cos, sin); positions
+    past max_ctx use the last row (ops.rs:53)."""
+    rng = np.random.default_rng(0)
+    D, M = 64, 300
+    lut = oracle.rope_lut(D, M)
+    q = rng.standard_normal((8, D), dtype=np.float32)
+    k = rng.standard_normal((2, D), dtype=np.float32)
+    q0, k0 = oracle.apply_rope(q, k, 0, M, lut)
+    assert np.array_equal(q0, q) and np.array_equal(k0, k)
+    q1, k1 = oracle.apply_rope(q, k, 123, M, lut)
+    c, s = lut[123, :, 0].astype(np.float64), lut[123, :, 1].astype(np.float64)
+    x, y = q[:, 0::2].astype(np.float64), q[:, 1::2].astype(np.float64)
+    assert np.max(np.abs(q1[:, 0::2] - (x * c - y * s))) < 1e-6
+    assert np.max(np.abs(q1[:, 1::2] - (x * s + y * c))) < 1e-6
+    n0 = x ** 2 + y ** 2
+    n1 = q1[:, 0::2].astype(np.float64) ** 2 + q1[:, 1::2].astype(np.float64) ** 2
+    assert np.max(np.abs(n1 - n0) / n0) < 1e-5
+    qa, _ = oracle.apply_rope(q, k, 10 * M, M, lut)
+    qb, _ = oracle.apply_rope(q, k, M - 1, M, lut)
+    assert np.array_equal(qa, qb)
