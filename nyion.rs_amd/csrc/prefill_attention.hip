@@ -102,6 +102,15 @@ __device__ __forceinline__ int vt_pos(int w) {
 
 typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
 
+// max(v, v of lane ^ 32): v_permlane32_swap exchanges the two 32-lane halves
+// without going through LDS (the result pair holds v and its partner in
+// either order, depending on the half).
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Two f32 -> one word of two fp16 (lo in the low half), round to nearest
 // even; one v_cvt_pk_f16_f32.
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
@@ -253,17 +262,30 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     // chunk 2s + h)
     auto scores_half = [&](int buf, int kb) {
         const unsigned char* kp = lds + buf * L::BUF + (kb * 32 + j) * L::KROW + 16 * h;
+        // all K fragments of the half are requested before the first MFMA
+        bf16x8 kf[KS];
+#pragma unroll
+        for (int s = 0; s < KS; s++) kf[s] = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMA chain
         floatx16 st = floatx16{};
 #pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const bf16x8 kf = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
-            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qreg[s], st, 0, 0, 0);
-        }
+        for (int s = 0; s < KS; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qreg[s], st, 0, 0, 0);
         return st;
     };
     // Online softmax of half kb and O += P.V over its two 16-key k-steps.
     auto consume_half = [&](floatx16 st, int buf, int kt, int kb, bool masked) {
         const unsigned char* base = lds + buf * L::BUF;
+        // B operands of the PV product (V^T row 32dt + j, the 8 keys of k-step
+        // t = 2kb + t2), requested first: they do not depend on P, so their
+        // LDS latency hides behind the softmax
+        const unsigned char* vp = base + L::KBYTES + j * L::VROW + 16 * h + 64 * kb;
+        halfx8 vb[2][DT];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                vb[t2][dt] = __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
+        __builtin_amdgcn_sched_barrier(0);
         // mask (raw scores); lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
         if (masked) {
 #pragma unroll
@@ -275,7 +297,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;  // scale > 0: max commutes
+        mt = max_xor32(mt) * a.scale_log2;  // scale > 0: max commutes
         // the running max (log2 units, scaled) moves only when some row's max
         // exceeds it by more than 2^8, so most halves skip the O rescale
         if (__any(mt > mrun + kPrefillRescaleLog2)) {
@@ -311,16 +333,11 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
                 pa[t2][e + 1] = pp[1];
             }
         lrun += psum;
-        // B operands: V^T row 32dt + j, the 8 keys of k-step t = 2kb + t2
-        const unsigned char* vp = base + L::KBYTES + j * L::VROW + 16 * h + 64 * kb;
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const halfx8 vb =
-                    __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb, o[dt], 0, 0, 0);
-            }
+            for (int dt = 0; dt < DT; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[t2][dt], o[dt], 0, 0, 0);
     };
 
     stage_load<D>(stg, kbase, vbase, tok_stride, a.n, 0, tid);
