@@ -527,7 +527,7 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
                 }
         }
         if (active && r == 0) {
-            const float inv = 1.0f / x.l;
+            const float inv = x.l > 0.f ? 1.0f / x.l : 0.f;  // nothing attended: zeros
             *(float4*)(out + hh * D + 4 * dq) =
                 float4{x.o[0] * inv, x.o[1] * inv, x.o[2] * inv, x.o[3] * inv};
             if (score_rows && dq == 0) {  // final (m, l) of the head: end of its score row
@@ -773,7 +773,7 @@ void decode_kernel(DecodeArgs a) {
                     sr[a.scores_stride - 1] = lh[r];
                 }
                 if (whole) {
-                    const float inv = 1.0f / lh[r];
+                    const float inv = lh[r] > 0.f ? 1.0f / lh[r] : 0.f;  // nothing attended: zeros
                     float* o = a.out + ((long long)b * a.n_heads + head0 + hh) * D + DPL * j;
 #pragma unroll
                     for (int x = 0; x < DPL / 4; x++)

@@ -99,6 +99,45 @@ def test_paged_edge_lengths(gpu, lens):
     assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"lens {lens}")
 
 
+@pytest.mark.parametrize("ctx,max_ctx,q_pos", [(1000, 4096, None), (4096, 4096, 100), (1, 64, None),
+                                              (3000, 3001, 0)])
+def test_single_sequence_host_bound(gpu, ctx, max_ctx, q_pos):
+    """One sequence: the split follows max_ctx, the actual length masks the
+    tail (pieces past it attend to nothing), and q_pos limits the range."""
+    pb = W.paged_batch([ctx], seed=ctx, spare_blocks=(max_ctx - ctx + 15) // 16)
+    nblk = (max_ctx + 15) // 16
+    if pb.tables.shape[1] < nblk:  # table rows for the whole host bound
+        extra = np.arange(pb.tables.shape[1], nblk, dtype=np.int32) % pb.k_pool.shape[0]
+        pb.tables = np.concatenate([pb.tables, extra[None, :]], axis=1)
+    qp = None if q_pos is None else [q_pos]
+    for p in (64, 0):
+        try:
+            gpu.set_partition_tokens(p)
+            got = run_paged(gpu, pb, q_pos=qp, max_ctx=max_ctx)
+        finally:
+            gpu.set_partition_tokens(0)
+        assert_close(got, W.reference_decode(pb, q_pos=qp), f"ctx {ctx} max {max_ctx} part {p}")
+
+
+def test_single_sequence_empty_is_zero(gpu):
+    """ctx_len 0 (nothing to attend to) writes zeros, with or without the
+    split-K merge."""
+    pb = W.paged_batch([64], seed=1)
+    q = to_dev(pb.q)
+    kp, vp, tab = to_dev(pb.k_pool), to_dev(pb.v_pool), to_dev(pb.tables)
+    ctx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for p in (64, 0):
+        out = torch.full_like(q, float("nan"))
+        try:
+            gpu.set_partition_tokens(p)
+            gpu.paged_decode(q, kp, vp, tab, ctx, out, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                             pb.block_tokens, max_ctx=64)
+        finally:
+            gpu.set_partition_tokens(0)
+        torch.cuda.synchronize()
+        assert torch.all(out == 0).item()
+
+
 def test_paged_variable_batch_and_partitions(gpu):
     lens = W.c3_lengths(seed=3, batch=24, lo=1, hi=3000)
     pb = W.paged_batch(lens, seed=3, spare_blocks=7)
