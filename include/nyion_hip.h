@@ -245,18 +245,36 @@ int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, i
 
 /* Causal prefill of one chunk on MFMA (bf16 in, f32 accumulate, f32 out).
  * Replaces the per-token ops::attention loop of prefill_slice
- * (executor.rs:106-137): row i attends to keys [0, start_pos+i] of this chunk
- * (start_pos = 0: the chunk is the whole prefix).  Layout: q [n][n_heads][D],
+ * (executor.rs:106-137) for a chunk that is the whole prefix (pos_offset 0):
+ * row i attends to keys [0, i] of the chunk.  Layout: q [n][n_heads][D],
  * k, v [n][n_kv_heads][D] bf16 (raw uint16 bits); out [n][n_heads][D] f32.
  * causal = 0 attends to all n keys.  head_dim 128 or 64.
  * When k_pool is non-NULL, the chunk's K/V are also written into the paged
  * cache at positions start_pos.. (the save_at loop, executor.rs:106-111),
- * widened to f32 or quantised to Q4-20B per kv_dtype. */
+ * widened to f32 or quantised to Q4-20B per kv_dtype.  Keys before the
+ * chunk are not attended here; a chunk that continues a cached prefix uses
+ * nyion_prefill_attention_bf16_ctx. */
 int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n,
                                  int n_heads, int n_kv_heads, int head_dim, int causal,
                                  float scale, float* out, void* k_pool, void* v_pool,
                                  const int32_t* block_table, int block_tokens, int num_blocks,
                                  int kv_dtype, int start_pos, nyion_stream_t stream);
+
+/* Chunked prefill after a cached prefix: prefill_slice with pos_offset =
+ * n_hist (executor.rs:106-137), where row i of the chunk (absolute position
+ * n_hist + i) attends to all n_hist history keys and to keys [0, i] of the
+ * chunk (causal = 0: all n).  k_hist, v_hist [n_hist][n_kv_heads][D] bf16
+ * hold the history (nyion_kv_gather_bf16 builds them from the paged cache);
+ * n_hist = 0 is nyion_prefill_attention_bf16.  The other arguments are those
+ * of nyion_prefill_attention_bf16; the KV write normally uses start_pos =
+ * n_hist. */
+int nyion_prefill_attention_bf16_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                     const uint16_t* k_hist, const uint16_t* v_hist, int n_hist,
+                                     int n, int n_heads, int n_kv_heads, int head_dim, int causal,
+                                     float scale, float* out, void* k_pool, void* v_pool,
+                                     const int32_t* block_table, int block_tokens,
+                                     int num_blocks, int kv_dtype, int start_pos,
+                                     nyion_stream_t stream);
 
 /* --------------------------------------------------------------- KV cache */
 
@@ -300,6 +318,14 @@ int nyion_rope_kv_append(float* d_q, const float* d_k, const float* d_v, const f
 int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_tokens,
                     int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
                     float* out, nyion_stream_t stream);
+/* Tokens [0, n_tokens) of one sequence's paged K (or V) cache (the rows
+ * ops::attention reads, ops.rs:170-278, through cache.rs's page lookup) as
+ * [n_tokens][n_kv_heads][D] bf16, rounded to nearest even (Q4-20B
+ * dequantised first): the history operand of
+ * nyion_prefill_attention_bf16_ctx.  out 16-byte aligned. */
+int nyion_kv_gather_bf16(const void* pool, const int32_t* block_table, int block_tokens,
+                         int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
+                         uint16_t* out, nyion_stream_t stream);
 int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out,
                      nyion_stream_t stream);
 int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* out,

@@ -227,7 +227,8 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a, long lo
 struct GatherArgs {
     const void* pool;
     const int32_t* table;
-    float* out;  // [Hkv][n_tokens][D]
+    float* out;         // [Hkv][n_tokens][D] f32, or
+    uint16_t* out_bf16; // [n_tokens][Hkv][D] bf16 (the prefill kernel's history layout)
     long long block_stride;
     long long head_stride;
     int token_stride;
@@ -239,8 +240,17 @@ struct GatherArgs {
     int kvt;
 };
 
+// f32 -> bf16 bits, round to nearest even; NaN -> the quiet NaN 0x7fc0 with
+// the sign kept.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    const uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return ((x >> 16) & 0x8000u) | 0x7fc0u;
+    return (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+}
+
 // One thread per (head, token, 8 dims), through the decode kernels' RowMap
 // and q4_dequant8.
+template <bool BF16>
 __global__ void kv_gather_kernel(GatherArgs a) {
     const int vec = a.head_dim / 8;
     const long long n = (long long)a.n_kv_heads * a.n_tokens * vec;
@@ -257,7 +267,6 @@ __global__ void kv_gather_kernel(GatherArgs a) {
         const int x = (int)(i % vec);
         const int t = (int)((i / vec) % a.n_tokens);
         const int h = (int)(i / ((long long)vec * a.n_tokens));
-        float* dst = a.out + ((long long)h * a.n_tokens + t) * a.head_dim + 8 * x;
         const long long off = row_offset(m, t, h);
         float vals[8];
         if (off < 0) {
@@ -273,7 +282,17 @@ __global__ void kv_gather_kernel(GatherArgs a) {
             const uint32_t w = *(const uint32_t*)(row + kQ4GroupBytes * g + 4 + ((e0 & 31) >> 1));
             q4_dequant8(w, f16_bits_to_f32(hdr), f16_bits_to_f32(hdr >> 16), vals);
         }
-        for (int e = 0; e < 8; e++) dst[e] = vals[e];
+        if (BF16) {
+            uint4 w;
+            w.x = f32_to_bf16_bits(vals[0]) | (f32_to_bf16_bits(vals[1]) << 16);
+            w.y = f32_to_bf16_bits(vals[2]) | (f32_to_bf16_bits(vals[3]) << 16);
+            w.z = f32_to_bf16_bits(vals[4]) | (f32_to_bf16_bits(vals[5]) << 16);
+            w.w = f32_to_bf16_bits(vals[6]) | (f32_to_bf16_bits(vals[7]) << 16);
+            *(uint4*)(a.out_bf16 + ((long long)t * a.n_kv_heads + h) * a.head_dim + 8 * x) = w;
+        } else {
+            float* dst = a.out + ((long long)h * a.n_tokens + t) * a.head_dim + 8 * x;
+            for (int e = 0; e < 8; e++) dst[e] = vals[e];
+        }
     }
 }
 
@@ -455,14 +474,17 @@ int nyion_kv_append_batch(void* k_pool, void* v_pool, const int32_t* block_table
     return launch_write(a, kv_dtype, (hipStream_t)stream);
 }
 
-int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_tokens,
-                    int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
-                    float* out, nyion_stream_t stream) {
+static int kv_gather_impl(const void* pool, const int32_t* block_table, int block_tokens,
+                          int num_blocks, int n_kv_heads, int head_dim, int kv_dtype,
+                          int n_tokens, float* out, uint16_t* out_bf16, nyion_stream_t stream) {
     clear_error();
     int rc;
     if ((rc = require_device()) != NYION_OK) return rc;
-    if (!pool || !block_table || !out || n_tokens <= 0 || n_kv_heads <= 0 || num_blocks <= 0)
+    if (!pool || !block_table || !(out || out_bf16) || n_tokens <= 0 || n_kv_heads <= 0 ||
+        num_blocks <= 0)
         return set_error(NYION_ERR_INVALID, "kv gather: null argument or non-positive size");
+    if (out_bf16 && !aligned(out_bf16, 16))
+        return set_error(NYION_ERR_INVALID, "kv gather: bf16 output must be 16-byte aligned");
     if (head_dim <= 0 || head_dim % 8)
         return set_error(NYION_ERR_UNSUPPORTED, "kv gather: head_dim %d not a multiple of 8",
                          head_dim);
@@ -474,6 +496,7 @@ int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_toke
     a.pool = pool;
     a.table = block_table;
     a.out = out;
+    a.out_bf16 = out_bf16;
     a.token_stride = (int)row;
     a.head_stride = (long long)block_tokens * row;
     a.block_stride = (long long)n_kv_heads * block_tokens * row;
@@ -484,9 +507,27 @@ int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_toke
     a.n_tokens = n_tokens;
     a.kvt = kv_dtype;
     const long long n = (long long)n_kv_heads * n_tokens * (head_dim / 8);
-    hipLaunchKernelGGL(kv_gather_kernel, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
-                       a);
+    if (out_bf16)
+        hipLaunchKernelGGL(kv_gather_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0,
+                           (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(kv_gather_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0,
+                           (hipStream_t)stream, a);
     return check_launch("kv gather");
+}
+
+int nyion_kv_gather(const void* pool, const int32_t* block_table, int block_tokens,
+                    int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
+                    float* out, nyion_stream_t stream) {
+    return kv_gather_impl(pool, block_table, block_tokens, num_blocks, n_kv_heads, head_dim,
+                          kv_dtype, n_tokens, out, nullptr, stream);
+}
+
+int nyion_kv_gather_bf16(const void* pool, const int32_t* block_table, int block_tokens,
+                         int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int n_tokens,
+                         uint16_t* out, nyion_stream_t stream) {
+    return kv_gather_impl(pool, block_table, block_tokens, num_blocks, n_kv_heads, head_dim,
+                          kv_dtype, n_tokens, nullptr, out, stream);
 }
 
 int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out,

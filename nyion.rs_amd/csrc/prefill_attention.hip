@@ -2,8 +2,10 @@
 //
 // The reference prefills by calling ops::attention once per token with
 // seq_len = abs_pos + 1 (swamp-engine/src/executor.rs:132-137, ops.rs:170-278):
-// row i attends to keys [0, i].  Here one kernel computes all rows of a chunk
-// as a flash-attention style pass: bf16 q, k, v in, fp32 accumulate, f32 out.
+// row i of a chunk that starts at position p attends to keys [0, p + i], the
+// p cached ones first.  Here one kernel computes all rows of a chunk as a
+// flash-attention style pass: bf16 q, k, v (and the p history tokens' k, v)
+// in, fp32 accumulate, f32 out.
 //
 // Work decomposition.  A workgroup owns one kv head and eight (four at
 // head_dim 64) (q head, 32-row block) pairs that read the same K/V: for GQA
@@ -14,10 +16,9 @@
 // head, row blocks are issued longest-first.
 //
 // Per 64-key tile:
-//   K tile  [64][D] bf16 -> LDS, 16-byte chunks XOR-swizzled by key row
+//   K tile  [64][D] bf16 -> LDS, rows padded by 16 bytes
 //   V tile  [64][D] bf16 -> LDS as fp16, transposed to V^T [D][64] (key
-//           pairs packed into 32-bit words, 8-byte chunks XOR-swizzled by
-//           dim row)
+//           pairs packed into 32-bit words, rows padded by 16 bytes)
 //   S^T[64 keys][32 rows] = K . Q^T      v_mfma_f32_32x32x16_bf16, Q^T from
 //                                        registers (loaded once)
 //   online softmax per row (rows are lanes; 32 keys per lane per half), the
@@ -55,8 +56,11 @@ struct PrefillArgs {
     const uint16_t* q;  // [N][Hq][D]
     const uint16_t* k;  // [N][Hkv][D]
     const uint16_t* v;
+    const uint16_t* kh;  // [n_hist][Hkv][D]: the sequence's tokens before the chunk
+    const uint16_t* vh;
     float* out;  // [N][Hq][D]
     int n;
+    int n_hist;
     int n_heads;
     int n_kv_heads;
     int group;     // q heads per kv head
@@ -129,10 +133,12 @@ struct TileStage {
     u32x4 v1[VUNITS];
 };
 
-// Loads of tile kt.  Offsets are 32-bit element offsets from the tile's
-// first token (the host keeps n * n_kv_heads * head_dim below 2^31), so a
-// full tile costs one per-thread base plus constant steps; only a tile
-// that reaches past n clamps or zeroes rows.
+// Loads of the tile whose first key is token kt of a source of n tokens
+// (kt may be negative for the first history tile).  Offsets are 32-bit
+// element offsets from the tile's first token (the host keeps n *
+// n_kv_heads * head_dim below 2^31), so a full tile costs one per-thread
+// base plus constant steps; only a tile that reaches outside [0, n) clamps
+// K rows and zeroes V rows.
 template <int D>
 __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kbase,
                                            const uint16_t* vbase, int tok_stride, int n, int kt,
@@ -142,7 +148,7 @@ __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kba
     const uint16_t* vp = vbase + (long long)kt * tok_stride;
     const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);            // chunk u adds u*NT/CPR keys
     const int v_off = 2 * (tid % (BN / 2)) * tok_stride + 8 * (tid / (BN / 2));  // unit u adds NT/4 dims
-    if (kt + BN <= n) {
+    if (kt >= 0 && kt + BN <= n) {
 #pragma unroll
         for (int u = 0; u < TileStage<D>::KLOADS; u++)
             st.k[u] = *(const u32x4*)(kp + k_off + u * (TileStage<D>::NT / CPR) * tok_stride);
@@ -156,17 +162,32 @@ __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kba
 #pragma unroll
     for (int u = 0; u < TileStage<D>::KLOADS; u++) {
         const int key = tid / CPR + u * (TileStage<D>::NT / CPR);
-        const int t = min(kt + key, n - 1);  // keys past n: finite values, masked
+        const int t = min(max(kt + key, 0), n - 1);  // keys outside: finite values, masked
         st.k[u] = *(const u32x4*)(kbase + (long long)t * tok_stride + 8 * (tid % CPR));
     }
 #pragma unroll
     for (int u = 0; u < TileStage<D>::VUNITS; u++) {
         const int t = kt + 2 * (tid % (BN / 2));
         const int dc = tid / (BN / 2) + u * (TileStage<D>::NT / (BN / 2));
-        st.v0[u] = t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + 8 * dc) : u32x4{0, 0, 0, 0};
-        st.v1[u] = t + 1 < n ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + 8 * dc)
-                             : u32x4{0, 0, 0, 0};
+        st.v0[u] = t >= 0 && t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + 8 * dc)
+                                   : u32x4{0, 0, 0, 0};
+        st.v1[u] = t + 1 >= 0 && t + 1 < n
+                       ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + 8 * dc)
+                       : u32x4{0, 0, 0, 0};
     }
+}
+
+// The tile at key kt (relative to the chunk): keys below 0 come from the
+// history, the rest from the chunk.  kt is uniform, so the selects are
+// scalar and one copy of the loads serves both sources.
+template <int D>
+__device__ __forceinline__ void load_tile(TileStage<D>& st, const PrefillArgs& a,
+                                          const uint16_t* kbase, const uint16_t* vbase,
+                                          const uint16_t* khbase, const uint16_t* vhbase,
+                                          int tok_stride, int kt, int tid) {
+    const bool hist = kt < 0;
+    stage_load<D>(st, hist ? khbase : kbase, hist ? vhbase : vbase, tok_stride,
+                  hist ? a.n_hist : a.n, hist ? kt + a.n_hist : kt, tid);
 }
 
 template <int D>
@@ -225,8 +246,15 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     const int head = g * a.group + hs * a.hw + (wave % a.hw);
     const int row0 = (rbg * a.rb_per_wg + wave / a.hw) * 32;
     const int wg_row_end = min(a.n, (rbg + 1) * a.rb_per_wg * 32);
+    // Keys are numbered relative to the chunk: history token t is key
+    // t - n_hist (negative), chunk token t is key t.  History tiles end at
+    // key -1, so the chunk's tiles start at key 0 whatever n_hist is, and
+    // only the first history tile can be partial.
     const int key_end = a.causal ? wg_row_end : a.n;
-    const int n_tiles = (key_end + BN - 1) / BN;
+    const int n_htiles = (a.n_hist + BN - 1) / BN;
+    const int n_tiles = n_htiles + (key_end + BN - 1) / BN;
+    const int kt0 = -n_htiles * BN;
+    const int key_lo = -a.n_hist;                                  // first key of every row
     const int lim = a.causal ? min(row0 + j, a.n - 1) : a.n - 1;  // last key of this lane's row
 
     // Q^T operand (B of S^T = K.Q^T): row row0+j, dims 16s + 8h .. +7
@@ -253,6 +281,8 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     //   V: unit id = tid + NT*u -> key pair id % (BN/2), dim chunk id / (BN/2)
     const uint16_t* kbase = a.k + (long long)g * D;
     const uint16_t* vbase = a.v + (long long)g * D;
+    const uint16_t* khbase = a.kh + (long long)g * D;
+    const uint16_t* vhbase = a.vh + (long long)g * D;
     const int tok_stride = a.n_kv_heads * D;
     TileStage<D> stg;
 
@@ -291,7 +321,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                st[r] = key <= lim ? st[r] : -INFINITY;
+                st[r] = key <= lim && key >= key_lo ? st[r] : -INFINITY;
             }
         }
         float mt = -INFINITY;
@@ -340,14 +370,14 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[t2][dt], o[dt], 0, 0, 0);
     };
 
-    stage_load<D>(stg, kbase, vbase, tok_stride, a.n, 0, tid);
+    load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt0, tid);
     stage_store<D>(stg, lds, tid);
     __syncthreads();
-    if (n_tiles > 1) stage_load<D>(stg, kbase, vbase, tok_stride, a.n, BN, tid);
+    if (n_tiles > 1) load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt0 + BN, tid);
     for (int it = 0; it < n_tiles; it++) {
-        const int kt = it * BN;
+        const int kt = kt0 + it * BN;
         const int cur = it & 1;
-        const bool masked = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0);
+        const bool masked = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0) || kt < key_lo;
         // both halves' S first: the second chain of MFMAs has no dependence
         // on the first half's softmax, so the two overlap
         const floatx16 s0 = scores_half(cur, 0);
@@ -358,7 +388,8 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         // before the previous barrier) and start loading the one after
         if (it + 1 < n_tiles) {
             stage_store<D>(stg, lds + (cur ^ 1) * L::BUF, tid);
-            if (it + 2 < n_tiles) stage_load<D>(stg, kbase, vbase, tok_stride, a.n, kt + 2 * BN, tid);
+            if (it + 2 < n_tiles)
+                load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt + 2 * BN, tid);
         }
         __syncthreads();
     }
@@ -381,18 +412,14 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
 
 }  // namespace nyion
 
-
-
-
-
 using namespace nyion;
 
-extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                            int n, int n_heads, int n_kv_heads, int head_dim,
-                                            int causal, float scale, float* out, void* k_pool,
-                                            void* v_pool, const int32_t* block_table,
-                                            int block_tokens, int num_blocks, int kv_dtype,
-                                            int start_pos, nyion_stream_t stream) {
+static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        const uint16_t* k_hist, const uint16_t* v_hist, int n_hist, int n,
+                        int n_heads, int n_kv_heads, int head_dim, int causal, float scale,
+                        float* out, void* k_pool, void* v_pool, const int32_t* block_table,
+                        int block_tokens, int num_blocks, int kv_dtype, int start_pos,
+                        nyion_stream_t stream) {
     clear_error();
     int rc;
     if ((rc = require_device()) != NYION_OK) return rc;
@@ -403,9 +430,15 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: head_dim %d (supported: 64, 128)", head_dim);
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
         return set_error(NYION_ERR_INVALID, "prefill: q/k/v/out must be 16-byte aligned");
+    if (n_hist < 0) return set_error(NYION_ERR_INVALID, "prefill: n_hist %d", n_hist);
+    if (n_hist > 0 && (!k_hist || !v_hist || !aligned(k_hist, 16) || !aligned(v_hist, 16)))
+        return set_error(NYION_ERR_INVALID, "prefill: history needs 16-byte aligned k_hist/v_hist");
     if ((long long)n * n_kv_heads * head_dim >= (1LL << 31) ||
         (long long)n * n_heads * head_dim >= (1LL << 40))
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: chunk of %d tokens too large", n);
+    if ((long long)n_hist * n_kv_heads * head_dim >= (1LL << 31) ||
+        (long long)n_hist + n + 2 * BN >= (1LL << 31))
+        return set_error(NYION_ERR_UNSUPPORTED, "prefill: history of %d tokens too large", n_hist);
     const int group = n_heads / n_kv_heads;
     const int hw = group < 4 ? group : 4;
     const int waves = (head_dim == 128 ? 512 : 256) / 64;
@@ -416,8 +449,12 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
     a.q = q;
     a.k = k;
     a.v = v;
+    // with no history the history pointers are never read; they alias k/v
+    a.kh = n_hist > 0 ? k_hist : k;
+    a.vh = n_hist > 0 ? v_hist : v;
     a.out = out;
     a.n = n;
+    a.n_hist = n_hist;
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
     a.group = group;
@@ -445,4 +482,28 @@ extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k
                                   head_dim, kv_dtype, start_pos, n, k, v, st);
     }
     return NYION_OK;
+}
+
+extern "C" int nyion_prefill_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                            int n, int n_heads, int n_kv_heads, int head_dim,
+                                            int causal, float scale, float* out, void* k_pool,
+                                            void* v_pool, const int32_t* block_table,
+                                            int block_tokens, int num_blocks, int kv_dtype,
+                                            int start_pos, nyion_stream_t stream) {
+    return prefill_impl(q, k, v, nullptr, nullptr, 0, n, n_heads, n_kv_heads, head_dim, causal,
+                        scale, out, k_pool, v_pool, block_table, block_tokens, num_blocks,
+                        kv_dtype, start_pos, stream);
+}
+
+extern "C" int nyion_prefill_attention_bf16_ctx(const uint16_t* q, const uint16_t* k,
+                                                const uint16_t* v, const uint16_t* k_hist,
+                                                const uint16_t* v_hist, int n_hist, int n,
+                                                int n_heads, int n_kv_heads, int head_dim,
+                                                int causal, float scale, float* out, void* k_pool,
+                                                void* v_pool, const int32_t* block_table,
+                                                int block_tokens, int num_blocks, int kv_dtype,
+                                                int start_pos, nyion_stream_t stream) {
+    return prefill_impl(q, k, v, k_hist, v_hist, n_hist, n, n_heads, n_kv_heads, head_dim, causal,
+                        scale, out, k_pool, v_pool, block_table, block_tokens, num_blocks,
+                        kv_dtype, start_pos, stream);
 }

@@ -95,10 +95,13 @@ SIGNATURES = {
     "nyion_get_decode_partition_tokens": (i32, [i32, i32, i32, i32]),
     "nyion_prefill_attention_bf16": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp, vp,
                                            vp, i32, i32, i32, i32, vp]),
+    "nyion_prefill_attention_bf16_ctx": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                               f32, vp, vp, vp, vp, i32, i32, i32, i32, vp]),
     "nyion_kv_write": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
     "nyion_kv_append_batch": (i32, [vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, vp, vp,
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_kv_gather_bf16": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
     "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
                                    i32, i32, i32, vp]),
@@ -376,6 +379,23 @@ def prefill_bf16(q, k, v, out, n_heads, n_kv_heads, head_dim, causal=True, scale
     check(rc, "nyion_prefill_attention_bf16")
 
 
+def prefill_bf16_ctx(q, k, v, k_hist, v_hist, out, n_heads, n_kv_heads, head_dim, causal=True,
+                     scale=0.0, k_pool=None, v_pool=None, block_table=None, block_tokens=16,
+                     kv_dtype=KV_F32, start_pos=None, stream=None):
+    """Chunk after a cached prefix: k_hist/v_hist [n_hist][Hkv][D] bf16 (or None for
+    n_hist = 0); the KV write defaults to start_pos = n_hist."""
+    n = q.shape[0]
+    n_hist = 0 if k_hist is None else k_hist.shape[0]
+    if start_pos is None:
+        start_pos = n_hist
+    num_blocks = 0 if k_pool is None else k_pool.shape[0]
+    rc = load().nyion_prefill_attention_bf16_ctx(
+        ptr(q), ptr(k), ptr(v), ptr(k_hist), ptr(v_hist), n_hist, n, n_heads, n_kv_heads,
+        head_dim, 1 if causal else 0, scale, ptr(out), ptr(k_pool), ptr(v_pool), ptr(block_table),
+        block_tokens, num_blocks, kv_dtype, start_pos, stream_handle(stream))
+    check(rc, "nyion_prefill_attention_bf16_ctx")
+
+
 # ----------------------------------------------------------------------------
 # KV cache
 # ----------------------------------------------------------------------------
@@ -442,3 +462,12 @@ def softmax_padic_dev(logits, probs, temperature=1.0, stream=None):
     check(load().nyion_softmax_padic_dev(ptr(logits), ptr(probs), logits.numel(),
                                          float(temperature), stream_handle(stream)),
           "nyion_softmax_padic_dev")
+
+
+def kv_gather_bf16(pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dtype, n_tokens,
+                   out, stream=None):
+    """Tokens [0, n_tokens) of a paged pool as [n_tokens][Hkv][D] bf16 in `out`."""
+    rc = load().nyion_kv_gather_bf16(ptr(pool), ptr(block_table), block_tokens, pool.shape[0],
+                                     n_kv_heads, head_dim, kv_dtype, n_tokens, ptr(out),
+                                     stream_handle(stream))
+    check(rc, "nyion_kv_gather_bf16")

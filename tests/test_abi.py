@@ -46,6 +46,11 @@ def test_no_device_is_reported_not_faked():
                                   None) == nyion_hip.ERR_NO_DEVICE
     assert L.nyion_prefill_attention_bf16(None, None, None, 1, 1, 1, 128, 1, 0.0, None, None,
                                           None, None, 16, 0, 0, 0, None) == nyion_hip.ERR_NO_DEVICE
+    assert L.nyion_prefill_attention_bf16_ctx(None, None, None, None, None, 0, 1, 1, 1, 128, 1,
+                                              0.0, None, None, None, None, 16, 0, 0, 0,
+                                              None) == nyion_hip.ERR_NO_DEVICE
+    assert L.nyion_kv_gather_bf16(None, None, 16, 1, 1, 64, 0, 1, None,
+                                  None) == nyion_hip.ERR_NO_DEVICE
     assert L.gpu_attention_device(None, None, None, None, 32, 4, 128, 64, 128) == -1
     assert L.mojo_stokes_init(64) is None
 

@@ -106,3 +106,165 @@ def test_prefill_writes_paged_kv(gpu, kv_dtype):
     else:
         assert np.array_equal(kh, oracle.q4_quantize_rows(kb))
         assert np.array_equal(vh, oracle.q4_quantize_rows(vb))
+
+
+# ---------------------------------------------------------------------------
+# chunked prefill after a cached prefix (pos_offset > 0)
+# ---------------------------------------------------------------------------
+
+def to_dev_bf16(x):
+    return torch.from_numpy(W.bf16_bits(x).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def run_prefill_ctx(gpu, q, k, v, kh, vh, causal=True, **kw):
+    n, hq, d = q.shape
+    hkv = k.shape[1]
+    out = torch.full((n, hq, d), float("nan"), device="cuda")
+    dkh = None if kh is None else to_dev_bf16(kh)
+    dvh = None if vh is None else to_dev_bf16(vh)
+    gpu.prefill_bf16_ctx(to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), dkh, dvh, out, hq, hkv,
+                         d, causal=causal, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_ctx_rows(q, k, v, kh, vh, rows, causal=True):
+    """Row i of the chunk is query position n_hist + i over the history followed
+    by the chunk: ops::attention with seq_len = n_hist + i + 1 (causal) or
+    n_hist + n (non-causal), on bf16-rounded inputs."""
+    n, hq, d = q.shape
+    hkv = k.shape[1]
+    nh = kh.shape[0]
+    kall = W.bf16_round(np.concatenate([kh, k]))
+    vall = W.bf16_round(np.concatenate([vh, v]))
+    lay = oracle.token_major_layout(kall, vall, hkv, d)
+    qb = W.bf16_round(q)
+    out = np.zeros_like(q)
+    if causal:
+        qall = np.zeros((nh + n, hq * d), dtype=np.float32)
+        qall[nh:] = qb.reshape(n, -1)
+        res = oracle.attention_rows(qall, lay, np.asarray(rows) + nh, hq, hkv, d,
+                                    threads=oracle.max_threads())
+        out[rows] = res[np.asarray(rows) + nh].reshape(-1, hq, d)
+        return out
+    for r in rows:
+        out[r] = oracle.attention(qb[r].reshape(-1), lay, nh + n, nh + n - 1, hq, hkv, d,
+                                  threads=oracle.max_threads()).reshape(hq, d)
+    return out
+
+
+@pytest.mark.parametrize("n_hist,n,hq,hkv,d", [(1, 64, 8, 2, 128), (63, 130, 8, 2, 128),
+                                               (64, 1, 4, 4, 64), (100, 97, 2, 1, 64),
+                                               (257, 300, 16, 2, 128), (640, 33, 8, 8, 128)])
+def test_prefill_ctx_all_rows(gpu, n_hist, n, hq, hkv, d):
+    """History lengths on, just off and far from the 64-key tile edge, chunks of
+    one row to several row blocks."""
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=n + n_hist)
+    _, kh, vh = W.prefill_inputs(n_hist, hq, hkv, d, seed=7 * n_hist + 1)
+    got = run_prefill_ctx(gpu, q, k, v, kh, vh)
+    rows = np.arange(n)
+    check(got, oracle_ctx_rows(q, k, v, kh, vh, rows), rows,
+          f"ctx {n_hist}+{n},{hq}/{hkv},{d}")
+
+
+def test_prefill_ctx_non_causal(gpu):
+    q, k, v = W.prefill_inputs(100, 8, 2, 128, seed=11)
+    _, kh, vh = W.prefill_inputs(77, 8, 2, 128, seed=12)
+    got = run_prefill_ctx(gpu, q, k, v, kh, vh, causal=False)
+    rows = np.array([0, 1, 50, 98, 99])
+    check(got, oracle_ctx_rows(q, k, v, kh, vh, rows, causal=False), rows, "ctx non-causal")
+
+
+def test_prefill_ctx_without_history_is_plain_prefill(gpu):
+    """n_hist = 0 runs the same kernel path as nyion_prefill_attention_bf16:
+    bit-identical outputs."""
+    q, k, v = W.prefill_inputs(300, 8, 2, 128, seed=13)
+    a = run_prefill(gpu, q, k, v)
+    b = run_prefill_ctx(gpu, q, k, v, None, None)
+    assert np.array_equal(a, b)
+
+
+def test_prefill_ctx_rejects_missing_history(gpu):
+    q, k, v = (to_dev_bf16(x) for x in W.prefill_inputs(8, 4, 4, 64, seed=1))
+    out = torch.empty((8, 4, 64), device="cuda")
+    rc = gpu.load().nyion_prefill_attention_bf16_ctx(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, 5, 8, 4, 4, 64, 1, 0.0,
+        out.data_ptr(), None, None, None, 16, 0, 0, 0, None)
+    assert rc != 0 and "history" in gpu.last_error()
+
+
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4])
+def test_chunked_prefill_through_paged_cache(gpu, kv_dtype):
+    """prefill_slice over a 520-token prompt in chunks of 200, 200, 120: each
+    chunk writes its K/V into the paged cache, the next chunk's history is
+    gathered back from the cache (bf16) and attended.  With an f32 cache every
+    row matches the one-shot oracle over the whole prompt; with Q4-20B the
+    history is the quantised cache, as ops::attention reads it."""
+    hq, hkv, d, bt = 8, 2, 128, 16
+    chunks = [200, 200, 120]
+    total = sum(chunks)
+    q, k, v = W.prefill_inputs(total, hq, hkv, d, seed=21)
+    nb = (total + bt - 1) // bt + 2
+    table_np = np.random.default_rng(22).permutation(nb).astype(np.int32)
+    table = torch.from_numpy(table_np).cuda()
+    rb = d if kv_dtype == oracle.KV_F32 else oracle.q4_row_bytes(d)
+    dt = torch.float32 if kv_dtype == oracle.KV_F32 else torch.uint8
+    kp = torch.zeros((nb, hkv, bt, rb), dtype=dt, device="cuda")
+    vp = torch.zeros_like(kp)
+    got = np.zeros_like(q)
+    pos = 0
+    for c in chunks:
+        sl = slice(pos, pos + c)
+        kh = vh = None
+        if pos:
+            kh = torch.empty((pos, hkv, d), dtype=torch.bfloat16, device="cuda")
+            vh = torch.empty_like(kh)
+            gpu.kv_gather_bf16(kp, table, bt, hkv, d, kv_dtype, pos, kh)
+            gpu.kv_gather_bf16(vp, table, bt, hkv, d, kv_dtype, pos, vh)
+        out = torch.full((c, hq, d), float("nan"), device="cuda")
+        gpu.prefill_bf16_ctx(to_dev_bf16(q[sl]), to_dev_bf16(k[sl]), to_dev_bf16(v[sl]), kh, vh,
+                             out, hq, hkv, d, k_pool=kp, v_pool=vp, block_table=table,
+                             block_tokens=bt, kv_dtype=kv_dtype)
+        torch.cuda.synchronize()
+        got[sl] = out.cpu().numpy()
+        pos += c
+    rows = np.arange(total)
+    if kv_dtype == oracle.KV_F32:
+        check(got, oracle_rows(q, k, v, rows), rows, "chunked f32")
+        return
+    # Q4: history keys/values are the dequantised cache rows
+    kq = oracle.q4_dequant_rows(oracle.q4_quantize_rows(W.bf16_round(k)), d)
+    vq = oracle.q4_dequant_rows(oracle.q4_quantize_rows(W.bf16_round(v)), d)
+    pos = 0
+    for c in chunks:
+        sl = slice(pos, pos + c)
+        r = np.arange(c)
+        ref = oracle_ctx_rows(q[sl], k[sl], v[sl], kq[:pos], vq[:pos], r)
+        check(got[sl], ref, r, f"chunked q4 at {pos}")
+        pos += c
+
+
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4])
+def test_kv_gather_bf16_bit_exact(gpu, kv_dtype):
+    """bf16 gather = round-to-nearest-even of the f32 gather (dequantised for
+    Q4-20B), token-major."""
+    hkv, d, bt, n = 4, 64, 16, 150
+    _, k, _ = W.prefill_inputs(n, 4, hkv, d, seed=31)
+    nb = (n + bt - 1) // bt + 1
+    table_np = np.random.default_rng(32).permutation(nb).astype(np.int32)
+    table = torch.from_numpy(table_np).cuda()
+    t = np.arange(n)
+    if kv_dtype == oracle.KV_F32:
+        pool = np.zeros((nb, hkv, bt, d), np.float32)
+        pool[table_np[t // bt], :, t % bt] = k
+        rows = k
+    else:
+        pool = np.zeros((nb, hkv, bt, oracle.q4_row_bytes(d)), np.uint8)
+        pool[table_np[t // bt], :, t % bt] = oracle.q4_quantize_rows(k)
+        rows = oracle.q4_dequant_rows(oracle.q4_quantize_rows(k), d)
+    dpool = torch.from_numpy(pool).cuda()
+    out = torch.empty((n, hkv, d), dtype=torch.bfloat16, device="cuda")
+    gpu.kv_gather_bf16(dpool, table, bt, hkv, d, kv_dtype, n, out)
+    torch.cuda.synchronize()
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, W.bf16_bits(rows))
