@@ -121,16 +121,21 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, halfx2{(_Float16)lo, (_Float16)hi});
 }
 
-// One tile's K and V in registers between its global loads and its LDS
+// One tile's K (or V) in registers between its global loads and its LDS
 // stores (K chunk u: key (tid+NT*u) / (D/8); V unit u: key pair and 8 dims).
+// K is staged one tile ahead of V.
 template <int D>
-struct TileStage {
+struct KStage {
     static constexpr int NT = prefill_threads<D>();
-    static constexpr int KLOADS = BN * (D / 8) / NT;
-    static constexpr int VUNITS = (BN / 2) * (D / 8) / NT;
-    u32x4 k[KLOADS];
-    u32x4 v0[VUNITS];
-    u32x4 v1[VUNITS];
+    static constexpr int LOADS = BN * (D / 8) / NT;
+    u32x4 k[LOADS];
+};
+template <int D>
+struct VStage {
+    static constexpr int NT = prefill_threads<D>();
+    static constexpr int UNITS = (BN / 2) * (D / 8) / NT;
+    u32x4 v0[UNITS];
+    u32x4 v1[UNITS];
 };
 
 // Loads of the tile whose first key is token kt of a source of n tokens
@@ -140,39 +145,46 @@ struct TileStage {
 // base plus constant steps; only a tile that reaches outside [0, n) clamps
 // K rows and zeroes V rows.
 template <int D>
-__device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kbase,
-                                           const uint16_t* vbase, int tok_stride, int n, int kt,
-                                           int tid) {
+__device__ __forceinline__ void stage_load_k(KStage<D>& st, const uint16_t* kbase, int tok_stride,
+                                             int n, int kt, int tid) {
     constexpr int CPR = D / 8;
-    const uint16_t* kp = kbase + (long long)kt * tok_stride;
-    const uint16_t* vp = vbase + (long long)kt * tok_stride;
-    const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);            // chunk u adds u*NT/CPR keys
-    const int v_off = 2 * (tid % (BN / 2)) * tok_stride + 8 * (tid / (BN / 2));  // unit u adds NT/4 dims
+    constexpr int STEP = KStage<D>::NT / CPR;  // keys between a thread's chunks
     if (kt >= 0 && kt + BN <= n) {
+        const uint16_t* kp = kbase + (long long)kt * tok_stride;
+        const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);
 #pragma unroll
-        for (int u = 0; u < TileStage<D>::KLOADS; u++)
-            st.k[u] = *(const u32x4*)(kp + k_off + u * (TileStage<D>::NT / CPR) * tok_stride);
+        for (int u = 0; u < KStage<D>::LOADS; u++)
+            st.k[u] = *(const u32x4*)(kp + k_off + u * STEP * tok_stride);
+        return;
+    }
 #pragma unroll
-        for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-            st.v0[u] = *(const u32x4*)(vp + v_off + 8 * (TileStage<D>::NT / (BN / 2)) * u);
-            st.v1[u] = *(const u32x4*)(vp + v_off + 8 * (TileStage<D>::NT / (BN / 2)) * u + tok_stride);
+    for (int u = 0; u < KStage<D>::LOADS; u++) {
+        const int t = min(max(kt + tid / CPR + u * STEP, 0), n - 1);  // outside: finite, masked
+        st.k[u] = *(const u32x4*)(kbase + (long long)t * tok_stride + 8 * (tid % CPR));
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_load_v(VStage<D>& st, const uint16_t* vbase, int tok_stride,
+                                             int n, int kt, int tid) {
+    constexpr int STEP = 8 * (VStage<D>::NT / (BN / 2));  // dims between a thread's units
+    const int t = kt + 2 * (tid % (BN / 2));
+    const int d0 = 8 * (tid / (BN / 2));
+    if (kt >= 0 && kt + BN <= n) {
+        const uint16_t* vp = vbase + (long long)t * tok_stride + d0;
+#pragma unroll
+        for (int u = 0; u < VStage<D>::UNITS; u++) {
+            st.v0[u] = *(const u32x4*)(vp + STEP * u);
+            st.v1[u] = *(const u32x4*)(vp + STEP * u + tok_stride);
         }
         return;
     }
 #pragma unroll
-    for (int u = 0; u < TileStage<D>::KLOADS; u++) {
-        const int key = tid / CPR + u * (TileStage<D>::NT / CPR);
-        const int t = min(max(kt + key, 0), n - 1);  // keys outside: finite values, masked
-        st.k[u] = *(const u32x4*)(kbase + (long long)t * tok_stride + 8 * (tid % CPR));
-    }
-#pragma unroll
-    for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-        const int t = kt + 2 * (tid % (BN / 2));
-        const int dc = tid / (BN / 2) + u * (TileStage<D>::NT / (BN / 2));
-        st.v0[u] = t >= 0 && t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + 8 * dc)
+    for (int u = 0; u < VStage<D>::UNITS; u++) {
+        st.v0[u] = t >= 0 && t < n ? *(const u32x4*)(vbase + (long long)t * tok_stride + d0 + STEP * u)
                                    : u32x4{0, 0, 0, 0};
         st.v1[u] = t + 1 >= 0 && t + 1 < n
-                       ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + 8 * dc)
+                       ? *(const u32x4*)(vbase + (long long)(t + 1) * tok_stride + d0 + STEP * u)
                        : u32x4{0, 0, 0, 0};
     }
 }
@@ -181,28 +193,39 @@ __device__ __forceinline__ void stage_load(TileStage<D>& st, const uint16_t* kba
 // history, the rest from the chunk.  kt is uniform, so the selects are
 // scalar and one copy of the loads serves both sources.
 template <int D>
-__device__ __forceinline__ void load_tile(TileStage<D>& st, const PrefillArgs& a,
-                                          const uint16_t* kbase, const uint16_t* vbase,
-                                          const uint16_t* khbase, const uint16_t* vhbase,
-                                          int tok_stride, int kt, int tid) {
+__device__ __forceinline__ void load_k_tile(KStage<D>& st, const PrefillArgs& a,
+                                            const uint16_t* kbase, const uint16_t* khbase,
+                                            int tok_stride, int kt, int tid) {
     const bool hist = kt < 0;
-    stage_load<D>(st, hist ? khbase : kbase, hist ? vhbase : vbase, tok_stride,
-                  hist ? a.n_hist : a.n, hist ? kt + a.n_hist : kt, tid);
+    stage_load_k<D>(st, hist ? khbase : kbase, tok_stride, hist ? a.n_hist : a.n,
+                    hist ? kt + a.n_hist : kt, tid);
+}
+template <int D>
+__device__ __forceinline__ void load_v_tile(VStage<D>& st, const PrefillArgs& a,
+                                            const uint16_t* vbase, const uint16_t* vhbase,
+                                            int tok_stride, int kt, int tid) {
+    const bool hist = kt < 0;
+    stage_load_v<D>(st, hist ? vhbase : vbase, tok_stride, hist ? a.n_hist : a.n,
+                    hist ? kt + a.n_hist : kt, tid);
 }
 
 template <int D>
-__device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned char* base, int tid) {
+__device__ __forceinline__ void stage_store_k(const KStage<D>& st, unsigned char* kslot, int tid) {
     using L = PrefillLds<D>;
     constexpr int CPR = D / 8;
 #pragma unroll
-    for (int u = 0; u < TileStage<D>::KLOADS; u++) {
-        const int id = tid + TileStage<D>::NT * u;
-        *(u32x4*)(base + (id / CPR) * L::KROW + 16 * (id % CPR)) = st.k[u];
+    for (int u = 0; u < KStage<D>::LOADS; u++) {
+        const int id = tid + KStage<D>::NT * u;
+        *(u32x4*)(kslot + (id / CPR) * L::KROW + 16 * (id % CPR)) = st.k[u];
     }
-    unsigned char* vt = base + L::KBYTES;
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char* vslot, int tid) {
+    using L = PrefillLds<D>;
 #pragma unroll
-    for (int u = 0; u < TileStage<D>::VUNITS; u++) {
-        const int id = tid + TileStage<D>::NT * u;
+    for (int u = 0; u < VStage<D>::UNITS; u++) {
+        const int id = tid + VStage<D>::NT * u;
         const int key = 2 * (id % (BN / 2));
         const int dc = id / (BN / 2);
         const int col = (key & ~15) + vt_pos(key & 15);  // even: keys key, key+1
@@ -214,7 +237,7 @@ __device__ __forceinline__ void stage_store(const TileStage<D>& st, unsigned cha
             const uint32_t x0 = st.v0[u][e >> 1], x1 = st.v1[u][e >> 1];
             const float lo = __uint_as_float((e & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
             const float hi = __uint_as_float((e & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
-            *(uint32_t*)(vt + (8 * dc + e) * L::VROW + 2 * col) = pack_f16x2(lo, hi);
+            *(uint32_t*)(vslot + (8 * dc + e) * L::VROW + 2 * col) = pack_f16x2(lo, hi);
         }
     }
 }
@@ -226,7 +249,8 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     constexpr int DT = D / 32;  // output dim tiles
     constexpr int KS = D / 16;  // k-steps of the S product
 
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * L::BUF];
+    // three K slots, then two V^T slots
+    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * L::KBYTES + 2 * L::VBYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -276,73 +300,61 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     float mrun = -1e30f;  // finite: exp2(s - mrun) of a masked s is 0, never NaN
     float lrun = 0.f;
 
-    // Per-thread roles in staging a tile (fixed for the whole loop).
-    //   K: chunk id = tid + NT*u -> key id / CPR, chunk id % CPR
-    //   V: unit id = tid + NT*u -> key pair id % (BN/2), dim chunk id / (BN/2)
     const uint16_t* kbase = a.k + (long long)g * D;
     const uint16_t* vbase = a.v + (long long)g * D;
     const uint16_t* khbase = a.kh + (long long)g * D;
     const uint16_t* vhbase = a.vh + (long long)g * D;
     const int tok_stride = a.n_kv_heads * D;
-    TileStage<D> stg;
+    unsigned char* const kslot0 = lds;
+    unsigned char* const vslot0 = lds + 3 * L::KBYTES;
+    KStage<D> kst;
+    VStage<D> vst;
 
-    // One 32-key half kb of the tile in buffer `buf`: S^T, online softmax,
-    // O += P.V over its two 16-key k-steps.
-    // S^T of 32-key half kb of the tile in buffer `buf` (K rows kb*32 + j,
+    // S^T of 32-key half kb of the tile in K slot `ks` (K rows kb*32 + j,
     // chunk 2s + h)
-    auto scores_half = [&](int buf, int kb) {
-        const unsigned char* kp = lds + buf * L::BUF + (kb * 32 + j) * L::KROW + 16 * h;
-        // all K fragments of the half are requested before the first MFMA
-        bf16x8 kf[KS];
-#pragma unroll
-        for (int s = 0; s < KS; s++) kf[s] = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * s));
-        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMA chain
+    auto scores_half = [&](const unsigned char* ks, int kb) {
+        const unsigned char* kp = ks + (kb * 32 + j) * L::KROW + 16 * h;
         floatx16 st = floatx16{};
 #pragma unroll
-        for (int s = 0; s < KS; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qreg[s], st, 0, 0, 0);
+        for (int s0_ = 0; s0_ < KS; s0_ += 4) {
+            bf16x8 kf[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) kf[s] = __builtin_bit_cast(bf16x8, *(const uint4*)(kp + 32 * (s0_ + s)));
+#pragma unroll
+            for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s], qreg[s0_ + s], st, 0, 0, 0);
+        }
         return st;
     };
-    // Online softmax of half kb and O += P.V over its two 16-key k-steps.
-    auto consume_half = [&](floatx16 st, int buf, int kt, int kb, bool masked) {
-        const unsigned char* base = lds + buf * L::BUF;
-        // B operands of the PV product (V^T row 32dt + j, the 8 keys of k-step
-        // t = 2kb + t2), requested first: they do not depend on P, so their
-        // LDS latency hides behind the softmax
-        const unsigned char* vp = base + L::KBYTES + j * L::VROW + 16 * h + 64 * kb;
-        halfx8 vb[2][DT];
+
+    // Online softmax of half kb of the tile at key kt and O += P.V over its
+    // two 16-key k-steps (V^T from slot `vs`).  Lane holds row row0+j, keys
+    // kt + 32kb + 8(r/4) + 4h + r%4 in st[r].  The O rescale of a moved max
+    // comes after the exps, so that the softmax up to there has no branch
+    // and can interleave with the MFMAs issued before it.
+    // Causal / range mask of half kb of the tile at key kt: the key of
+    // st[r] is kt + 32kb + 4h + c(r), c(r) = 8(r/4) + r%4, compared as the
+    // constant c(r) against this lane's bounds.
+    auto mask_half = [&](floatx16& st, int kt, int kb) {
+        const int hi = lim - kt - 32 * kb - 4 * h;
+        const int lo = key_lo - kt - 32 * kb - 4 * h;
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-                vb[t2][dt] = __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
-        __builtin_amdgcn_sched_barrier(0);
-        // mask (raw scores); lane holds row row0+j, keys kt + 32kb + 8(r/4) + 4h + r%4
-        if (masked) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                st[r] = key <= lim && key >= key_lo ? st[r] : -INFINITY;
-            }
+        for (int r = 0; r < 16; r++) {
+            const int c = 8 * (r >> 2) + (r & 3);
+            st[r] = c <= hi && c >= lo ? st[r] : -INFINITY;
         }
+    };
+    auto consume_half = [&](floatx16 st, const unsigned char* vs, int kb) {
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
         mt = max_xor32(mt) * a.scale_log2;  // scale > 0: max commutes
         // the running max (log2 units, scaled) moves only when some row's max
         // exceeds it by more than 2^8, so most halves skip the O rescale
-        if (__any(mt > mrun + kPrefillRescaleLog2)) {
-            const float mnew = fmaxf(mrun, mt);
-            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-            mrun = mnew;
-            lrun *= alpha;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                // O reg r of this lane is row 8(r/4) + 4h + r%4
-                const float ar = __shfl(alpha, 8 * (r >> 2) + 4 * h + (r & 3));
-#pragma unroll
-                for (int t = 0; t < DT; t++) o[t][r] *= ar;
-            }
-        }
+        const bool moved = __any(mt > mrun + kPrefillRescaleLog2);
+        const float mnew = moved ? fmaxf(mrun, mt) : mrun;
+        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+        mrun = mnew;
+        lrun *= alpha;
         // p = exp2(s*scale - m), one FMA + one exp per score, converted to
         // fp16 pairs; the row sum adds the same fp16 values the PV product
         // uses (v_dot2 against (1, 1)).  A operands of the PV product: k-step
@@ -363,35 +375,86 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
                 pa[t2][e + 1] = pp[1];
             }
         lrun += psum;
+        // B operands of the PV product: V^T row 32dt + j, the 8 keys of
+        // k-step t = 2kb + t2
+        const unsigned char* vp = vs + j * L::VROW + 16 * h + 64 * kb;
+        if (moved) {
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
+            for (int r = 0; r < 16; r++) {
+                // O reg r of this lane is row 8(r/4) + 4h + r%4
+                const float ar = __shfl(alpha, 8 * (r >> 2) + 4 * h + (r & 3));
+#pragma unroll
+                for (int t = 0; t < DT; t++) o[t][r] *= ar;
+            }
+        }
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+            halfx8 vb[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[t2][dt], o[dt], 0, 0, 0);
-    };
-
-    load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt0, tid);
-    stage_store<D>(stg, lds, tid);
-    __syncthreads();
-    if (n_tiles > 1) load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt0 + BN, tid);
-    for (int it = 0; it < n_tiles; it++) {
-        const int kt = kt0 + it * BN;
-        const int cur = it & 1;
-        const bool masked = (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0) || kt < key_lo;
-        // both halves' S first: the second chain of MFMAs has no dependence
-        // on the first half's softmax, so the two overlap
-        const floatx16 s0 = scores_half(cur, 0);
-        const floatx16 s1 = scores_half(cur, 1);
-        consume_half(s0, cur, kt, 0, masked);
-        consume_half(s1, cur, kt, 1, masked);
-        // stage the next tile into the other buffer (last read one tile ago,
-        // before the previous barrier) and start loading the one after
-        if (it + 1 < n_tiles) {
-            stage_store<D>(stg, lds + (cur ^ 1) * L::BUF, tid);
-            if (it + 2 < n_tiles)
-                load_tile<D>(stg, a, kbase, vbase, khbase, vhbase, tok_stride, kt + 2 * BN, tid);
+                vb[dt] = __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[dt], o[dt], 0, 0, 0);
         }
+    };
+    auto tile_masked = [&](int kt) {
+        return (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0) || kt < key_lo;
+    };
+    auto kslot = [&](int it) { return kslot0 + (it % 3) * L::KBYTES; };
+
+    // Pipeline over 32-key halves: the S MFMAs of the next half are issued
+    // before the softmax of the current one, so the matrix and vector pipes
+    // have independent work.  At the top of iteration it: K slots hold
+    // tiles it and it+1, V slot it&1 holds tile it, s0 = S of tile it's
+    // first half, and the staging registers hold K of tile it+2 and V of
+    // tile it+1.  The iteration writes the staged K into the slot of tile
+    // it-1 and the staged V into the other V slot (both last read one
+    // iteration ago), issues the next global loads and synchronises once.
+    load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0, tid);
+    load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0, tid);
+    stage_store_k<D>(kst, kslot0, tid);
+    stage_store_v<D>(vst, vslot0, tid);
+    if (n_tiles > 1) {
+        load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + BN, tid);
+        stage_store_k<D>(kst, kslot0 + L::KBYTES, tid);
+    }
+    __syncthreads();
+    floatx16 s0 = scores_half(kslot0, 0);
+    if (n_tiles > 2) load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + 2 * BN, tid);
+    if (n_tiles > 1) load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0 + BN, tid);
+
+    auto step = [&](int it, bool masked) {
+        const int kt = kt0 + it * BN;
+        const unsigned char* vs = vslot0 + (it & 1) * L::VBYTES;
+        if (masked) mask_half(s0, kt, 0);
+        floatx16 s1 = scores_half(kslot(it), 1);
+        consume_half(s0, vs, 0);
+        s0 = scores_half(kslot(it + 1), 0);
+        if (masked) mask_half(s1, kt, 1);
+        consume_half(s1, vs, 1);
+        // a slot past the last tile is written and never read
+        stage_store_k<D>(kst, kslot(it + 2), tid);
+        stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid);
+        if (it + 3 < n_tiles) load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt + 3 * BN, tid);
+        if (it + 2 < n_tiles) load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt + 2 * BN, tid);
         __syncthreads();
+    };
+    int it = 0;
+    if (n_tiles > 1 && tile_masked(kt0)) step(it++, true);  // partial first history tile
+    for (; it + 1 < n_tiles && !tile_masked(kt0 + it * BN); it++) step(it, false);
+    for (; it + 1 < n_tiles; it++) step(it, true);
+    {
+        const int it = n_tiles - 1;
+        const int kt = kt0 + it * BN;
+        const unsigned char* vs = vslot0 + (it & 1) * L::VBYTES;
+        floatx16 s1 = scores_half(kslot(it), 1);
+        if (tile_masked(kt)) {
+            mask_half(s0, kt, 0);
+            mask_half(s1, kt, 1);
+        }
+        consume_half(s0, vs, 0);
+        consume_half(s1, vs, 1);
     }
 
     // epilogue: divide by the row sums and store
