@@ -331,6 +331,36 @@ int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out
 int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* out,
                       nyion_stream_t stream);
 
+/* ------------------------------------------------------ Q4_K weight GEMV */
+
+/* out[r] = sum_j W[r][j] x[j] for a GGUF Q4_K matrix W (n_rows rows of
+ * n_cols/256 blocks of 144 bytes: f16 d, f16 dmin, 12 bytes of 6-bit
+ * scales/mins, 128 nibble bytes), f32 x and out, all device memory.
+ * Replaces swamp_fused_gemv_q4k / fused_gemv_q4k
+ * (swamp-kernels/src/fused_gemv_q4k.rs:59-99, 903-927), the Q4_K arm of
+ * forward_linear (swamp-engine/src/linear.rs:99-189), with the f32
+ * semantics of its scalar path (395-448).  n_cols a positive multiple of
+ * 256; W and x 16-byte aligned.  out is written, not accumulated. */
+int nyion_gemv_q4k(const uint8_t* d_w, const float* d_x, float* d_out, int n_rows, int n_cols,
+                   nyion_stream_t stream);
+
+/* Up to four matrices of n_cols columns that share x in one launch
+ * (fused_gemv_q4k_multi, fused_gemv_q4k.rs:330-390; the executor's q/k/v
+ * and gate/up projections).  d_ws, d_outs, row_counts are host arrays of
+ * n_mats entries. */
+int nyion_gemv_q4k_multi(const uint8_t* const* d_ws, const float* d_x, float* const* d_outs,
+                         const int32_t* row_counts, int n_mats, int n_cols,
+                         nyion_stream_t stream);
+
+/* batch inputs against one matrix, W read once per four inputs
+ * (fused_gemv_q4k_batched, fused_gemv_q4k.rs:456-485, the Q4_K arm of
+ * forward_linear_batch, linear.rs:301-354): x [batch][x_stride] (x_stride
+ * >= n_cols, a multiple of 4), out [batch][out_stride] (>= n_rows).  Each
+ * output row equals nyion_gemv_q4k of its input bit for bit. */
+int nyion_gemv_q4k_batched(const uint8_t* d_w, const float* d_x, int64_t x_stride, float* d_out,
+                           int64_t out_stride, int n_rows, int n_cols, int batch,
+                           nyion_stream_t stream);
+
 /* --------------------------------------------------------- HMA arena */
 
 /* The HeterogeneousMemoryAllocator contract (swamp-tensors/src/hma.rs:5-9,

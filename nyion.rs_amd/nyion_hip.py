@@ -102,6 +102,9 @@ SIGNATURES = {
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_kv_gather_bf16": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_gemv_q4k": (i32, [vp, vp, vp, i32, i32, vp]),
+    "nyion_gemv_q4k_multi": (i32, [vp, vp, vp, vp, i32, i32, vp]),
+    "nyion_gemv_q4k_batched": (i32, [vp, vp, i64, vp, i64, i32, i32, i32, vp]),
     "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
     "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
                                    i32, i32, i32, vp]),
@@ -471,3 +474,34 @@ def kv_gather_bf16(pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dty
                                      n_kv_heads, head_dim, kv_dtype, n_tokens, ptr(out),
                                      stream_handle(stream))
     check(rc, "nyion_kv_gather_bf16")
+
+
+# ----------------------------------------------------------------------------
+# Q4_K weight GEMV
+# ----------------------------------------------------------------------------
+
+Q4K_BLOCK = 256
+Q4K_BYTES = 144
+
+
+def gemv_q4k(w, x, out, n_rows, n_cols, stream=None):
+    """w: device uint8 [n_rows][n_cols/256*144]; x [n_cols] f32; out [n_rows] f32."""
+    check(load().nyion_gemv_q4k(ptr(w), ptr(x), ptr(out), n_rows, n_cols, stream_handle(stream)),
+          "nyion_gemv_q4k")
+
+
+def gemv_q4k_multi(ws, x, outs, n_cols, stream=None):
+    """Several Q4_K matrices sharing x: ws, outs lists of device tensors."""
+    n = len(ws)
+    wa = (C.c_void_p * n)(*[w.data_ptr() for w in ws])
+    oa = (C.c_void_p * n)(*[o.data_ptr() for o in outs])
+    rows = (C.c_int32 * n)(*[int(o.shape[-1]) for o in outs])
+    check(load().nyion_gemv_q4k_multi(wa, ptr(x), oa, rows, n, n_cols, stream_handle(stream)),
+          "nyion_gemv_q4k_multi")
+
+
+def gemv_q4k_batched(w, x, out, n_rows, n_cols, stream=None):
+    """x [batch][>= n_cols] f32, out [batch][>= n_rows] f32 (row-major, strided)."""
+    check(load().nyion_gemv_q4k_batched(ptr(w), ptr(x), x.stride(0), ptr(out), out.stride(0),
+                                        n_rows, n_cols, x.shape[0], stream_handle(stream)),
+          "nyion_gemv_q4k_batched")

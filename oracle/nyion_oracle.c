@@ -670,3 +670,80 @@ void orc_apply_rope(float* q, float* k, int pos, int n_heads, int n_kv_heads, in
     rope_rows(q, n_heads, head_dim, cs);
     rope_rows(k, n_kv_heads, head_dim, cs);
 }
+
+/* ------------------------------------------------------------------ Q4_K */
+
+/* swamp-kernels/src/fused_gemv_q4k.rs:30-43 (unpack_scales_q4k): 12 bytes
+ * -> eight 6-bit scales and mins. */
+void orc_q4k_unpack_scales(const uint8_t* sc, uint8_t* scales, uint8_t* mins) {
+    for (int j = 0; j < 4; j++) {
+        scales[j] = sc[j] & 63;
+        mins[j] = sc[j + 4] & 63;
+    }
+    for (int j = 4; j < 8; j++) {
+        scales[j] = (uint8_t)((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
+        mins[j] = (uint8_t)((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+    }
+}
+
+/* One 144-byte block -> 256 weights, as the scalar GEMV forms them
+ * (fused_gemv_q4k.rs:395-448): w = (d * scale) * q - (dmin * min), the two
+ * products rounded to f32 first; qs pair p holds sub-block 2p in its low
+ * nibbles and 2p+1 in its high nibbles. */
+void orc_q4k_dequant_block(const uint8_t* blk, float* out) {
+    const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    const float dmin = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+    uint8_t scales[8], mins[8];
+    orc_q4k_unpack_scales(blk + 4, scales, mins);
+    const uint8_t* qs = blk + 16;
+    for (int pair = 0; pair < 4; pair++) {
+        const uint8_t* qb = qs + pair * 32;
+        const int se = pair * 2, so = pair * 2 + 1;
+        const float sve = d * (float)(scales[se] & 0x3F), mve = dmin * (float)(mins[se] & 0x3F);
+        const float svo = d * (float)(scales[so] & 0x3F), mvo = dmin * (float)(mins[so] & 0x3F);
+        for (int i = 0; i < 32; i++) {
+            out[se * 32 + i] = sve * (float)(qb[i] & 0x0F) - mve;
+            out[so * 32 + i] = svo * (float)(qb[i] >> 4) - mvo;
+        }
+    }
+}
+
+/* fused_gemv_q4k_scalar (fused_gemv_q4k.rs:395-448), same accumulation
+ * order: per row one f32 accumulator over blocks, pairs, the even
+ * sub-block's 32 products then the odd one's. */
+int orc_gemv_q4k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols) {
+    if (n_cols <= 0 || n_cols % 256 || n_rows < 0) return -1;
+    const int nb = n_cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int row = 0; row < n_rows; row++) {
+        float acc = 0.0f;
+        for (int blk = 0; blk < nb; blk++) {
+            const uint8_t* b = w + ((size_t)row * nb + blk) * 144;
+            const float d = orc_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            const float dmin = orc_f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+            uint8_t scales[8], mins[8];
+            orc_q4k_unpack_scales(b + 4, scales, mins);
+            const uint8_t* qs = b + 16;
+            const float* xb = x + (size_t)blk * 256;
+            for (int pair = 0; pair < 4; pair++) {
+                const uint8_t* qb = qs + pair * 32;
+                const int se = pair * 2;
+                const float sve = d * (float)(scales[se] & 0x3F);
+                const float mve = dmin * (float)(mins[se] & 0x3F);
+                for (int i = 0; i < 32; i++) {
+                    const float wf = sve * (float)(qb[i] & 0x0F) - mve;
+                    acc += wf * xb[se * 32 + i];
+                }
+                const int so = pair * 2 + 1;
+                const float svo = d * (float)(scales[so] & 0x3F);
+                const float mvo = dmin * (float)(mins[so] & 0x3F);
+                for (int i = 0; i < 32; i++) {
+                    const float wf = svo * (float)(qb[i] >> 4) - mvo;
+                    acc += wf * xb[so * 32 + i];
+                }
+            }
+        }
+        out[row] = acc;
+    }
+    return 0;
+}

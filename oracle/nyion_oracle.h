@@ -30,6 +30,14 @@
  *                                              angles within f32 rounding,
  *                                              pos 0 identity, rotation
  *                                              preserves pair norms
+ *   orc_q4k_unpack_scales / _dequant_block   : the reference's own block
+ *                                              builder (fused_gemv_q4k.rs:812-
+ *                                              828) round-tripped, and a numpy
+ *                                              restatement of the 12-byte packing
+ *   orc_gemv_q4k                             : closed form of the reference test
+ *                                              weights (constant nibble 8,
+ *                                              fused_gemv_q4k.rs:830-845) and
+ *                                              float64 dequantise-then-dot
  * Bit-parity of attention outputs with the Rust binary (glibc expf order,
  * rayon scheduling of the importance sum) is unpinned and not required:
  * attention parity is at tolerance.
@@ -128,6 +136,13 @@ int   orc_stokes_append(void* cache, int token_id, const float* key,
 void  orc_stokes_free(void* cache);
 int   orc_stokes_count(const void* cache);
 int   orc_stokes_read(const void* cache, float* keys, float* values, float* scores);
+
+/* Q4_K weights (GGUF 144-byte blocks of 256: f16 d, f16 dmin, 12 bytes of
+ * 6-bit scales/mins, 128 bytes of nibbles) and the scalar GEMV of
+ * swamp-kernels/src/fused_gemv_q4k.rs */
+void orc_q4k_unpack_scales(const uint8_t* sc, uint8_t* scales, uint8_t* mins);
+void orc_q4k_dequant_block(const uint8_t* blk, float* out);
+int  orc_gemv_q4k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols);
 
 int orc_max_threads(void);
 

@@ -57,6 +57,10 @@ def lib():
         L.orc_rope_lut.argtypes = [C.c_int, C.c_int, C.c_void_p]
         L.orc_apply_rope.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                                      C.c_int, C.c_void_p]
+        L.orc_q4k_unpack_scales.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_q4k_dequant_block.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_gemv_q4k.restype = C.c_int
+        L.orc_gemv_q4k.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         L.orc_dot_avx512_order.restype = C.c_float
         L.orc_dot_avx512_order.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
         L.orc_weighted_sum.argtypes = [C.c_void_p, C.c_void_p, C.c_float, C.c_int]
@@ -287,3 +291,38 @@ def exp_q16_16(x: int) -> int:
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ----------------------------------------------------------------------------
+# Q4_K weights (swamp-kernels/src/fused_gemv_q4k.rs)
+# ----------------------------------------------------------------------------
+
+Q4K_BLOCK = 256
+Q4K_BYTES = 144
+
+
+def q4k_unpack_scales(sc: np.ndarray):
+    sc = np.ascontiguousarray(sc, dtype=np.uint8)
+    scales = np.zeros(8, np.uint8)
+    mins = np.zeros(8, np.uint8)
+    lib().orc_q4k_unpack_scales(sc.ctypes.data, scales.ctypes.data, mins.ctypes.data)
+    return scales, mins
+
+
+def q4k_dequant(w: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    """Q4_K bytes [n_rows][n_cols/256 * 144] -> f32 [n_rows][n_cols]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, Q4K_BYTES)
+    out = np.empty((w.shape[0], Q4K_BLOCK), np.float32)
+    for i in range(w.shape[0]):
+        lib().orc_q4k_dequant_block(w[i].ctypes.data, out[i].ctypes.data)
+    return out.reshape(n_rows, n_cols)
+
+
+def gemv_q4k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert w.size == n_rows * (n_cols // Q4K_BLOCK) * Q4K_BYTES and x.size >= n_cols
+    out = np.empty(n_rows, np.float32)
+    if lib().orc_gemv_q4k(w.ctypes.data, x.ctypes.data, out.ctypes.data, n_rows, n_cols) != 0:
+        raise ValueError("orc_gemv_q4k: n_cols must be a positive multiple of 256")
+    return out

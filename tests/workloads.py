@@ -150,3 +150,82 @@ def brute_force_attention(q, k, v, valid_end, scale=None):
     p = np.exp(s)
     p /= p.sum()
     return p @ v
+
+
+# ---------------------------------------------------------------------------
+# Q4_K weights (GGUF 144-byte blocks, swamp-kernels/src/fused_gemv_q4k.rs)
+# ---------------------------------------------------------------------------
+
+def q4k_pack_scales(scales, mins) -> np.ndarray:
+    """Eight 6-bit scales and mins -> the 12 packed bytes (the inverse of
+    unpack_scales_q4k, fused_gemv_q4k.rs:30-43)."""
+    s = np.asarray(scales, dtype=np.uint8) & 63
+    m = np.asarray(mins, dtype=np.uint8) & 63
+    out = np.zeros(12, np.uint8)
+    out[0:4] = s[0:4] | ((s[4:8] >> 4) << 6)
+    out[4:8] = m[0:4] | ((m[4:8] >> 4) << 6)
+    out[8:12] = (s[4:8] & 0x0F) | ((m[4:8] & 0x0F) << 4)
+    return out
+
+
+def q4k_block(d, dmin, scales, mins, qs) -> np.ndarray:
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    b[4:16] = q4k_pack_scales(scales, mins)
+    b[16:144] = np.asarray(qs, dtype=np.uint8)
+    return b
+
+
+def q4k_random_weights(n_rows, n_cols, seed=0, d_range=(5e-5, 5e-4)) -> np.ndarray:
+    """Random Q4_K matrix [n_rows][n_cols/256 * 144] u8 with finite f16
+    d, dmin of realistic magnitude and uniform 6-bit scales, mins, nibbles."""
+    rng = np.random.default_rng(seed)
+    nb = n_rows * (n_cols // 256)
+    w = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    d = rng.uniform(*d_range, size=nb).astype(np.float16)
+    dmin = rng.uniform(0.0, d_range[1], size=nb).astype(np.float16)
+    w[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    w[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return w.reshape(n_rows, -1)
+
+
+def q4k_dequant_np(w: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    """numpy restatement of the Q4_K weight formula (f32 products as the
+    scalar GEMV rounds them): [n_rows][n_cols] f32."""
+    b = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, 144)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc = b[:, 4:16].astype(np.uint8)
+    scales = np.zeros((b.shape[0], 8), np.uint8)
+    mins = np.zeros((b.shape[0], 8), np.uint8)
+    scales[:, 0:4] = sc[:, 0:4] & 63
+    mins[:, 0:4] = sc[:, 4:8] & 63
+    scales[:, 4:8] = (sc[:, 8:12] & 0x0F) | ((sc[:, 0:4] >> 6) << 4)
+    mins[:, 4:8] = (sc[:, 8:12] >> 4) | ((sc[:, 4:8] >> 6) << 4)
+    qs = b[:, 16:144].reshape(-1, 4, 32)
+    q = np.zeros((b.shape[0], 8, 32), np.uint8)
+    q[:, 0::2, :] = qs & 0x0F
+    q[:, 1::2, :] = qs >> 4
+    sv = (d[:, None] * scales.astype(np.float32)).astype(np.float32)
+    mv = (dmin[:, None] * mins.astype(np.float32)).astype(np.float32)
+    wf = (sv[:, :, None] * q.astype(np.float32)).astype(np.float32) - mv[:, :, None]
+    return wf.astype(np.float32).reshape(n_rows, n_cols)
+
+
+def q4k_reference_test_weights(n_rows: int) -> np.ndarray:
+    """The weights of the reference's own GEMV tests (fused_gemv_q4k.rs:830-840):
+    one block per row, d = 0.5 + 0.1 r, dmin = 0.1 + 0.05 r, every scale
+    (r + 1) & 63, every min (r + 2) & 63, every nibble 8."""
+    rows = []
+    for r in range(n_rows):
+        d = np.float32(0.5) + np.float32(r) * np.float32(0.1)
+        dm = np.float32(0.1) + np.float32(r) * np.float32(0.05)
+        rows.append(q4k_block(d, dm, [(r + 1) & 63] * 8, [(r + 2) & 63] * 8, [8 | (8 << 4)] * 128))
+    return np.stack(rows)
+
+
+def q4k_reference_test_x(n_cols: int) -> np.ndarray:
+    """fused_gemv_q4k.rs:842-844: x_i = (i % 100) / 50 - 1."""
+    i = np.arange(n_cols)
+    return ((i % 100).astype(np.float32) / np.float32(50.0) - np.float32(1.0)).astype(np.float32)
