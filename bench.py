@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5 (default all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 512 MiB device copy (PMC traffic calibration)")
@@ -344,6 +344,94 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
             "tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
 
 
+def _q4k_random(torch, rows, cols, seed):
+    """Random Q4_K matrix on the device: uniform nibbles/scales, finite f16
+    d = dmin in [5e-5, 5e-4]."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    nb = cols // 256
+    w = torch.randint(0, 256, (rows, nb, 144), dtype=torch.uint8, device="cuda", generator=g)
+    d = (torch.rand((rows, nb), device="cuda", generator=g) * 4.5e-4 + 5e-5).half()
+    w[:, :, 0:2] = d.view(torch.uint8).view(rows, nb, 2)
+    w[:, :, 2:4] = d.view(torch.uint8).view(rows, nb, 2)
+    return w.view(rows, -1).contiguous()
+
+
+def _graph_us(torch, fn, reps):
+    """Mean replay time of fn captured in a HIP graph (no host overhead)."""
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        fn()
+    gph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        gph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1e3 / reps
+
+
+def bench_gemv(nh, torch, steps, warmup, cpu=True):
+    """Q4_K weight GEMV (the projections either side of decode attention):
+    the TinyLlama-1.1B decode step's 88 launches (per layer q/k/v in one
+    launch, o, gate/up in one launch, down; 22 layers, 545 MB of weights, so
+    the 256 MB MALL does not hold them) and Llama-3-8B-shaped gate/up
+    (2 x 14336 x 4096, 66 MB per launch, 8 layers rotated), both replayed
+    from HIP graphs."""
+    H, F, KV, L = 2048, 5632, 256, 22
+    lw = [{k: _q4k_random(torch, r, c, 7 * l + i) for i, (k, r, c) in enumerate(
+        [("q", H, H), ("k", KV, H), ("v", KV, H), ("o", H, H), ("g", F, H), ("u", F, H), ("d", H, F)])}
+        for l in range(L)]
+    x = torch.randn(H, device="cuda")
+    xf = torch.randn(F, device="cuda")
+    o = {k: torch.empty(n, device="cuda") for k, n in
+         dict(q=H, k=KV, v=KV, o=H, g=F, u=F, d=H).items()}
+    step_bytes = sum(t.numel() for w in lw for t in w.values())
+
+    def step():
+        for w in lw:
+            nh.gemv_q4k_multi([w["q"], w["k"], w["v"]], x, [o["q"], o["k"], o["v"]], H)
+            nh.gemv_q4k(w["o"], x, o["o"], H, H)
+            nh.gemv_q4k_multi([w["g"], w["u"]], x, [o["g"], o["u"]], H)
+            nh.gemv_q4k(w["d"], xf, o["d"], H, F)
+
+    reps = max(3, steps // 5)
+    step_us = _graph_us(torch, step, reps)
+    H8, F8, L8 = 4096, 14336, 8
+    big = [(_q4k_random(torch, F8, H8, 100 + l), _q4k_random(torch, F8, H8, 200 + l)) for l in range(L8)]
+    x8 = torch.randn(H8, device="cuda")
+    og, ou = torch.empty(F8, device="cuda"), torch.empty(F8, device="cuda")
+
+    def gateup():
+        for gw, uw in big:
+            nh.gemv_q4k_multi([gw, uw], x8, [og, ou], H8)
+
+    gu_us = _graph_us(torch, gateup, reps) / L8
+    gu_bytes = 2 * big[0][0].numel()
+    res = {"tinyllama_step_us": step_us, "tinyllama_step_bytes": step_bytes, "launches": 4 * L,
+           "tinyllama_step_gbs": step_bytes / step_us / 1e3,
+           "gateup_8b_us": gu_us, "gateup_8b_bytes": gu_bytes,
+           "gateup_8b_gbs": gu_bytes / gu_us / 1e3,
+           "gateup_8b_hbm_frac": gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS}
+    if cpu:
+        import oracle
+
+        wg = lw[0]["g"].cpu().numpy()
+        xc = x.cpu().numpy()
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < 2.0:
+            oracle.gemv_q4k(wg, xc, F, H)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res["cpu_oracle_gate_us"] = dt * 1e6
+        res["cpu_oracle_threads"] = oracle.max_threads()
+        res["cpu_oracle_gate_gbs"] = wg.size / dt / 1e9
+    del lw, big
+    torch.cuda.empty_cache()
+    return res
+
+
 # ----------------------------------------------------------------------------
 
 def main():
@@ -358,7 +446,7 @@ def main():
     import nyion_hip as nh
 
     nh.init(0)
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5"}
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -386,6 +474,9 @@ def main():
     if "c5" in only:
         log("C5: causal prefill N=8192")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
+    if "gemv" in only:
+        log("Q4_K weight GEMV: TinyLlama decode-step projections, 8B-shaped gate/up")
+        res["gemv_q4k"] = bench_gemv(nh, torch, steps, warmup, cpu=not args.no_cpu)
     cpu = None
     if not args.no_cpu and "c2" in only:
         log("CPU baseline (oracle) on C2 layers")
