@@ -361,6 +361,67 @@ int nyion_gemv_q4k_batched(const uint8_t* d_w, const float* d_x, int64_t x_strid
                            int64_t out_stride, int n_rows, int n_cols, int batch,
                            nyion_stream_t stream);
 
+/* ------------------------------------------- paged KV pool with host spill */
+
+/* One step of the page policy.  CREATE: a new page took block `block`
+ * (zeroed); EVICT: the page left block `block` for cold slot `slot`;
+ * RELOAD: the page came back from cold slot `slot` into block `block`. */
+enum { NYION_PAGE_CREATE = 0, NYION_PAGE_EVICT = 1, NYION_PAGE_RELOAD = 2 };
+typedef struct nyion_page_event {
+    int32_t kind;
+    int32_t page;
+    int32_t block;
+    int32_t slot;
+} nyion_page_event;
+
+/* The PagedKVCache page policy (swamp-engine/src/cache.rs:277-336 page
+ * creation and LRU, 407-477 eviction, 479-523 reload, 525-553 ensure_page /
+ * ensure_pages_hot, 563-581 importance), host only: at most hot_limit hot
+ * pages (physical blocks 0..hot_limit-1); eviction takes the lowest
+ * importance among the LRU tail and the seven pages before it, into the
+ * first free cold slot at or after a write cursor.  A full cold tier is an
+ * error (the reference overwrites a used slot).  ensure makes pages
+ * first..last hot in order (creating pages up to last as the reference
+ * does) and reports the events; the range may not exceed hot_limit pages.
+ * state returns 0 unmapped, 1 hot (where = block), 2 cold (where = slot),
+ * -1 out of range; lru lists hot pages, most recent first. */
+void* nyion_page_policy_create(int hot_limit, int cold_slots, int max_pages);
+void  nyion_page_policy_destroy(void* policy);
+int   nyion_page_policy_ensure(void* policy, int first_page, int last_page,
+                               nyion_page_event* events, int max_events, int* n_events);
+int   nyion_page_policy_record(void* policy, int page, double weight);
+int   nyion_page_policy_reset(void* policy);
+int   nyion_page_policy_state(void* policy, int page, int* where, double* importance);
+int   nyion_page_policy_lru(void* policy, int* pages, int cap);
+
+/* Device-resident paged KV cache of one sequence with a pinned-host cold
+ * tier: the PagedKVCache contract (cache.rs) with HBM as the hot tier in
+ * place of host RAM and pinned host memory in place of the cold file.  K
+ * and V pools [n_layers][hot_blocks][n_kv_heads][block_tokens][row] (f32 or
+ * Q4-20B rows) and the cold store are allocated at create.  ensure makes
+ * pages first..last hot on `stream` (spill, reload and zeroing as copy
+ * kernels on that stream) and updates the device block table
+ * (nyion_kv_pool_table: [max_pages] int32, -1 for pages not in HBM), which
+ * the decode and KV-write entry points take with max_blocks_per_seq =
+ * max_pages and num_blocks = hot_blocks.  record_importance is the
+ * executor's hand-off (executor.rs:751-755): positions whose importance
+ * exceeds `threshold` add it to their page.  nyion_kv_pool_policy exposes
+ * the pool's policy to the nyion_page_policy_state/lru queries (not to
+ * ensure: that would leave device memory behind).  cold_slot gives the host
+ * bytes of a slot ([layer][K|V][block bytes]). */
+void*          nyion_kv_pool_create(int n_layers, int n_kv_heads, int head_dim, int block_tokens,
+                                    int kv_dtype, int hot_blocks, int cold_slots, int max_pages);
+void           nyion_kv_pool_destroy(void* pool);
+int            nyion_kv_pool_layer(void* pool, int layer, void** k_pool, void** v_pool);
+const int32_t* nyion_kv_pool_table(void* pool);
+void*          nyion_kv_pool_policy(void* pool);
+int            nyion_kv_pool_ensure(void* pool, int first_page, int last_page, nyion_stream_t stream);
+int            nyion_kv_pool_record_importance(void* pool, const double* importance,
+                                               int n_positions, double threshold);
+int            nyion_kv_pool_stats(void* pool, int64_t* hot, int64_t* cold, int64_t* evictions,
+                                   int64_t* reloads);
+const void*    nyion_kv_pool_cold_slot(void* pool, int slot);
+
 /* --------------------------------------------------------- HMA arena */
 
 /* The HeterogeneousMemoryAllocator contract (swamp-tensors/src/hma.rs:5-9,

@@ -102,6 +102,23 @@ SIGNATURES = {
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_kv_gather_bf16": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_page_policy_create": (vp, [i32, i32, i32]),
+    "nyion_page_policy_destroy": (None, [vp]),
+    "nyion_page_policy_ensure": (i32, [vp, i32, i32, vp, i32, C.POINTER(C.c_int)]),
+    "nyion_page_policy_record": (i32, [vp, i32, C.c_double]),
+    "nyion_page_policy_reset": (i32, [vp]),
+    "nyion_page_policy_state": (i32, [vp, i32, C.POINTER(C.c_int), C.POINTER(C.c_double)]),
+    "nyion_page_policy_lru": (i32, [vp, vp, i32]),
+    "nyion_kv_pool_create": (vp, [i32, i32, i32, i32, i32, i32, i32, i32]),
+    "nyion_kv_pool_destroy": (None, [vp]),
+    "nyion_kv_pool_layer": (i32, [vp, i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
+    "nyion_kv_pool_table": (vp, [vp]),
+    "nyion_kv_pool_policy": (vp, [vp]),
+    "nyion_kv_pool_ensure": (i32, [vp, i32, i32, vp]),
+    "nyion_kv_pool_record_importance": (i32, [vp, vp, i32, C.c_double]),
+    "nyion_kv_pool_stats": (i32, [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                  C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "nyion_kv_pool_cold_slot": (vp, [vp, i32]),
     "nyion_gemv_q4k": (i32, [vp, vp, vp, i32, i32, vp]),
     "nyion_gemv_q4k_multi": (i32, [vp, vp, vp, vp, i32, i32, vp]),
     "nyion_gemv_q4k_batched": (i32, [vp, vp, i64, vp, i64, i32, i32, i32, vp]),
@@ -505,3 +522,121 @@ def gemv_q4k_batched(w, x, out, n_rows, n_cols, stream=None):
     check(load().nyion_gemv_q4k_batched(ptr(w), ptr(x), x.stride(0), ptr(out), out.stride(0),
                                         n_rows, n_cols, x.shape[0], stream_handle(stream)),
           "nyion_gemv_q4k_batched")
+
+
+# ----------------------------------------------------------------------------
+# paged KV pool with host spill
+# ----------------------------------------------------------------------------
+
+PAGE_CREATE, PAGE_EVICT, PAGE_RELOAD = 0, 1, 2
+PAGE_UNMAPPED, PAGE_HOT, PAGE_COLD = 0, 1, 2
+
+
+class PageEvent(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("page", C.c_int32), ("block", C.c_int32),
+                ("slot", C.c_int32)]
+
+
+def _policy_state(h, page):
+    where, imp = C.c_int(0), C.c_double(0.0)
+    st = load().nyion_page_policy_state(h, page, C.byref(where), C.byref(imp))
+    return st, where.value, imp.value
+
+
+def _policy_lru(h, cap):
+    buf = (C.c_int * max(cap, 1))()
+    n = load().nyion_page_policy_lru(h, buf, cap)
+    return list(buf[:max(n, 0)])
+
+
+class PagePolicy:
+    """Host page policy (no device needed)."""
+
+    def __init__(self, hot_limit, cold_slots, max_pages):
+        self.h = load().nyion_page_policy_create(hot_limit, cold_slots, max_pages)
+        if not self.h:
+            raise NyionError(ERR_INVALID, last_error())
+        self.max_pages = max_pages
+
+    def ensure(self, first, last=None):
+        last = first if last is None else last
+        # creating pages up to `last` can evict once per page; reloads in range
+        cap = 2 * (last + 1) + 4 * (last - first + 1) + 16
+        buf = (PageEvent * cap)()
+        n = C.c_int(0)
+        rc = load().nyion_page_policy_ensure(self.h, first, last, buf, cap, C.byref(n))
+        events = [(e.kind, e.page, e.block, e.slot) for e in buf[:min(n.value, cap)]]
+        return rc, events
+
+    def record(self, page, weight):
+        check(load().nyion_page_policy_record(self.h, page, weight), "page_policy_record")
+
+    def reset(self):
+        check(load().nyion_page_policy_reset(self.h), "page_policy_reset")
+
+    def state(self, page):
+        return _policy_state(self.h, page)
+
+    def lru(self):
+        return _policy_lru(self.h, self.max_pages)
+
+    def close(self):
+        if self.h:
+            load().nyion_page_policy_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+class KvPool:
+    """Device-resident paged KV cache of one sequence with a pinned-host cold tier."""
+
+    def __init__(self, n_layers, n_kv_heads, head_dim, block_tokens, kv_dtype, hot_blocks,
+                 cold_slots, max_pages):
+        self.h = load().nyion_kv_pool_create(n_layers, n_kv_heads, head_dim, block_tokens,
+                                             kv_dtype, hot_blocks, cold_slots, max_pages)
+        if not self.h:
+            raise NyionError(ERR_INVALID, last_error())
+        self.n_layers, self.n_kv_heads, self.head_dim = n_layers, n_kv_heads, head_dim
+        self.block_tokens, self.kv_dtype = block_tokens, kv_dtype
+        self.hot_blocks, self.cold_slots, self.max_pages = hot_blocks, cold_slots, max_pages
+
+    def layer(self, layer):
+        k, v = C.c_void_p(), C.c_void_p()
+        check(load().nyion_kv_pool_layer(self.h, layer, C.byref(k), C.byref(v)), "kv_pool_layer")
+        return k.value, v.value
+
+    def table(self):
+        return load().nyion_kv_pool_table(self.h)
+
+    def ensure(self, first, last=None, stream=None):
+        last = first if last is None else last
+        check(load().nyion_kv_pool_ensure(self.h, first, last, stream_handle(stream)),
+              "kv_pool_ensure")
+
+    def record_importance(self, importance, threshold=0.001):
+        import numpy as np
+        imp = np.ascontiguousarray(importance, dtype=np.float64)
+        check(load().nyion_kv_pool_record_importance(self.h, imp.ctypes.data, imp.size, threshold),
+              "kv_pool_record_importance")
+
+    def stats(self):
+        v = [C.c_int64(0) for _ in range(4)]
+        check(load().nyion_kv_pool_stats(self.h, *[C.byref(x) for x in v]), "kv_pool_stats")
+        return dict(zip(("hot", "cold", "evictions", "reloads"), [x.value for x in v]))
+
+    def state(self, page):
+        return _policy_state(load().nyion_kv_pool_policy(self.h), page)
+
+    def lru(self):
+        return _policy_lru(load().nyion_kv_pool_policy(self.h), self.max_pages)
+
+    def cold_slot_ptr(self, slot):
+        return load().nyion_kv_pool_cold_slot(self.h, slot)
+
+    def close(self):
+        if self.h:
+            load().nyion_kv_pool_destroy(self.h)
+            self.h = None
+
+    __del__ = close
