@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv (default all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv,pool (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 512 MiB device copy (PMC traffic calibration)")
@@ -432,6 +432,42 @@ def bench_gemv(nh, torch, steps, warmup, cpu=True):
     return res
 
 
+def bench_kv_pool(nh, torch, steps, warmup):
+    """Paged KV pool with host spill, TinyLlama geometry (22 layers, 4 kv heads,
+    D=64, 16-token pages, f32: 704 KiB per page over all layers, K and V):
+    cost of bringing a cold page back when the hot tier is full (one spill to
+    pinned host memory plus one reload), and of creating a page."""
+    layers, hkv, d, bt, hot, cold, pages = 22, 4, 64, 16, 64, 512, 512
+    pool = nh.KvPool(layers, hkv, d, bt, nh.KV_F32, hot, cold, pages)
+    page_bytes = 2 * layers * hkv * bt * d * 4
+    n_create = 256
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for p in range(n_create):
+        pool.ensure(p)
+    torch.cuda.synchronize()
+    create_us = (time.perf_counter() - t0) * 1e6 / n_create  # includes the spills past 64
+    rng = np.random.default_rng(0)
+    order = [int(p) for p in rng.integers(0, n_create - hot, max(32, steps))]
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st0 = pool.stats()
+    s.record()
+    t0 = time.perf_counter()
+    for p in order:
+        pool.ensure(p)
+    e.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e6 / len(order)
+    st1 = pool.stats()
+    moves = (st1["evictions"] - st0["evictions"]) + (st1["reloads"] - st0["reloads"])
+    gpu_us = s.elapsed_time(e) * 1e3
+    res = {"page_bytes": page_bytes, "create_or_spill_us_wall": create_us,
+           "cold_hit_us_wall": wall, "cold_hit_us_gpu": gpu_us / len(order),
+           "page_moves": moves, "host_link_gbs": moves * page_bytes / gpu_us / 1e3}
+    pool.close()
+    return res
+
+
 # ----------------------------------------------------------------------------
 
 def main():
@@ -446,7 +482,7 @@ def main():
     import nyion_hip as nh
 
     nh.init(0)
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv"}
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv", "pool"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -474,6 +510,9 @@ def main():
     if "c5" in only:
         log("C5: causal prefill N=8192")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
+    if "pool" in only:
+        log("paged KV pool: cold-page round trips over the host link")
+        res["kv_pool"] = bench_kv_pool(nh, torch, steps, warmup)
     if "gemv" in only:
         log("Q4_K weight GEMV: TinyLlama decode-step projections, 8B-shaped gate/up")
         res["gemv_q4k"] = bench_gemv(nh, torch, steps, warmup, cpu=not args.no_cpu)
