@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv,pool (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="GEMV section: issue the launches directly instead of replaying graphs")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 512 MiB device copy (PMC traffic calibration)")
     return ap.parse_args()
@@ -356,8 +358,22 @@ def _q4k_random(torch, rows, cols, seed):
     return w.view(rows, -1).contiguous()
 
 
+USE_GRAPHS = True
+
+
 def _graph_us(torch, fn, reps):
-    """Mean replay time of fn captured in a HIP graph (no host overhead)."""
+    """Mean replay time of fn captured in a HIP graph (no host overhead);
+    with --no-graph the same launches are issued directly."""
+    if not USE_GRAPHS:
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps
     gph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gph):
         fn()
@@ -409,7 +425,8 @@ def bench_gemv(nh, torch, steps, warmup, cpu=True):
 
     gu_us = _graph_us(torch, gateup, reps) / L8
     gu_bytes = 2 * big[0][0].numel()
-    res = {"tinyllama_step_us": step_us, "tinyllama_step_bytes": step_bytes, "launches": 4 * L,
+    res = {"timing": "graph replay" if USE_GRAPHS else "direct launches",
+           "tinyllama_step_us": step_us, "tinyllama_step_bytes": step_bytes, "launches": 4 * L,
            "tinyllama_step_gbs": step_bytes / step_us / 1e3,
            "gateup_8b_us": gu_us, "gateup_8b_bytes": gu_bytes,
            "gateup_8b_gbs": gu_bytes / gu_us / 1e3,
@@ -482,6 +499,8 @@ def main():
     import nyion_hip as nh
 
     nh.init(0)
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv", "pool"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
