@@ -50,6 +50,32 @@ def test_gemv_q4k_vs_oracle(gpu, n_rows, n_cols):
     check(out.cpu().numpy(), oracle.gemv_q4k(w, x, n_rows, n_cols), f"gemv {n_rows}x{n_cols}")
 
 
+@pytest.mark.parametrize("n_rows,n_cols", [(37, 16640), (9, 32768), (130, 20480)])
+def test_gemv_q4k_long_rows(gpu, n_rows, n_cols):
+    """Rows longer than eight wavefronts' single pass (16384 columns): each
+    wavefront makes several passes and reloads its x values per pass."""
+    w = W.q4k_random_weights(n_rows, n_cols, seed=n_cols)
+    x = np.random.default_rng(n_rows).standard_normal(n_cols).astype(np.float32)
+    out = torch.full((n_rows,), float("nan"), device="cuda")
+    gpu.gemv_q4k(dev(w), dev(x), out, n_rows, n_cols)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle.gemv_q4k(w, x, n_rows, n_cols), f"gemv {n_rows}x{n_cols}")
+
+
+def test_gemv_q4k_long_rows_batched_equals_single(gpu):
+    n_rows, n_cols, batch = 33, 16896, 3
+    w = dev(W.q4k_random_weights(n_rows, n_cols, seed=11))
+    xs = torch.from_numpy(np.random.default_rng(12).standard_normal((batch, n_cols))
+                          .astype(np.float32)).cuda()
+    out = torch.empty((batch, n_rows), device="cuda")
+    gpu.gemv_q4k_batched(w, xs, out, n_rows, n_cols)
+    for b in range(batch):
+        single = torch.empty(n_rows, device="cuda")
+        gpu.gemv_q4k(w, xs[b].contiguous(), single, n_rows, n_cols)
+        torch.cuda.synchronize()
+        assert torch.equal(out[b], single), b
+
+
 def test_gemv_q4k_reference_test_weights(gpu):
     """The reference tests' weights and input (fused_gemv_q4k.rs:830-845)."""
     for n_rows in (2, 3, 4, 7):
