@@ -581,11 +581,15 @@ class PagePolicy:
         return _policy_lru(self.h, self.max_pages)
 
     def close(self):
-        if self.h:
+        if getattr(self, "h", None):
             load().nyion_page_policy_destroy(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone
+            pass
 
 
 class KvPool:
@@ -635,8 +639,12 @@ class KvPool:
         return load().nyion_kv_pool_cold_slot(self.h, slot)
 
     def close(self):
-        if self.h:
+        if getattr(self, "h", None):
             load().nyion_kv_pool_destroy(self.h)
             self.h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone
+            pass
