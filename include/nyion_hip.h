@@ -234,8 +234,9 @@ int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion
 /* Decode work split.  The decode grid cuts the concatenated 16-token tile
  * lists of all (sequence, kv head, head group) segments into equal ranges, one
  * per workgroup; the grid is sized for `tokens` per workgroup (a power of two
- * in 64..4096; 0 restores the default, 256) and capped at the workgroups the
- * device holds resident.  Process-wide; for tuning.  The getter returns the
+ * in 64..4096; 0 restores the default: the launch's tokens divided by the CU
+ * count, within 128..256) and capped at the workgroups the device holds
+ * resident.  Process-wide; for tuning.  The getter returns the
  * tokens per workgroup the current setting gives for `batch` sequences of
  * max_len tokens. */
 int nyion_set_decode_partition_tokens(int tokens);

@@ -852,9 +852,12 @@ __global__ void fill_zero_kernel(int* p, long long n) {
 
 // Tiles per workgroup the grid is sized for: small enough to spread a short
 // context over many CUs, large enough that each wavefront pipelines a few
-// tiles.  Workspace sizes assume the smallest allowed value, so tuning never
-// outgrows a workspace.
+// tiles.  By default the launch's tiles divided by the CU count, within
+// [kSmallWgTiles, kDefaultWgTiles] (a single 4096-token sequence then fills
+// every CU with 8-tile ranges; large batches use 16).  Workspace sizes assume
+// the smallest allowed value, so tuning never outgrows a workspace.
 constexpr int kDefaultWgTiles = 16;
+constexpr int kSmallWgTiles = 8;
 constexpr int kMinWgTiles = 4;
 constexpr int kMaxGrid = 2048;  // workgroups per launch (partial slots are sized for it)
 static int g_wg_tiles_override = 0;
@@ -973,10 +976,29 @@ static int resident_capacity() {
     return cap;
 }
 
+static int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) {
+            (void)hipGetLastError();
+            return 256;
+        }
+        n = c;
+    }
+    return n;
+}
+
+static int wg_tiles_for(long long total_tiles) {
+    if (g_wg_tiles_override > 0) return g_wg_tiles_override;
+    const long long per_cu = total_tiles / cu_count();
+    return per_cu < kSmallWgTiles ? kSmallWgTiles : per_cu > kDefaultWgTiles ? kDefaultWgTiles : (int)per_cu;
+}
+
 template <int D, int KVT, bool AL, bool TR>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
     const int units = pl.a.n_kv_heads * pl.a.n_hg;
-    const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
     const int cap = resident_capacity<D, KVT, AL, TR>();
     for (int b0 = 0; b0 < pl.batch; b0 += pl.chunk) {
         const int nb = pl.batch - b0 < pl.chunk ? pl.batch - b0 : pl.chunk;
@@ -991,7 +1013,8 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
         if (a.positions) a.positions += (long long)b0 * a.pos_stride;
         if (a.n_pos) a.n_pos += b0;
         if (a.scores) a.scores += (long long)b0 * a.n_heads * a.scores_stride;
-        int grid = grid_for((long long)nb * units * pl.tiles_max, wg_tiles, cap);
+        const long long total = (long long)nb * units * pl.tiles_max;
+        int grid = grid_for(total, wg_tiles_for(total), cap);
         if (grid > pl.grid_bound) grid = pl.grid_bound;
         if (pl.ws_bytes == 0 || (nb == 1 && grid <= units)) grid = units;  // whole segments
         hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR>), dim3(grid), dim3(256), 0, stream, a);
@@ -1059,11 +1082,13 @@ int nyion_set_decode_partition_tokens(int tokens) {
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len) {
     if (batch <= 0 || n_kv_heads <= 0 || max_len <= 0) return 0;
     const long long tiles = (long long)batch * n_kv_heads * (max_len / 16 + 2);
-    const int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
     int cap = kMaxGrid;
-    if (require_device() == NYION_OK)
+    int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
+    if (require_device() == NYION_OK) {
         cap = head_dim == 128 ? resident_capacity<128, NYION_KV_F32, true, false>()
                               : resident_capacity<64, NYION_KV_F32, true, false>();
+        wg_tiles = wg_tiles_for(tiles);
+    }
     clear_error();
     const int grid = grid_for(tiles, wg_tiles, cap);
     return (int)(16 * ((tiles + grid - 1) / grid));
