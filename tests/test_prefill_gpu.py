@@ -167,6 +167,22 @@ def test_prefill_ctx_all_rows(gpu, n_hist, n, hq, hkv, d):
           f"ctx {n_hist}+{n},{hq}/{hkv},{d}")
 
 
+@pytest.mark.parametrize("n_hist,n,hq,hkv,d,causal", [
+    (200, 150, 16, 2, 128, True),   # GQA 8:1: two four-head subsets per kv head
+    (130, 70, 8, 1, 64, True),      # GQA 8:1 at D=64
+    (65, 129, 4, 2, 64, True),      # GQA 2:1, history one past a tile edge
+    (190, 40, 8, 2, 128, False),    # non-causal with a ragged history
+    (33, 96, 6, 6, 64, True),       # MHA, six heads
+])
+def test_prefill_ctx_more_shapes(gpu, n_hist, n, hq, hkv, d, causal):
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=3 * n + n_hist)
+    _, kh, vh = W.prefill_inputs(n_hist, hq, hkv, d, seed=5 * n_hist + 2)
+    got = run_prefill_ctx(gpu, q, k, v, kh, vh, causal=causal)
+    rows = np.arange(n) if causal else np.array([0, 1, n // 2, n - 1])
+    check(got, oracle_ctx_rows(q, k, v, kh, vh, rows, causal=causal), rows,
+          f"ctx {n_hist}+{n},{hq}/{hkv},{d},causal={causal}")
+
+
 def test_prefill_ctx_non_causal(gpu):
     q, k, v = W.prefill_inputs(100, 8, 2, 128, seed=11)
     _, kh, vh = W.prefill_inputs(77, 8, 2, 128, seed=12)
