@@ -99,6 +99,30 @@ def test_paged_edge_lengths(gpu, lens):
     assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"lens {lens}")
 
 
+@pytest.mark.parametrize("bt,kv", [(4, oracle.KV_F32), (8, oracle.KV_F32), (32, oracle.KV_F32),
+                                   (64, oracle.KV_F32), (256, oracle.KV_F32), (8, oracle.KV_Q4),
+                                   (64, oracle.KV_Q4)])
+def test_paged_block_sizes(gpu, bt, kv):
+    """Pages of 4 and 8 tokens take the per-row gather path, 16 and up the
+    aligned block walk (runs of a tile inside one block)."""
+    pb = W.paged_batch([1, 17, 100, 300, 777], block_tokens=bt, seed=bt + kv, kv_dtype=kv)
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"block_tokens {bt} kv {kv}")
+
+
+@pytest.mark.parametrize("bt", [8, 32])
+def test_window_small_and_large_blocks(gpu, bt):
+    pb = W.paged_batch([70, 300, 1000], block_tokens=bt, seed=bt)
+    assert_close(run_paged(gpu, pb, window=64, global_stride=16),
+                 W.reference_decode(pb, window=64, global_stride=16), f"window bt {bt}")
+
+
+def test_paged_batch_beyond_one_launch(gpu):
+    """2100 sequences: more than one launch's 2048 (the host splits the batch)."""
+    lens = np.random.default_rng(9).integers(1, 48, 2100)
+    pb = W.paged_batch(lens, n_heads=8, n_kv_heads=2, seed=9)
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), "2100 sequences")
+
+
 @pytest.mark.parametrize("ctx,max_ctx,q_pos", [(1000, 4096, None), (4096, 4096, 100), (1, 64, None),
                                               (3000, 3001, 0)])
 def test_single_sequence_host_bound(gpu, ctx, max_ctx, q_pos):
