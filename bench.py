@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv,pool (default all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv,gemv6,pool (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true",
                     help="GEMV section: issue the launches directly instead of replaying graphs")
@@ -358,6 +358,17 @@ def _q4k_random(torch, rows, cols, seed):
     return w.view(rows, -1).contiguous()
 
 
+def _q6k_random(torch, rows, cols, seed):
+    """Random Q6_K matrix on the device: uniform ql/qh/scales, normal f16 d in
+    [7e-5, 5e-4]."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    nb = cols // 256
+    w = torch.randint(0, 256, (rows, nb, 210), dtype=torch.uint8, device="cuda", generator=g)
+    d = (torch.rand((rows, nb), device="cuda", generator=g) * 4.3e-4 + 7e-5).half()
+    w[:, :, 208:210] = d.view(torch.uint8).view(rows, nb, 2)
+    return w.view(rows, -1).contiguous()
+
+
 USE_GRAPHS = True
 
 
@@ -449,6 +460,73 @@ def bench_gemv(nh, torch, steps, warmup, cpu=True):
     return res
 
 
+def bench_gemv_q6k(nh, torch, steps, warmup, cpu=True):
+    """Q6_K weight GEMV: the TinyLlama-1.1B output projection (32000 x 2048,
+    53.8 MB; six copies rotated so that the 256 MB MALL does not hold them),
+    and a Q4_K_M-style TinyLlama decode step through the spec list (per layer
+    q/k/o/gate/up Q4_K, v/down Q6_K; one list per layer, launched as q+k,
+    v, o, gate+up and down: 110 launches), both replayed from HIP graphs."""
+    V, H, F, KV, L = 32000, 2048, 5632, 256, 22
+    heads = [_q6k_random(torch, V, H, 300 + i) for i in range(6)]
+    x = torch.randn(H, device="cuda")
+    xf = torch.randn(F, device="cuda")
+    logits = torch.empty(V, device="cuda")
+
+    def lm_head():
+        for w in heads:
+            nh.gemv_q6k(w, x, logits, V, H)
+
+    reps = max(3, steps // 5)
+    head_us = _graph_us(torch, lm_head, reps) / len(heads)
+    head_bytes = heads[0].numel()
+    del heads
+    lw = []
+    for l in range(L):
+        lw.append({"q": _q4k_random(torch, H, H, 7 * l), "k": _q4k_random(torch, KV, H, 7 * l + 1),
+                   "v": _q6k_random(torch, KV, H, 7 * l + 2), "o": _q4k_random(torch, H, H, 7 * l + 3),
+                   "g": _q4k_random(torch, F, H, 7 * l + 4), "u": _q4k_random(torch, F, H, 7 * l + 5),
+                   "d": _q6k_random(torch, H, F, 7 * l + 6)})
+    o = {k: torch.empty(n, device="cuda") for k, n in dict(q=H, k=KV, v=KV, o=H, g=F, u=F, d=H).items()}
+    fmt = dict(q=144, k=144, v=210, o=144, g=144, u=144, d=210)
+    rows = dict(q=H, k=KV, v=KV, o=H, g=F, u=F, d=H)
+    xa = torch.randn(H, device="cuda")  # attention output, the o projection's input
+    xm = torch.randn(H, device="cuda")  # post-attention hidden state, gate/up's input
+    xin = dict(q=x, k=x, v=x, o=xa, g=xm, u=xm, d=xf)
+    specs = [[(w[k], xin[k], o[k], rows[k], F if k == "d" else H, fmt[k]) for k in "qkvogud"]
+             for w in lw]
+    step_bytes = sum(t.numel() for w in lw for t in w.values())
+
+    def step():
+        for sp in specs:
+            nh.gemv_specs(sp)
+
+    step_us = _graph_us(torch, step, reps)
+    res = {"timing": "graph replay" if USE_GRAPHS else "direct launches",
+           "output_proj_us": head_us, "output_proj_bytes": head_bytes,
+           "output_proj_gbs": head_bytes / head_us / 1e3,
+           "output_proj_hbm_frac": head_bytes / head_us / 1e3 / HBM_PEAK_GBS,
+           "q4km_step_us": step_us, "q4km_step_bytes": step_bytes, "launches": 5 * L,
+           "q4km_step_gbs": step_bytes / step_us / 1e3}
+    if cpu:
+        import oracle
+
+        n_rows = 2048  # a slice of the output projection's rows
+        w0 = _q6k_random(torch, n_rows, H, 400).cpu().numpy()
+        xc = x.cpu().numpy()
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < 2.0:
+            oracle.gemv_q6k(w0, xc, n_rows, H)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res["cpu_oracle_rows"] = n_rows
+        res["cpu_oracle_us"] = dt * 1e6
+        res["cpu_oracle_threads"] = oracle.max_threads()
+        res["cpu_oracle_gbs"] = w0.size / dt / 1e9
+    del lw, specs
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_kv_pool(nh, torch, steps, warmup):
     """Paged KV pool with host spill, TinyLlama geometry (22 layers, 4 kv heads,
     D=64, 16-token pages, f32: 704 KiB per page over all layers, K and V):
@@ -501,7 +579,7 @@ def main():
     nh.init(0)
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv", "pool"}
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv", "gemv6", "pool"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -535,6 +613,9 @@ def main():
     if "gemv" in only:
         log("Q4_K weight GEMV: TinyLlama decode-step projections, 8B-shaped gate/up")
         res["gemv_q4k"] = bench_gemv(nh, torch, steps, warmup, cpu=not args.no_cpu)
+    if "gemv6" in only:
+        log("Q6_K weight GEMV: TinyLlama output projection, Q4_K_M-style decode step")
+        res["gemv_q6k"] = bench_gemv_q6k(nh, torch, steps, warmup, cpu=not args.no_cpu)
     cpu = None
     if not args.no_cpu and "c2" in only:
         log("CPU baseline (oracle) on C2 layers")

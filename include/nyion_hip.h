@@ -362,6 +362,48 @@ int nyion_gemv_q4k_batched(const uint8_t* d_w, const float* d_x, int64_t x_strid
                            int64_t out_stride, int n_rows, int n_cols, int batch,
                            nyion_stream_t stream);
 
+/* ------------------------------------------------------ Q6_K weight GEMV */
+
+/* out[r] = sum_j W[r][j] x[j] for a GGUF Q6_K matrix W (n_rows rows of
+ * n_cols/256 blocks of 210 bytes: ql[128], qh[64], int8 scales[16], f16 d).
+ * Replaces fused_gemv_q6k (swamp-kernels/src/fused_gemv_q6k.rs:22-43), the
+ * Q6_K arm of forward_linear (swamp-engine/src/linear.rs:173-189), with the
+ * f32 semantics of its scalar path (248-293), including its own f16
+ * conversion of d (11-20: exact for normal values; zero and subnormal d
+ * become about -2e34, infinities and NaNs finite values).  n_cols a positive
+ * multiple of 256; W 2-byte aligned, x 16-byte aligned.  out is written. */
+int nyion_gemv_q6k(const uint8_t* d_w, const float* d_x, float* d_out, int n_rows, int n_cols,
+                   nyion_stream_t stream);
+
+/* batch inputs against one Q6_K matrix, W read once per four inputs (the
+ * Q6_K arm of fallback_gemv, linear.rs:437-465); strides and bit-for-bit
+ * equality with the single call as for nyion_gemv_q4k_batched. */
+int nyion_gemv_q6k_batched(const uint8_t* d_w, const float* d_x, int64_t x_stride, float* d_out,
+                           int64_t out_stride, int n_rows, int n_cols, int batch,
+                           nyion_stream_t stream);
+
+/* ------------------------------------------- mixed Q4_K / Q6_K GEMV lists */
+
+/* One GEMV of a list: the reference's (raw, x, out, n_rows, n_cols,
+ * block_size) tuple of forward_gemvs_ring (linear.rs:472-525); block_bytes
+ * 144 is Q4_K, 210 Q6_K (the is_q4k switch of forward_gemvs,
+ * linear.rs:379-432).  Device pointers. */
+typedef struct nyion_gemv_spec {
+    const uint8_t* w;
+    const float* x;
+    float* out;
+    int32_t n_rows;
+    int32_t n_cols;
+    int32_t block_bytes;
+    int32_t reserved; /* 0 */
+} nyion_gemv_spec;
+
+/* Every spec of a host array: out = W x.  Specs of one format, n_cols and x
+ * share a launch (up to four each; a Q4_K_M layer's q/k with its Q6_K v take
+ * two launches).  All specs are checked before the first launch; a spec with
+ * n_rows 0 is skipped.  No spec's out may overlap another spec's x or W. */
+int nyion_gemv_specs(const nyion_gemv_spec* specs, int n_specs, nyion_stream_t stream);
+
 /* ------------------------------------------- paged KV pool with host spill */
 
 /* One step of the page policy.  CREATE: a new page took block `block`

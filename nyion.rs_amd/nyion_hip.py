@@ -122,6 +122,9 @@ SIGNATURES = {
     "nyion_gemv_q4k": (i32, [vp, vp, vp, i32, i32, vp]),
     "nyion_gemv_q4k_multi": (i32, [vp, vp, vp, vp, i32, i32, vp]),
     "nyion_gemv_q4k_batched": (i32, [vp, vp, i64, vp, i64, i32, i32, i32, vp]),
+    "nyion_gemv_q6k": (i32, [vp, vp, vp, i32, i32, vp]),
+    "nyion_gemv_q6k_batched": (i32, [vp, vp, i64, vp, i64, i32, i32, i32, vp]),
+    "nyion_gemv_specs": (i32, [vp, i32, vp]),
     "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
     "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
                                    i32, i32, i32, vp]),
@@ -522,6 +525,41 @@ def gemv_q4k_batched(w, x, out, n_rows, n_cols, stream=None):
     check(load().nyion_gemv_q4k_batched(ptr(w), ptr(x), x.stride(0), ptr(out), out.stride(0),
                                         n_rows, n_cols, x.shape[0], stream_handle(stream)),
           "nyion_gemv_q4k_batched")
+
+
+# ----------------------------------------------------------------------------
+# Q6_K weight GEMV and mixed Q4_K / Q6_K lists
+# ----------------------------------------------------------------------------
+
+Q6K_BYTES = 210
+
+
+def gemv_q6k(w, x, out, n_rows, n_cols, stream=None):
+    """w: device uint8 [n_rows][n_cols/256*210] (2-byte aligned); x [n_cols] f32; out [n_rows] f32."""
+    check(load().nyion_gemv_q6k(ptr(w), ptr(x), ptr(out), n_rows, n_cols, stream_handle(stream)),
+          "nyion_gemv_q6k")
+
+
+def gemv_q6k_batched(w, x, out, n_rows, n_cols, stream=None):
+    """x [batch][>= n_cols] f32, out [batch][>= n_rows] f32 (row-major, strided)."""
+    check(load().nyion_gemv_q6k_batched(ptr(w), ptr(x), x.stride(0), ptr(out), out.stride(0),
+                                        n_rows, n_cols, x.shape[0], stream_handle(stream)),
+          "nyion_gemv_q6k_batched")
+
+
+class GemvSpec(C.Structure):
+    """nyion_gemv_spec: (w, x, out, n_rows, n_cols, block_bytes 144 | 210)."""
+    _fields_ = [("w", C.c_void_p), ("x", C.c_void_p), ("out", C.c_void_p), ("n_rows", C.c_int32),
+                ("n_cols", C.c_int32), ("block_bytes", C.c_int32), ("reserved", C.c_int32)]
+
+
+def gemv_specs(specs, stream=None):
+    """specs: list of (w, x, out, n_rows, n_cols, block_bytes) with device tensors."""
+    n = len(specs)
+    arr = (GemvSpec * max(n, 1))()
+    for i, (w, x, out, nr, nc, bb) in enumerate(specs):
+        arr[i] = GemvSpec(ptr(w), ptr(x), ptr(out), nr, nc, bb, 0)
+    check(load().nyion_gemv_specs(arr, n, stream_handle(stream)), "nyion_gemv_specs")
 
 
 # ----------------------------------------------------------------------------

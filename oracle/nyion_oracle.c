@@ -747,3 +747,83 @@ int orc_gemv_q4k(const uint8_t* w, const float* x, float* out, int n_rows, int n
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------ Q6_K */
+
+/* swamp-kernels/src/fused_gemv_q6k.rs:6-20: the reference's own f16 -> f32
+ * of the block scale.  Normal values convert exactly; exponent 0 (zero and
+ * subnormals) builds the bits sign | (1009 << 23, wrapped to 32 bits) |
+ * mant << 13, i.e. a large negative number, and exponent 31 (inf, NaN)
+ * becomes a finite value.  Restated as is. */
+float orc_q6k_scale_to_f32(uint16_t v) {
+    const uint32_t sign = (uint32_t)(v >> 15) << 31;
+    const uint32_t e = (v >> 10) & 0x1f;
+    const uint32_t mant = v & 0x3ff;
+    uint32_t bits;
+    if (e == 0)
+        bits = sign | (uint32_t)(1009u << 23) | (mant << 13);
+    else
+        bits = sign | ((e + 112u) << 23) | (mant << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* One 210-byte block (ql[128], qh[64], int8 scales[16], f16 d) -> 256
+ * weights d * sc * (q - 32), each product rounded left to right in f32 as
+ * the scalar GEMV forms it (fused_gemv_q6k.rs:248-293): half h, l = 0..31:
+ * element 128h + l + 32k takes q_k from the low (k = 0, 1) or high (k = 2, 3)
+ * nibble of ql[64h + l + 32(k&1)] and bits 2k..2k+1 of qh[32h + l], and
+ * scale sc[8h + l/16 + 2k]. */
+void orc_q6k_dequant_block(const uint8_t* blk, float* out) {
+    const float d = orc_q6k_scale_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+    for (int h = 0; h < 2; h++) {
+        const uint8_t* ql = blk + 64 * h;
+        const uint8_t* qh = blk + 128 + 32 * h;
+        const int8_t* sc = (const int8_t*)(blk + 192 + 8 * h);
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q[4] = {(ql[l] & 0x0F) | ((qh[l] & 3) << 4),
+                              (ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4),
+                              (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4),
+                              (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)};
+            for (int k = 0; k < 4; k++)
+                out[128 * h + l + 32 * k] = d * (float)sc[is + 2 * k] * (float)(q[k] - 32);
+        }
+    }
+}
+
+/* fused_gemv_q6k_scalar (fused_gemv_q6k.rs:248-293), same accumulation
+ * order: per block, halves, l = 0..31, the four elements l, l+32, l+64,
+ * l+96, each acc += ((d * sc) * q) * x. */
+int orc_gemv_q6k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols) {
+    if (n_cols <= 0 || n_cols % 256 || n_rows < 0) return -1;
+    const int nb = n_cols / 256;
+#pragma omp parallel for schedule(static)
+    for (int row = 0; row < n_rows; row++) {
+        float acc = 0.0f;
+        for (int blk = 0; blk < nb; blk++) {
+            const uint8_t* b = w + ((size_t)row * nb + blk) * 210;
+            const float d = orc_q6k_scale_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+            for (int h = 0; h < 2; h++) {
+                const uint8_t* ql = b + 64 * h;
+                const uint8_t* qh = b + 128 + 32 * h;
+                const int8_t* sc = (const int8_t*)(b + 192 + 8 * h);
+                const float* xh = x + (size_t)blk * 256 + 128 * h;
+                for (int l = 0; l < 32; l++) {
+                    const int is = l / 16;
+                    const float q1 = (float)(((ql[l] & 0x0F) | ((qh[l] & 3) << 4)) - 32);
+                    const float q2 = (float)(((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                    const float q3 = (float)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                    const float q4 = (float)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+                    acc += d * (float)sc[is] * q1 * xh[l];
+                    acc += d * (float)sc[is + 2] * q2 * xh[l + 32];
+                    acc += d * (float)sc[is + 4] * q3 * xh[l + 64];
+                    acc += d * (float)sc[is + 6] * q4 * xh[l + 96];
+                }
+            }
+        }
+        out[row] = acc;
+    }
+    return 0;
+}

@@ -38,6 +38,14 @@
  *                                              weights (constant nibble 8,
  *                                              fused_gemv_q4k.rs:830-845) and
  *                                              float64 dequantise-then-dot
+ *   orc_q6k_scale_to_f32                     : IEEE binary16 on normal values
+ *                                              (numpy), the reference's own bit
+ *                                              formula on exponents 0 and 31
+ *   orc_q6k_dequant_block / orc_gemv_q6k     : single-element probes of the
+ *                                              bit layout, the reference test
+ *                                              blocks (fused_gemv_q6k.rs:329-
+ *                                              356), a numpy restatement and
+ *                                              float64 dequantise-then-dot
  * Bit-parity of attention outputs with the Rust binary (glibc expf order,
  * rayon scheduling of the importance sum) is unpinned and not required:
  * attention parity is at tolerance.
@@ -143,6 +151,12 @@ int   orc_stokes_read(const void* cache, float* keys, float* values, float* scor
 void orc_q4k_unpack_scales(const uint8_t* sc, uint8_t* scales, uint8_t* mins);
 void orc_q4k_dequant_block(const uint8_t* blk, float* out);
 int  orc_gemv_q4k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols);
+
+/* Q6_K weights (210-byte blocks of 256: ql[128], qh[64], int8 scales[16],
+ * f16 d) and the scalar GEMV of swamp-kernels/src/fused_gemv_q6k.rs */
+float orc_q6k_scale_to_f32(uint16_t v);
+void  orc_q6k_dequant_block(const uint8_t* blk, float* out);
+int   orc_gemv_q6k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols);
 
 int orc_max_threads(void);
 

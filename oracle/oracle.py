@@ -59,6 +59,11 @@ def lib():
                                      C.c_int, C.c_void_p]
         L.orc_q4k_unpack_scales.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
         L.orc_q4k_dequant_block.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_q6k_scale_to_f32.restype = C.c_float
+        L.orc_q6k_scale_to_f32.argtypes = [C.c_uint16]
+        L.orc_q6k_dequant_block.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_gemv_q6k.restype = C.c_int
+        L.orc_gemv_q6k.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         L.orc_gemv_q4k.restype = C.c_int
         L.orc_gemv_q4k.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         L.orc_dot_avx512_order.restype = C.c_float
@@ -325,4 +330,33 @@ def gemv_q4k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np.ndarr
     out = np.empty(n_rows, np.float32)
     if lib().orc_gemv_q4k(w.ctypes.data, x.ctypes.data, out.ctypes.data, n_rows, n_cols) != 0:
         raise ValueError("orc_gemv_q4k: n_cols must be a positive multiple of 256")
+    return out
+
+
+# ----------------------------------------------------------------------------
+# Q6_K weights (swamp-kernels/src/fused_gemv_q6k.rs)
+# ----------------------------------------------------------------------------
+
+Q6K_BYTES = 210
+
+
+def q6k_scale_to_f32(bits: int) -> float:
+    return float(lib().orc_q6k_scale_to_f32(int(bits)))
+
+
+def q6k_dequant(w: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, Q6K_BYTES)
+    out = np.empty((w.shape[0], Q4K_BLOCK), np.float32)
+    for i in range(w.shape[0]):
+        lib().orc_q6k_dequant_block(w[i].ctypes.data, out[i].ctypes.data)
+    return out.reshape(n_rows, n_cols)
+
+
+def gemv_q6k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert w.size == n_rows * (n_cols // Q4K_BLOCK) * Q6K_BYTES and x.size >= n_cols
+    out = np.empty(n_rows, np.float32)
+    if lib().orc_gemv_q6k(w.ctypes.data, x.ctypes.data, out.ctypes.data, n_rows, n_cols) != 0:
+        raise ValueError("orc_gemv_q6k: n_cols must be a positive multiple of 256")
     return out

@@ -51,6 +51,9 @@ def test_no_device_is_reported_not_faked():
                                               None) == nyion_hip.ERR_NO_DEVICE
     assert L.nyion_kv_gather_bf16(None, None, 16, 1, 1, 64, 0, 1, None,
                                   None) == nyion_hip.ERR_NO_DEVICE
+    assert L.nyion_gemv_q6k(None, None, None, 1, 256, None) == nyion_hip.ERR_NO_DEVICE
+    spec = nyion_hip.GemvSpec(256, 512, 1024, 1, 256, 210, 0)  # never dereferenced
+    assert L.nyion_gemv_specs(C.byref(spec), 1, None) == nyion_hip.ERR_NO_DEVICE
     assert L.gpu_attention_device(None, None, None, None, 32, 4, 128, 64, 128) == -1
     assert L.mojo_stokes_init(64) is None
 

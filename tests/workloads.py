@@ -229,3 +229,59 @@ def q4k_reference_test_x(n_cols: int) -> np.ndarray:
     """fused_gemv_q4k.rs:842-844: x_i = (i % 100) / 50 - 1."""
     i = np.arange(n_cols)
     return ((i % 100).astype(np.float32) / np.float32(50.0) - np.float32(1.0)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Q6_K weights (210-byte blocks, swamp-kernels/src/fused_gemv_q6k.rs)
+# ---------------------------------------------------------------------------
+
+def q6k_random_weights(n_rows, n_cols, seed=0, d_range=(7e-5, 5e-4)) -> np.ndarray:
+    """Random Q6_K matrix [n_rows][n_cols/256 * 210] u8.  d stays a normal f16:
+    the reference converts exponent-0 values (zero, subnormals) to about
+    -2e34, which overflows any dot product."""
+    rng = np.random.default_rng(seed)
+    nb = n_rows * (n_cols // 256)
+    w = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)
+    d = rng.uniform(*d_range, size=nb).astype(np.float16)
+    w[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return w.reshape(n_rows, -1)
+
+
+def q6k_dequant_np(w: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    """numpy restatement (normal d only): element 128h + l + 32k of a block
+    is d * sc[8h + l//16 + 2k] * (q - 32), q from the low (k < 2) or high
+    nibble of ql[64h + l + 32(k % 2)] and bits 2k..2k+1 of qh[32h + l]."""
+    b = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, 210)
+    d = b[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
+    out = np.empty((b.shape[0], 256), np.float32)
+    l = np.arange(32)
+    for h in range(2):
+        ql = b[:, 64 * h:64 * h + 64].astype(np.int32)
+        qh = b[:, 128 + 32 * h:128 + 32 * h + 32].astype(np.int32)
+        sc = b[:, 192 + 8 * h:200 + 8 * h].view(np.int8).astype(np.float32)
+        for k in range(4):
+            nib = ql[:, l + 32 * (k % 2)]
+            nib = (nib & 0x0F) if k < 2 else (nib >> 4)
+            q = nib | (((qh[:, l] >> (2 * k)) & 3) << 4)
+            s = sc[:, l // 16 + 2 * k]
+            out[:, 128 * h + l + 32 * k] = ((d[:, None] * s).astype(np.float32) *
+                                           (q - 32).astype(np.float32)).astype(np.float32)
+    return out.reshape(n_rows, n_cols)
+
+
+def q6k_reference_test_weights(n_rows: int, n_blocks: int) -> np.ndarray:
+    """The blocks of the reference's own Q6_K tests (fused_gemv_q6k.rs:329-356)."""
+    i128, i64, i16 = np.arange(128), np.arange(64), np.arange(16)
+    ql = ((i128 & 0x0F) | (((i128 + 128) & 0x0F) << 4)).astype(np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for j in range(4):
+        qh |= ((((i64 + 64 * j) >> 4) & 3) << (2 * j)).astype(np.uint8)
+    rows = []
+    for r in range(n_rows):
+        blk = np.zeros(210, np.uint8)
+        blk[0:128] = ql
+        blk[128:192] = qh
+        blk[192:208] = ((r * 16 + i16 + 1) & 0x7F).astype(np.uint8)
+        blk[208:210] = np.array([0x3800], np.uint16).view(np.uint8)
+        rows.append(np.tile(blk, n_blocks))
+    return np.stack(rows)
