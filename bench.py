@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention path (one GPU).
 
-Workload of the headline line (BASELINE config 2): one full 22-layer decode
+Workload of the headline line: one full 22-layer decode
 step at TinyLlama-1.1B attention shape -- batch 1, 32 q / 4 kv heads,
 head_dim 64, f32 KV context 4096 in a paged cache of 16-token blocks with a
 seeded random permutation block table.  A step is 22 calls of
@@ -11,16 +11,18 @@ never sits in the 256 MB Infinity Cache from the previous step.
 
 metric/unit: achieved algorithmic HBM bandwidth of the decode step in GB/s
 (K + V + q + out + block table bytes, counted once), with us/layer beside it.
-The other BASELINE configs are measured in the same run and reported under
-"configs": C1 (contiguous 128-position node), C3 (64-sequence continuous
-batch), C4 (4-bit KV, 131072 context, window 4096) and C5 (causal prefill,
-TFLOP/s against the bf16 MFMA peak).
+The other workloads are measured in the same run and reported under
+"configs", keyed by their --only selector: c1 (contiguous 128-position
+node), c3 (64-sequence continuous batch), c4 (4-bit KV, 131072 context,
+window 4096), c5 (causal prefill of 8192 tokens, TFLOP/s against the bf16
+MFMA peak), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV
+pool with host spill).
 
 roofline: the decode call (one decode kernel launch, split-K merge fused) timed with
 HIP events on the stream it is launched on, against 8 TB/s.
 cpu_baseline: the C restatement of ops::attention (oracle/, the reference's
-AVX-512 dot/axpy order, OpenMP over heads) on the host cores, one C2 layer at
-a time, 6 threads (the reference executor's rayon pool) and all cores.
+AVX-512 dot/axpy order, OpenMP over heads) on the host cores, one layer of
+the headline workload at a time, 6 threads (the reference executor's rayon pool) and all cores.
 """
 from __future__ import annotations
 
@@ -111,7 +113,7 @@ def paged_tables(rng, n_seqs, nblk, total):
 
 
 # ----------------------------------------------------------------------------
-# C2: 22-layer decode step (headline)
+# 22-layer decode step, ctx 4096 (headline; selector c2)
 # ----------------------------------------------------------------------------
 
 def bench_c2(nh, torch, steps, warmup, seed=0):
@@ -167,7 +169,7 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
 
 
 def cpu_baseline_c2(seed=0):
-    """Oracle (C restatement of ops::attention) on C2 layers, host cores."""
+    """Oracle (C restatement of ops::attention) on headline-workload layers, host cores."""
     import oracle
     import workloads as W
 
@@ -197,7 +199,7 @@ def cpu_baseline_c2(seed=0):
         "unit": "GB/s",
         "cores": thr6,
         "kind": "port",
-        "sample": (f"{n6} single-layer C2 decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
+        "sample": (f"{n6} single-layer decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
                    f"at {thr6} threads: {us6:.0f} us/layer; all {thra} cores: {usa:.0f} us/layer "
                    f"({bytes_layer / (usa * 1e-6) / 1e9:.2f} GB/s)"),
         "us_per_layer": us6,
@@ -591,21 +593,21 @@ def main():
         log("calibration copy: 3 x 512 MiB")
         del a, b
     if "c2" in only:
-        log("C2: 22-layer decode step, ctx 4096")
+        log("22-layer decode step, ctx 4096")
         res["c2"] = bench_c2(nh, torch, steps, warmup)
     if "c1" in only:
-        log("C1: contiguous 128-position node")
+        log("contiguous 128-position node")
         res["c1"] = bench_c1(nh, torch, steps, warmup)
     if "c3" in only:
-        log("C3: 64-sequence continuous batch")
+        log("64-sequence continuous batch")
         res["c3"] = bench_c3(nh, torch, steps, warmup)
         torch.cuda.empty_cache()
     if "c4" in only:
-        log("C4: Q4 KV, ctx 131072, window 4096")
+        log("Q4 KV, ctx 131072, window 4096")
         res["c4"] = bench_c4(nh, torch, steps, warmup)
         torch.cuda.empty_cache()
     if "c5" in only:
-        log("C5: causal prefill N=8192")
+        log("causal prefill N=8192")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
     if "pool" in only:
         log("paged KV pool: cold-page round trips over the host link")
@@ -618,7 +620,7 @@ def main():
         res["gemv_q6k"] = bench_gemv_q6k(nh, torch, steps, warmup, cpu=not args.no_cpu)
     cpu = None
     if not args.no_cpu and "c2" in only:
-        log("CPU baseline (oracle) on C2 layers")
+        log("CPU baseline (oracle) on headline-workload layers")
         cpu = cpu_baseline_c2()
 
     c2 = res.get("c2")

@@ -34,7 +34,7 @@ struct LayerState {
     size_t layer_floats() const { return (size_t)n_kv_heads * window * head_dim; }
 };
 
-// A4 position set of one sequence: sentinels stride*g (g < min(ws/stride,
+// attention_fugu position set of one sequence (ops.rs:445-541): sentinels stride*g (g < min(ws/stride,
 // 128)), the window [ws, valid_end], then each DSPark position <= valid_end
 // not already present, in input order.
 __global__ __launch_bounds__(256) void fugu_positions_kernel(

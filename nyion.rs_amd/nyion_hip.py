@@ -333,7 +333,7 @@ def fugu_decide_attention(seq_len, n_heads, head_dim, is_prefill=False, predicti
 
 def fugu_positions(ctx_lens, window, sentinel_stride, dspark, positions, n_positions, q_pos=None,
                    stream=None):
-    """Device A4 position sets: dspark [B][n] int32 -> positions [B][max], n_positions [B]."""
+    """Device attention_fugu position sets: dspark [B][n] int32 -> positions [B][max], n_positions [B]."""
     B = ctx_lens.shape[0]
     nd = 0 if dspark is None else dspark.shape[1]
     rc = load().nyion_fugu_positions(ptr(ctx_lens), ptr(q_pos), B, window, sentinel_stride,

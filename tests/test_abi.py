@@ -60,7 +60,7 @@ def test_no_device_is_reported_not_faked():
 
 def test_workspace_sizes_are_host_only():
     L = nyion_hip.load()
-    # C3-like: 64 seqs up to 32K tokens needs split-K partials
+    # 64 sequences up to 32K tokens needs split-K partials
     ws = L.nyion_paged_decode_workspace_size(64, 32, 4, 64, 32768, 0, 0)
     assert ws > 0
     # a single short sequence runs in one partition per head group: no workspace

@@ -1,6 +1,6 @@
 """Decode attention on the GPU against the oracle (gpu).
 
-Tolerance (BASELINE): max-abs-err <= 2e-3 and rel-err <= 1e-3, where rel-err
+Tolerance: max-abs-err <= 2e-3 and rel-err <= 1e-3, where rel-err
 is max|gpu - ref| / max|ref| over the compared tensor (fp32 accumulation on
 both sides).
 """
@@ -54,13 +54,13 @@ def test_attention_node_c1(gpu):
     out = torch.full_like(dq, float("nan"))
     gpu.attention_node(dq, dk, dv, out, 32, 4, 128, 64, 128)
     torch.cuda.synchronize()
-    assert_close(out.cpu().numpy(), ref, "node C1")
+    assert_close(out.cpu().numpy(), ref, "128-position node")
     # with the node's scores buffer as split-K workspace
     scores = torch.empty(32 * 128, dtype=torch.float32, device="cuda")
     out2 = torch.full_like(dq, float("nan"))
     gpu.attention_node(dq, dk, dv, out2, 32, 4, 128, 64, 128, scores=scores)
     torch.cuda.synchronize()
-    assert_close(out2.cpu().numpy(), ref, "node C1 + scores")
+    assert_close(out2.cpu().numpy(), ref, "128-position node + scores")
 
 
 def test_attention_node_stride_and_project_names(gpu):
@@ -88,9 +88,9 @@ def test_attention_node_stride_and_project_names(gpu):
 # ---------------------------------------------------------------- paged full causal
 
 def test_paged_c2_layer(gpu):
-    """BASELINE config 2, one layer: ctx 4096 in 16-token blocks, shuffled table."""
+    """One TinyLlama decode layer: ctx 4096 in 16-token blocks, shuffled table."""
     pb = W.paged_batch([4096], seed=2)
-    assert_close(run_paged(gpu, pb), W.reference_decode(pb), "C2 layer")
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), "ctx 4096 layer")
 
 
 @pytest.mark.parametrize("lens", [[1], [15, 16, 17], [1, 2, 31, 32, 33, 500, 1023, 1024, 1025]])
@@ -180,7 +180,7 @@ def test_paged_q_pos(gpu):
     assert_close(run_paged(gpu, pb, q_pos=q_pos), W.reference_decode(pb, q_pos=q_pos), "q_pos")
 
 
-# ---------------------------------------------------------------- tracked (A2)
+# ---------------------------------------------------------------- tracked (attention_tracked)
 
 def run_tracked(gpu, pb, q_pos=None, window=0, global_stride=0, init=None, stride_pad=5):
     q = to_dev(pb.q)
@@ -252,12 +252,12 @@ def test_paged_head_shapes(gpu, n_heads, n_kv, hd):
 
 
 def test_paged_c3_full_size(gpu):
-    """BASELINE config 3 at full size: 64 sequences, ctx ~ U[512, 32768]."""
+    """Continuous batch at full size: 64 sequences, ctx ~ U[512, 32768]."""
     lens = W.c3_lengths(seed=0)
     pb = W.paged_batch(lens, seed=0)
     got = run_paged(gpu, pb)
     ref = W.reference_decode(pb, threads=oracle.max_threads())
-    assert_close(got, ref, "C3")
+    assert_close(got, ref, "64-sequence batch")
 
 
 # ---------------------------------------------------------------- window / Q4
@@ -285,7 +285,7 @@ def test_q4_full_and_d128(gpu):
 
 
 def test_c4_full_size_window(gpu):
-    """B=8, ctx 131072, window 4096, Q4-20B.  Only the rows
+    """4-bit KV: B=8, ctx 131072, window 4096, Q4-20B.  Only the rows
     the position set touches hold quantised N(0,1) data; every other row is
     random bytes, so reading a wrong row shows up as garbage or NaN."""
     B, ctx, w, bt, hkv, hd = 8, 131072, 4096, 16, 4, 64
@@ -310,7 +310,7 @@ def test_c4_full_size_window(gpu):
                           oracle.KV_Q4, 9)
         got = run_paged(gpu, pb, window=w, global_stride=stride)
         ref = W.reference_decode(pb, window=w, global_stride=stride, threads=8)
-        assert_close(got, ref, f"C4 stride {stride}")
+        assert_close(got, ref, f"Q4 window stride {stride}")
 
 
 # ---------------------------------------------------------------- position lists

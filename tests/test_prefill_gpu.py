@@ -70,7 +70,7 @@ def test_prefill_non_causal(gpu):
 
 
 def test_prefill_c5_full_size_sampled_rows(gpu):
-    """N=8192, 32/8 heads, D=128; every output is computed,
+    """Causal prefill of 8192 tokens, 32/8 heads, D=128; every output is computed,
     416 rows (first, last and random) are checked against the oracle."""
     n = 8192
     q, k, v = W.prefill_inputs(n, 32, 8, 128, seed=0)
@@ -78,7 +78,7 @@ def test_prefill_c5_full_size_sampled_rows(gpu):
     rng = np.random.default_rng(5)
     rows = np.unique(np.concatenate([np.arange(64), np.arange(n - 64, n),
                                      rng.integers(0, n, 288)])).astype(np.int32)
-    check(got, oracle_rows(q, k, v, rows), rows, "C5")
+    check(got, oracle_rows(q, k, v, rows), rows, "prefill 8192")
     assert np.all(np.isfinite(got))
 
 

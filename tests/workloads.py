@@ -85,7 +85,7 @@ def paged_batch(ctx_lens, n_heads=32, n_kv_heads=4, head_dim=64, block_tokens=16
 
 
 def c1_contiguous(seed=0):
-    """B=1, 32/4 heads, D=64, contiguous f32 KV of 128 positions."""
+    """Contiguous node: B=1, 32/4 heads, D=64, contiguous f32 KV of 128 positions."""
     rng = np.random.default_rng(seed)
     q = _normal(rng, (32, 64))
     k = _normal(rng, (4, 128, 64))
@@ -94,14 +94,14 @@ def c1_contiguous(seed=0):
 
 
 def c3_lengths(seed=0, batch=64, lo=512, hi=32768):
-    """per-sequence context lengths ~ U[lo, hi]."""
+    """Continuous batch: per-sequence context lengths ~ U[lo, hi]."""
     rng = np.random.default_rng(seed)
     return rng.integers(lo, hi + 1, size=batch).astype(np.int32)
 
 
 def reference_decode(pb: PagedBatch, window=0, global_stride=0, q_pos=None, threads=1,
                      batches=None):
-    """Oracle output [B][Hq][D] for the batch (A1 or A3 semantics)."""
+    """Oracle output [B][Hq][D] for the batch (ops::attention or its sliding-window form)."""
     out = np.zeros_like(pb.q)
     for b in (range(pb.batch) if batches is None else batches):
         L = int(pb.ctx_lens[b])
@@ -118,7 +118,7 @@ def reference_decode(pb: PagedBatch, window=0, global_stride=0, q_pos=None, thre
 
 
 def prefill_inputs(n, n_heads=32, n_kv_heads=8, head_dim=128, seed=0):
-    """BASELINE config 5 shapes: fp32 N(0,1) q [n][Hq][D], k, v [n][Hkv][D]."""
+    """Prefill shapes: fp32 N(0,1) q [n][Hq][D], k, v [n][Hkv][D]."""
     rng = np.random.default_rng(seed)
     q = _normal(rng, (n, n_heads, head_dim))
     k = _normal(rng, (n, n_kv_heads, head_dim))
