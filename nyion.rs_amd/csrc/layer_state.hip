@@ -34,9 +34,9 @@ struct LayerState {
     size_t layer_floats() const { return (size_t)n_kv_heads * window * head_dim; }
 };
 
-// attention_fugu position set of one sequence (ops.rs:445-541): sentinels stride*g (g < min(ws/stride,
-// 128)), the window [ws, valid_end], then each DSPark position <= valid_end
-// not already present, in input order.
+// attention_fugu position set of one sequence (ops.rs:445-541): sentinels
+// stride*g (g < min(ws/stride, 128)), the window [ws, valid_end], then each
+// DSPark position <= valid_end not already present, in input order.
 __global__ __launch_bounds__(256) void fugu_positions_kernel(
     const int32_t* ctx_lens, const int32_t* q_pos, int window, int sentinel_stride,
     const int32_t* dspark, int n_dspark, int dspark_stride, int32_t* positions, int max_positions,
