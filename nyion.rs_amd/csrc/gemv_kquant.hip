@@ -561,6 +561,11 @@ int nyion_gemv_specs(const nyion_gemv_spec* specs, int n_specs, nyion_stream_t s
             return set_error(NYION_ERR_INVALID, "gemv specs: spec %d: %d x %d", i, g.n_rows, g.n_cols);
         if (g.n_rows > 0 && (!g.w || !g.x || !g.out))
             return set_error(NYION_ERR_INVALID, "gemv specs: spec %d: null pointer", i);
+        const bool w_ok = g.block_bytes == Q4kFormat::kBlockBytes ? weights_aligned<Q4kFormat>(g.w)
+                                                                 : weights_aligned<Q6kFormat>(g.w);
+        if (g.n_rows > 0 && (!w_ok || !aligned(g.x, 16)))
+            return set_error(NYION_ERR_INVALID, "gemv specs: spec %d: W or x not aligned (x 16 bytes, "
+                                                "Q4_K W 16 bytes, Q6_K W 2 bytes)", i);
     }
     // specs of one format, width and input share a launch (up to four each)
     std::vector<char> done(n_specs, 0);

@@ -184,6 +184,11 @@ def test_gemv_q6k_rejects_bad_arguments(gpu):
                                gpu.GemvSpec(w.data_ptr(), x.data_ptr(), out.data_ptr(), 1, 256, 200, 0))
     assert L.nyion_gemv_specs(specs, 2, None) != 0
     assert "block_bytes" in gpu.last_error()
+    # so does a misaligned spec after a valid group
+    specs = (gpu.GemvSpec * 2)(gpu.GemvSpec(w.data_ptr(), x.data_ptr(), out.data_ptr(), 2, 512, 210, 0),
+                               gpu.GemvSpec(w.data_ptr(), x.data_ptr() + 4, out.data_ptr(), 1, 256, 144, 0))
+    assert L.nyion_gemv_specs(specs, 2, None) != 0
+    assert "aligned" in gpu.last_error()
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), torch.full((2,), 7.0))
     assert L.nyion_gemv_specs(None, 0, None) == 0
