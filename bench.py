@@ -153,11 +153,22 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
 
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
     ms = timed(step, steps, warmup, torch)
+    # spread of the step time: each of another `steps` steps between two events
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(st)
+        step(i)
+        e1.record(st)
+    torch.cuda.synchronize()
+    p10, p50, p90 = np.percentile([e0.elapsed_time(e1) for e0, e1 in evs], [10, 50, 90])
     # roofline: decode calls timed with HIP events on the launching stream
     us_call = event_mean(lambda i: layer_call(i % R, i % L), steps * L, torch) * 1e3
     achieved = bytes_layer / (us_call * 1e-6) / 1e9
     return {
         "ms_per_step": ms,
+        "step_ms_p10_p50_p90": [round(float(x), 4) for x in (p10, p50, p90)],
         "us_per_layer": ms * 1e3 / L,
         "gbs": L * bytes_layer / (ms * 1e-3) / 1e9,
         "bytes_per_layer": bytes_layer,
@@ -207,6 +218,123 @@ def cpu_baseline_c2(seed=0):
         "cores_all": thra,
         "cpu_model": _cpu_model(),
     }
+
+
+def _cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _cpu_time(fn, budget_s=2.0, max_calls=2000):
+    """Mean seconds per call of fn after one warm call, over about budget_s."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= max_calls:
+            return el / n, n
+
+
+def cpu_baseline_c1():
+    """Oracle on the contiguous 128-position node (all host cores)."""
+    import oracle
+    import workloads as W
+
+    q, k, v = W.c1_contiguous(seed=0)
+    lay = oracle.contiguous_layout(k, v, 128, 64)
+    thr = _cores()
+    dt, n = _cpu_time(lambda: oracle.attention(q.reshape(-1), lay, 128, 127, 32, 4, 64, threads=thr))
+    nbytes = 278528
+    return {"value": dt * 1e6, "unit": "us/layer", "cores": thr, "kind": "port",
+            "gbs": nbytes / dt / 1e9,
+            "sample": f"{n} calls of the whole node (32/4 heads, D=64, 128 positions)"}
+
+
+def cpu_baseline_c3(seed=0, n_sample=2):
+    """Oracle on the first n_sample sequences of the 64-sequence batch (same
+    context lengths), extrapolated to the batch by attended tokens."""
+    import oracle
+    import workloads as W
+
+    lens = W.c3_lengths(seed=seed)
+    pb = W.paged_batch([int(x) for x in lens[:n_sample]], seed=seed)
+    thr = _cores()
+
+    def run():
+        for b in range(n_sample):
+            oracle.attention(pb.q[b], pb.layout(b), int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
+                             threads=thr)
+
+    dt, n = _cpu_time(run)
+    toks_sample, toks_all = int(lens[:n_sample].sum()), int(lens.sum())
+    est = dt * toks_all / toks_sample
+    nbytes = 2 * toks_all * 4 * 64 * 4
+    return {"value": est * 1e6, "unit": "us/layer (extrapolated)", "cores": thr, "kind": "port",
+            "gbs": nbytes / est / 1e9,
+            "sample": (f"{n} runs over sequences 0-{n_sample - 1} ({toks_sample} tokens, "
+                       f"{dt * 1e6:.0f} us), scaled by tokens to the batch's {toks_all}")}
+
+
+def cpu_baseline_c4(seed=0):
+    """Oracle on the 4-bit window workload: 8 sequences, ctx 131072, window
+    4096 (the attended rows quantised, Q4-20B)."""
+    import oracle
+    import workloads as W
+
+    B, ctx, w, bt, hkv, hd = 8, 131072, 4096, 16, 4, 64
+    rng = np.random.default_rng(seed)
+    nblk = ctx // bt
+    tables = rng.permutation(B * nblk).astype(np.int32).reshape(B, nblk)
+    rb = oracle.q4_row_bytes(hd)
+    kp = np.zeros((B * nblk, hkv, bt, rb), np.uint8)
+    vp = np.zeros_like(kp)
+    pos = oracle.sparse_positions(ctx, ctx - 1, w, 0)
+    for b in range(B):
+        blk = tables[b, pos // bt]
+        kp[blk, :, pos % bt] = oracle.q4_quantize_rows(rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+        vp[blk, :, pos % bt] = oracle.q4_quantize_rows(rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+    q = rng.standard_normal((B, 32, hd), dtype=np.float32)
+    pb = W.PagedBatch(q, kp, vp, tables, np.full(B, ctx, np.int32), 32, hkv, hd, bt, oracle.KV_Q4, seed)
+    thr = _cores()
+
+    def run():
+        for b in range(B):
+            oracle.attention_positions(q[b], pb.layout(b), pos, 32, hkv, hd, threads=thr)
+
+    dt, n = _cpu_time(run)
+    nbytes = 2 * B * len(pos) * hkv * rb
+    return {"value": dt * 1e6, "unit": "us/layer", "cores": thr, "kind": "port",
+            "gbs_packed": nbytes / dt / 1e9,
+            "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0"}
+
+
+def cpu_baseline_c5(seed=0, n_rows=256):
+    """The reference's prefill: one decode call per row (executor.rs:132-137),
+    timed on n_rows rows spread over the 8192 and scaled by attended keys."""
+    import oracle
+    import workloads as W
+
+    n, hq, hkv, d = 8192, 32, 8, 128
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=seed)
+    qb, kb, vb = W.bf16_round(q), W.bf16_round(k), W.bf16_round(v)
+    lay = oracle.token_major_layout(kb, vb, hkv, d)
+    rows = np.linspace(0, n - 1, n_rows).astype(np.int32)
+    thr = _cores()
+    qf = qb.reshape(n, -1)
+    dt, runs = _cpu_time(lambda: oracle.attention_rows(qf, lay, rows, hq, hkv, d, threads=thr),
+                         budget_s=3.0, max_calls=50)
+    keys_sample = float((rows.astype(np.int64) + 1).sum())
+    keys_all = n * (n + 1) / 2.0
+    est = dt * keys_all / keys_sample
+    flops = 4 * hq * d * keys_all
+    return {"value": flops / est / 1e12, "unit": "TFLOP/s (extrapolated)", "cores": thr,
+            "kind": "port", "us_extrapolated": est * 1e6,
+            "sample": (f"{runs} runs of {n_rows} evenly spaced rows, all 32 heads "
+                       f"({dt * 1e3:.1f} ms), scaled by attended keys to all 8192 rows")}
 
 
 def _cpu_model():
@@ -618,6 +746,12 @@ def main():
     if "gemv6" in only:
         log("Q6_K weight GEMV: TinyLlama output projection, Q4_K_M-style decode step")
         res["gemv_q6k"] = bench_gemv_q6k(nh, torch, steps, warmup, cpu=not args.no_cpu)
+    if not args.no_cpu:
+        for key, fn in (("c1", cpu_baseline_c1), ("c3", cpu_baseline_c3), ("c4", cpu_baseline_c4),
+                        ("c5", cpu_baseline_c5)):
+            if key in res:
+                log(f"CPU baseline (oracle) for {key}")
+                res[key]["cpu_baseline"] = fn()
     cpu = None
     if not args.no_cpu and "c2" in only:
         log("CPU baseline (oracle) on headline-workload layers")
@@ -643,6 +777,7 @@ def main():
     }
     if c2:
         line["us_per_layer"] = round(c2["us_per_layer"], 3)
+        line["ms_per_step_p10_p50_p90"] = c2["step_ms_p10_p50_p90"]
         line["roofline"] = {
             "bound": "hbm",
             "achieved": round(c2["achieved_call_gbs"], 2),
