@@ -92,6 +92,21 @@ int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float
                            float* d_output, int n_heads, int n_kv_heads, int seq_len,
                            int head_dim, int kv_stride, nyion_stream_t stream);
 
+/* The node captured once into a HIP graph and replayed (the project ABI of
+ * fused_attention.cu:595-663: gpu_graph_create_attention,
+ * gpu_graph_replay_attention, gpu_graph_destroy).  Every argument is fixed at
+ * creation; d_scores (n_heads*kv_stride floats, 256-byte aligned, or NULL)
+ * is the node's scratch as for nyion_attention_node, its counters cleared
+ * inside the graph by a fill kernel.  create returns NULL on error (message
+ * in nyion_last_error()); replay returns 0 / -1.  Replays of one graph on
+ * different streams must not overlap (they share d_scores and d_output). */
+void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache,
+                                 const float* d_v_cache, float* d_scores, float* d_output,
+                                 int n_heads, int n_kv_heads, int seq_len, int head_dim,
+                                 int kv_stride);
+int gpu_graph_replay_attention(void* graph_handle, nyion_stream_t stream);
+void gpu_graph_destroy(void* graph_handle);
+
 /* Batched paged GQA decode with split-K partitions and a log-sum-exp merge.
  * Replaces the CPU decode call of the executor (executor.rs:739-763):
  *   window <= 0           : ops::attention / attention_tracked semantics

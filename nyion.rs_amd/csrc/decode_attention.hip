@@ -1363,4 +1363,60 @@ int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* 
                                   head_dim, kv_stride, nullptr);
 }
 
+void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache, const float* d_v_cache,
+                                 float* d_scores, float* d_output, int n_heads, int n_kv_heads,
+                                 int seq_len, int head_dim, int kv_stride) {
+    clear_error();
+    if (require_device() != NYION_OK) return nullptr;
+    if (n_heads <= 0 || n_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0 || kv_stride <= 0) {
+        set_error(NYION_ERR_INVALID, "gpu_graph_create_attention: non-positive size");
+        return nullptr;
+    }
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+        set_error(NYION_ERR_LAUNCH, "gpu_graph_create_attention: stream: %s", hipGetErrorString(hipGetLastError()));
+        return nullptr;
+    }
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = NYION_OK;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        rc = set_error(NYION_ERR_LAUNCH, "gpu_graph_create_attention: begin capture failed");
+    } else {
+        // the node records its launches (and, with d_scores, the fill kernel
+        // that clears its arrival counters) on the capturing stream
+        rc = nyion_attention_node(d_q, d_k_cache, d_v_cache, d_scores, d_output, (uint32_t)n_heads,
+                                  (uint32_t)n_kv_heads, (uint32_t)seq_len, (uint32_t)head_dim,
+                                  (uint32_t)kv_stride, NYION_KV_F32, s);
+        const hipError_t e = hipStreamEndCapture(s, &graph);
+        if (rc == NYION_OK && e != hipSuccess)
+            rc = set_error(NYION_ERR_LAUNCH, "gpu_graph_create_attention: end capture: %s", hipGetErrorString(e));
+        if (rc == NYION_OK && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            rc = set_error(NYION_ERR_LAUNCH, "gpu_graph_create_attention: instantiate failed");
+            exec = nullptr;
+        }
+    }
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipStreamDestroy(s);
+    return rc == NYION_OK ? (void*)exec : nullptr;
+}
+
+int gpu_graph_replay_attention(void* graph_handle, nyion_stream_t stream) {
+    clear_error();
+    if (!graph_handle) {
+        set_error(NYION_ERR_INVALID, "gpu_graph_replay_attention: null graph");
+        return -1;
+    }
+    const hipError_t e = hipGraphLaunch((hipGraphExec_t)graph_handle, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        set_error(NYION_ERR_LAUNCH, "gpu_graph_replay_attention: %s", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+void gpu_graph_destroy(void* graph_handle) {
+    if (graph_handle) (void)hipGraphExecDestroy((hipGraphExec_t)graph_handle);
+}
+
 }  // extern "C"

@@ -125,6 +125,9 @@ SIGNATURES = {
     "nyion_gemv_q6k": (i32, [vp, vp, vp, i32, i32, vp]),
     "nyion_gemv_q6k_batched": (i32, [vp, vp, i64, vp, i64, i32, i32, i32, vp]),
     "nyion_gemv_specs": (i32, [vp, i32, vp]),
+    "gpu_graph_create_attention": (vp, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "gpu_graph_replay_attention": (i32, [vp, vp]),
+    "gpu_graph_destroy": (None, [vp]),
     "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
     "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
                                    i32, i32, i32, vp]),

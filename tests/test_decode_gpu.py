@@ -63,6 +63,46 @@ def test_attention_node_c1(gpu):
     assert_close(out2.cpu().numpy(), ref, "128-position node + scores")
 
 
+@pytest.mark.parametrize("with_scores", [False, True])
+def test_graph_attention_replays_equal_eager(gpu, with_scores):
+    """gpu_graph_create_attention / replay / destroy (fused_attention.cu:595-663):
+    every replay equals the eager node bit for bit, with eager work and
+    synchronisations between replays; with the scores scratch the split-K
+    counters are cleared inside the graph by a kernel, not a memset."""
+    rng = np.random.default_rng(31)
+    S, stride = 3000, 3072
+    q = rng.standard_normal((32, 64), dtype=np.float32)
+    k = rng.standard_normal((4, stride, 64), dtype=np.float32)
+    v = rng.standard_normal((4, stride, 64), dtype=np.float32)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    scores = torch.empty(32 * stride, dtype=torch.float32, device="cuda") if with_scores else None
+    eager = torch.empty_like(dq)
+    gpu.attention_node(dq, dk, dv, eager, 32, 4, S, 64, stride, scores=scores)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.reshape(-1), oracle.contiguous_layout(k, v, stride, 64), S, S - 1, 32,
+                           4, 64).reshape(32, 64)
+    assert_close(eager.cpu().numpy(), ref, "eager node")
+    L = gpu.load()
+    out = torch.full_like(dq, float("nan"))
+    g = L.gpu_graph_create_attention(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                     scores.data_ptr() if with_scores else None, out.data_ptr(),
+                                     32, 4, S, 64, stride)
+    assert g, gpu.last_error()
+    try:
+        stream = torch.cuda.current_stream().cuda_stream
+        for rep in range(4):
+            out.fill_(float("nan"))
+            other = torch.empty_like(dq)
+            gpu.attention_node(dq, dk, dv, other, 32, 4, S // 2, 64, stride, scores=scores)
+            torch.cuda.synchronize()
+            assert L.gpu_graph_replay_attention(g, stream) == 0, gpu.last_error()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), rep
+    finally:
+        L.gpu_graph_destroy(g)
+    assert L.gpu_graph_replay_attention(None, None) == -1
+
+
 def test_attention_node_stride_and_project_names(gpu):
     rng = np.random.default_rng(21)
     S, stride = 1000, 1536
