@@ -17,7 +17,8 @@
  * partial results go into a caller-provided workspace.
  *
  * KV pool layout (paged):   [num_blocks][n_kv_heads][block_tokens][row]
- *   row = head_dim f32 (NYION_KV_F32) or ceil(head_dim/32)*20 bytes of the
+ *   row = head_dim f32 (NYION_KV_F32), head_dim binary16 (NYION_KV_F16) or
+ *   ceil(head_dim/32)*20 bytes of the
  *   reference's Q4-20B groups (NYION_KV_Q4_20B: f16 d, f16 dmin, 16 nibble
  *   bytes; element i of a group in byte 4+i/2, low nibble when i is even;
  *   swamp-engine/src/cache.rs:637-663, 375-394).
@@ -46,7 +47,10 @@ enum nyion_status {
     NYION_ERR_WORKSPACE = -6    /* caller workspace too small */
 };
 
-enum nyion_kv_dtype { NYION_KV_F32 = 0, NYION_KV_Q4_20B = 1 };
+/* KV row formats: f32; the reference's Q4-20B groups; IEEE binary16 (the
+ * f16 caches of the reference's CUDA path, fused_attention.cu:534-545;
+ * written with round-to-nearest-even, read exactly). */
+enum nyion_kv_dtype { NYION_KV_F32 = 0, NYION_KV_Q4_20B = 1, NYION_KV_F16 = 2 };
 
 /* ---------------------------------------------------------------- runtime */
 
@@ -107,6 +111,19 @@ void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache,
 int gpu_graph_replay_attention(void* graph_handle, nyion_stream_t stream);
 void gpu_graph_destroy(void* graph_handle);
 
+/* The same two on binary16 K/V caches (NYION_KV_F16 rows, [n_kv_heads]
+ * [kv_stride][head_dim], 8-byte aligned): gpu_attention_streamed_half
+ * (fused_attention.cu:534-545) and gpu_graph_create_attention_half
+ * (fused_attention.cu:672-717).  K/V values are widened to f32 exactly. */
+int gpu_attention_streamed_half(const float* d_q, const uint16_t* d_k_cache,
+                                const uint16_t* d_v_cache, float* d_output, int n_heads,
+                                int n_kv_heads, int seq_len, int head_dim, int kv_stride,
+                                nyion_stream_t stream);
+void* gpu_graph_create_attention_half(const float* d_q, const uint16_t* d_k_cache,
+                                      const uint16_t* d_v_cache, float* d_scores,
+                                      float* d_output, int n_heads, int n_kv_heads, int seq_len,
+                                      int head_dim, int kv_stride);
+
 /* Batched paged GQA decode with split-K partitions and a log-sum-exp merge.
  * Replaces the CPU decode call of the executor (executor.rs:739-763):
  *   window <= 0           : ops::attention / attention_tracked semantics
@@ -119,6 +136,8 @@ void gpu_graph_destroy(void* graph_handle);
  *                           valid_end-window+1 if valid_end > window else 0.
  *   kv_dtype Q4_20B       : K/V dequantised in registers exactly as
  *                           dequant_block (cache.rs:375-394).
+ *   kv_dtype F16          : K/V binary16 rows widened exactly to f32 (the
+ *                           same results as f32 pools holding those values).
  * d_q, d_out: [batch][n_heads][head_dim] f32.  ctx_lens[batch] (>= 1);
  * q_pos[batch] or NULL (= ctx_len-1).  max_ctx: host upper bound of ctx_lens,
  * sizes the grid.  scale <= 0 means 1/sqrt(head_dim).

@@ -51,6 +51,8 @@
 namespace nyion {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 enum DecodeMode { MODE_FULL = 0, MODE_WINDOW = 1, MODE_LIST = 2 };
 
@@ -166,7 +168,7 @@ __device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e,
 // kq), row 4kq+r: DPL = D/16 consecutive dims from DPL*j.
 template <int D, int KVT>
 __device__ __forceinline__ int qk_dim(int c, int kq) {
-    if constexpr (KVT == NYION_KV_F32)
+    if constexpr (KVT != NYION_KV_Q4_20B)
         return 16 * (c >> 2) + 4 * kq + (c & 3);
     else
         return kq * (D / 4) + c;
@@ -183,6 +185,12 @@ struct Tile<D, NYION_KV_F32> {
 };
 
 template <int D>
+struct Tile<D, NYION_KV_F16> {
+    u32x2 k[D / 16];          // K row j: dims 16x + 4kq .. +3, four binary16 values
+    u32x2 v[4][D / 64];       // V rows 4kq+r: dims DPL*j + 4x .. +3
+};
+
+template <int D>
 struct Tile<D, NYION_KV_Q4_20B> {
     uint32_t khdr;            // f16 d | f16 dmin << 16 of the lane's K group
     uint32_t k[D / 32];       // D/4 nibbles of K row j
@@ -196,7 +204,19 @@ struct Tile<D, NYION_KV_Q4_20B> {
 template <int D, int KVT>
 __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const void* vb,
                                           long long koff, const long long* voff, int j, int kq) {
-    if constexpr (KVT == NYION_KV_F32) {
+    if constexpr (KVT == NYION_KV_F16) {
+        const uint16_t* kr = (const uint16_t*)kb + koff;
+#pragma unroll
+        for (int x = 0; x < D / 16; x++)
+            t.k[x] = __builtin_nontemporal_load((const u32x2*)(kr + 16 * x + 4 * kq));
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint16_t* vr = (const uint16_t*)vb + voff[r] + (D / 16) * j;
+#pragma unroll
+            for (int x = 0; x < D / 64; x++)
+                t.v[r][x] = __builtin_nontemporal_load((const u32x2*)(vr + 4 * x));
+        }
+    } else if constexpr (KVT == NYION_KV_F32) {
         const float* kr = (const float*)kb + koff;
 #pragma unroll
         for (int x = 0; x < D / 16; x++)
@@ -229,9 +249,24 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
     }
 }
 
+// Four binary16 values (two words) -> f32, exact.  The words are copied to
+// scalars first: this compiler's __builtin_bit_cast of a vector element
+// (w[1]) yields the bits of element 0.
+__device__ __forceinline__ void f16x4_to_f32(u32x2 w, float* out) {
+    const uint32_t w0 = w[0], w1 = w[1];
+    const halfx2 lo = __builtin_bit_cast(halfx2, w0), hi = __builtin_bit_cast(halfx2, w1);
+    out[0] = (float)lo[0];
+    out[1] = (float)lo[1];
+    out[2] = (float)hi[0];
+    out[3] = (float)hi[1];
+}
+
 template <int D, int KVT>
 __device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
-    if constexpr (KVT == NYION_KV_F32) {
+    if constexpr (KVT == NYION_KV_F16) {
+#pragma unroll
+        for (int x = 0; x < D / 16; x++) f16x4_to_f32(t.k[x], kv + 4 * x);
+    } else if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
         for (int x = 0; x < D / 16; x++) {
             kv[4 * x + 0] = t.k[x].x;
@@ -248,7 +283,10 @@ __device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
 
 template <int D, int KVT>
 __device__ __forceinline__ void decode_v(const Tile<D, KVT>& t, int r, float* vv) {
-    if constexpr (KVT == NYION_KV_F32) {
+    if constexpr (KVT == NYION_KV_F16) {
+#pragma unroll
+        for (int x = 0; x < D / 64; x++) f16x4_to_f32(t.v[r][x], vv + 4 * x);
+    } else if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
         for (int x = 0; x < D / 64; x++) {
             vv[4 * x + 0] = t.v[r][x].x;
@@ -376,7 +414,7 @@ __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const A
         mask = 0;
     }
     // rows of a paged pool are contiguous: the token stride is the row size
-    constexpr int TS = KVT == NYION_KV_F32 ? D : q4_row_bytes(D);
+    constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
     const long long base = (long long)blk * a.block_stride + w.head_off +
                            (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
     koff = base + j * TS;
@@ -901,7 +939,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
                          n_heads, n_kv_heads);
     if (head_dim != 64 && head_dim != 128)
         return set_error(NYION_ERR_UNSUPPORTED, "decode: head_dim %d (supported: 64, 128)", head_dim);
-    if (kvt != NYION_KV_F32 && kvt != NYION_KV_Q4_20B)
+    if (kvt != NYION_KV_F32 && kvt != NYION_KV_Q4_20B && kvt != NYION_KV_F16)
         return set_error(NYION_ERR_INVALID, "decode: kv_dtype %d", kvt);
     if (max_main <= 0) return set_error(NYION_ERR_INVALID, "decode: max_ctx must be positive");
     DecodeArgs& a = pl.a;
@@ -1038,22 +1076,27 @@ static void launch_dkt(const DecodePlan& pl, hipStream_t stream) {
 static int launch_plan(const DecodePlan& pl, hipStream_t stream) {
     if (pl.head_dim == 64 && pl.kvt == NYION_KV_F32)
         launch_dkt<64, NYION_KV_F32>(pl, stream);
+    else if (pl.head_dim == 64 && pl.kvt == NYION_KV_F16)
+        launch_dkt<64, NYION_KV_F16>(pl, stream);
     else if (pl.head_dim == 64)
         launch_dkt<64, NYION_KV_Q4_20B>(pl, stream);
     else if (pl.kvt == NYION_KV_F32)
         launch_dkt<128, NYION_KV_F32>(pl, stream);
+    else if (pl.kvt == NYION_KV_F16)
+        launch_dkt<128, NYION_KV_F16>(pl, stream);
     else
         launch_dkt<128, NYION_KV_Q4_20B>(pl, stream);
     return check_launch("decode");
 }
 
+// Row size in the pool's own units: f32 or f16 elements, Q4-20B bytes.
 static long long row_elems(int head_dim, int kvt) {
-    return kvt == NYION_KV_F32 ? head_dim : q4_row_bytes(head_dim);
+    return kvt == NYION_KV_Q4_20B ? q4_row_bytes(head_dim) : head_dim;
 }
 
 static int check_pool_ptrs(const void* k, const void* v, int kvt) {
     if (!k || !v) return set_error(NYION_ERR_INVALID, "decode: null K/V pool");
-    const size_t al = kvt == NYION_KV_F32 ? 16 : 4;
+    const size_t al = kvt == NYION_KV_F32 ? 16 : kvt == NYION_KV_F16 ? 8 : 4;
     if (!aligned(k, al) || !aligned(v, al))
         return set_error(NYION_ERR_INVALID, "decode: K/V pools must be %zu-byte aligned", al);
     return NYION_OK;
@@ -1363,9 +1406,12 @@ int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* 
                                   head_dim, kv_stride, nullptr);
 }
 
-void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache, const float* d_v_cache,
-                                 float* d_scores, float* d_output, int n_heads, int n_kv_heads,
-                                 int seq_len, int head_dim, int kv_stride) {
+}  // extern "C"
+
+// The attention node captured on a private stream and instantiated.
+static void* graph_create_node(const float* d_q, const void* d_k_cache, const void* d_v_cache,
+                               float* d_scores, float* d_output, int n_heads, int n_kv_heads,
+                               int seq_len, int head_dim, int kv_stride, int kv_dtype) {
     clear_error();
     if (require_device() != NYION_OK) return nullptr;
     if (n_heads <= 0 || n_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0 || kv_stride <= 0) {
@@ -1387,7 +1433,7 @@ void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache, const
         // that clears its arrival counters) on the capturing stream
         rc = nyion_attention_node(d_q, d_k_cache, d_v_cache, d_scores, d_output, (uint32_t)n_heads,
                                   (uint32_t)n_kv_heads, (uint32_t)seq_len, (uint32_t)head_dim,
-                                  (uint32_t)kv_stride, NYION_KV_F32, s);
+                                  (uint32_t)kv_stride, kv_dtype, s);
         const hipError_t e = hipStreamEndCapture(s, &graph);
         if (rc == NYION_OK && e != hipSuccess)
             rc = set_error(NYION_ERR_LAUNCH, "gpu_graph_create_attention: end capture: %s", hipGetErrorString(e));
@@ -1399,6 +1445,37 @@ void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache, const
     if (graph) (void)hipGraphDestroy(graph);
     (void)hipStreamDestroy(s);
     return rc == NYION_OK ? (void*)exec : nullptr;
+}
+
+extern "C" {
+
+void* gpu_graph_create_attention(const float* d_q, const float* d_k_cache, const float* d_v_cache,
+                                 float* d_scores, float* d_output, int n_heads, int n_kv_heads,
+                                 int seq_len, int head_dim, int kv_stride) {
+    return graph_create_node(d_q, d_k_cache, d_v_cache, d_scores, d_output, n_heads, n_kv_heads,
+                             seq_len, head_dim, kv_stride, NYION_KV_F32);
+}
+
+void* gpu_graph_create_attention_half(const float* d_q, const uint16_t* d_k_cache,
+                                      const uint16_t* d_v_cache, float* d_scores, float* d_output,
+                                      int n_heads, int n_kv_heads, int seq_len, int head_dim,
+                                      int kv_stride) {
+    return graph_create_node(d_q, d_k_cache, d_v_cache, d_scores, d_output, n_heads, n_kv_heads,
+                             seq_len, head_dim, kv_stride, NYION_KV_F16);
+}
+
+int gpu_attention_streamed_half(const float* d_q, const uint16_t* d_k_cache,
+                                const uint16_t* d_v_cache, float* d_output, int n_heads,
+                                int n_kv_heads, int seq_len, int head_dim, int kv_stride,
+                                nyion_stream_t stream) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0 || kv_stride <= 0) {
+        set_error(NYION_ERR_INVALID, "gpu_attention_streamed_half: non-positive size");
+        return -1;
+    }
+    const int rc = nyion_attention_node(d_q, d_k_cache, d_v_cache, nullptr, d_output,
+                                        (uint32_t)n_heads, (uint32_t)n_kv_heads, (uint32_t)seq_len,
+                                        (uint32_t)head_dim, (uint32_t)kv_stride, NYION_KV_F16, stream);
+    return rc == NYION_OK ? 0 : -1;
 }
 
 int gpu_graph_replay_attention(void* graph_handle, nyion_stream_t stream) {

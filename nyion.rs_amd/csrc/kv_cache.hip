@@ -89,8 +89,16 @@ __device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r,
     return row_offset(m, pos, h);
 }
 
-// One thread per (row, head, 4 floats).
-__global__ void kv_write_f32_kernel(WriteArgs a) {
+typedef _Float16 halfx2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> one word of two binary16 (round to nearest even), lo first.
+__device__ __forceinline__ uint32_t f16x2_bits(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, halfx2_t{(_Float16)lo, (_Float16)hi});
+}
+
+// One thread per (row, head, 4 values): f32 rows, or binary16 rows (F16).
+template <bool F16>
+__global__ void kv_write_flat_kernel(WriteArgs a) {
     const int vec = a.head_dim / 4;
     const long long n = (long long)a.rows * a.n_kv_heads * vec;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
@@ -109,8 +117,13 @@ __global__ void kv_write_f32_kernel(WriteArgs a) {
             kk = *(const float4*)(a.k + src);
             vv = *(const float4*)(a.v + src);
         }
-        *(float4*)((float*)a.k_pool + off + 4 * x) = kk;
-        *(float4*)((float*)a.v_pool + off + 4 * x) = vv;
+        if (F16) {
+            *(uint2*)((uint16_t*)a.k_pool + off + 4 * x) = uint2{f16x2_bits(kk.x, kk.y), f16x2_bits(kk.z, kk.w)};
+            *(uint2*)((uint16_t*)a.v_pool + off + 4 * x) = uint2{f16x2_bits(vv.x, vv.y), f16x2_bits(vv.z, vv.w)};
+        } else {
+            *(float4*)((float*)a.k_pool + off + 4 * x) = kk;
+            *(float4*)((float*)a.v_pool + off + 4 * x) = vv;
+        }
     }
 }
 
@@ -189,7 +202,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a, long lo
             continue;
         }
         const long long j = i - nq;
-        const int units = KVT == NYION_KV_F32 ? half : (D + 31) / 32;
+        const int units = KVT == NYION_KV_Q4_20B ? (D + 31) / 32 : half;
         const int u = (int)(j % units);
         const int h = (int)((j / units) % a.w.n_kv_heads);
         const int b = (int)(j / ((long long)units * a.w.n_kv_heads));
@@ -202,6 +215,11 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a, long lo
             const float2 r = rope_pair(a.k[src + 2 * u], a.k[src + 2 * u + 1], cs[u]);
             *(float2*)((float*)a.w.k_pool + off + 2 * u) = r;
             *(float2*)((float*)a.w.v_pool + off + 2 * u) = *(const float2*)(a.w.v + src + 2 * u);
+        } else if constexpr (KVT == NYION_KV_F16) {
+            const float2 r = rope_pair(a.k[src + 2 * u], a.k[src + 2 * u + 1], cs[u]);
+            *(uint32_t*)((uint16_t*)a.w.k_pool + off + 2 * u) = f16x2_bits(r.x, r.y);
+            const float2 vv = *(const float2*)(a.w.v + src + 2 * u);
+            *(uint32_t*)((uint16_t*)a.w.v_pool + off + 2 * u) = f16x2_bits(vv.x, vv.y);
         } else {
             const int len = min(32, D - 32 * u);
             float kb[32];
@@ -274,6 +292,14 @@ __global__ void kv_gather_kernel(GatherArgs a) {
         } else if (a.kvt == NYION_KV_F32) {
             const float* src = (const float*)a.pool + off + 8 * x;
             for (int e = 0; e < 8; e++) vals[e] = src[e];
+        } else if (a.kvt == NYION_KV_F16) {
+            const uint4 w = *(const uint4*)((const uint16_t*)a.pool + off + 8 * x);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            for (int e = 0; e < 4; e++) {
+                const halfx2_t hv = __builtin_bit_cast(halfx2_t, ws[e]);
+                vals[2 * e] = (float)hv[0];
+                vals[2 * e + 1] = (float)hv[1];
+            }
         } else {
             const uint8_t* row = (const uint8_t*)a.pool + off;
             const int e0 = 8 * x;
@@ -353,6 +379,12 @@ static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_t
                              head_dim);
         if (!aligned(k_pool, 16) || !aligned(v_pool, 16))
             return set_error(NYION_ERR_INVALID, "kv write f32: pools must be 16-byte aligned");
+    } else if (kv_dtype == NYION_KV_F16) {
+        if (head_dim <= 0 || head_dim % 4)
+            return set_error(NYION_ERR_UNSUPPORTED, "kv write f16: head_dim %d not a multiple of 4",
+                             head_dim);
+        if (!aligned(k_pool, 8) || !aligned(v_pool, 8))
+            return set_error(NYION_ERR_INVALID, "kv write f16: pools must be 8-byte aligned");
     } else if (kv_dtype == NYION_KV_Q4_20B) {
         if (head_dim <= 0) return set_error(NYION_ERR_INVALID, "kv write q4: head_dim");
         if (!aligned(k_pool, 4) || !aligned(v_pool, 4))
@@ -360,7 +392,7 @@ static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_t
     } else {
         return set_error(NYION_ERR_INVALID, "kv write: kv_dtype %d", kv_dtype);
     }
-    const long long row = kv_dtype == NYION_KV_F32 ? head_dim : q4_row_bytes(head_dim);
+    const long long row = kv_dtype == NYION_KV_Q4_20B ? q4_row_bytes(head_dim) : head_dim;
     a.k_pool = k_pool;
     a.v_pool = v_pool;
     a.n_kv_heads = n_kv_heads;
@@ -374,9 +406,12 @@ static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_t
 }
 
 static int launch_write(const WriteArgs& a, int kv_dtype, hipStream_t stream) {
-    if (kv_dtype == NYION_KV_F32) {
+    if (kv_dtype == NYION_KV_F32 || kv_dtype == NYION_KV_F16) {
         const long long n = (long long)a.rows * a.n_kv_heads * (a.head_dim / 4);
-        hipLaunchKernelGGL(kv_write_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
+        if (kv_dtype == NYION_KV_F16)
+            hipLaunchKernelGGL(kv_write_flat_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL(kv_write_flat_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
     } else {
         const long long n = (long long)a.rows * a.n_kv_heads * ((a.head_dim + 31) / 32);
         hipLaunchKernelGGL(kv_write_q4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
@@ -396,7 +431,7 @@ int kv_write_impl(void* k_pool, void* v_pool, const int32_t* block_table, int bl
     if (!block_table || !k || !v) return set_error(NYION_ERR_INVALID, "kv write: null argument");
     if (start_pos < 0 || n_tokens <= 0)
         return set_error(NYION_ERR_INVALID, "kv write: start_pos %d, n_tokens %d", start_pos, n_tokens);
-    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 16) || !aligned(v, 16)))
+    if (kv_dtype != NYION_KV_Q4_20B && (!aligned(k, 16) || !aligned(v, 16)))
         return set_error(NYION_ERR_INVALID, "kv write: k/v must be 16-byte aligned");
     a.tables = block_table;
     a.positions = nullptr;
@@ -420,7 +455,7 @@ int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, i
     if (!block_table || !k || !v) return set_error(NYION_ERR_INVALID, "kv write: null argument");
     if (start_pos < 0 || n_tokens <= 0)
         return set_error(NYION_ERR_INVALID, "kv write: start_pos %d, n_tokens %d", start_pos, n_tokens);
-    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 8) || !aligned(v, 8)))
+    if (kv_dtype != NYION_KV_Q4_20B && (!aligned(k, 8) || !aligned(v, 8)))
         return set_error(NYION_ERR_INVALID, "kv write: bf16 k/v must be 8-byte aligned");
     a.tables = block_table;
     a.positions = nullptr;
@@ -462,7 +497,7 @@ int nyion_kv_append_batch(void* k_pool, void* v_pool, const int32_t* block_table
         return rc;
     if (!block_tables || !positions || !k || !v || batch <= 0 || max_blocks_per_seq <= 0)
         return set_error(NYION_ERR_INVALID, "kv append: null argument or non-positive size");
-    if (kv_dtype == NYION_KV_F32 && (!aligned(k, 16) || !aligned(v, 16)))
+    if (kv_dtype != NYION_KV_Q4_20B && (!aligned(k, 16) || !aligned(v, 16)))
         return set_error(NYION_ERR_INVALID, "kv append: k/v must be 16-byte aligned");
     a.tables = block_tables;
     a.positions = positions;
@@ -489,9 +524,11 @@ static int kv_gather_impl(const void* pool, const int32_t* block_table, int bloc
         return set_error(NYION_ERR_UNSUPPORTED, "kv gather: head_dim %d not a multiple of 8",
                          head_dim);
     if (!is_pow2(block_tokens)) return set_error(NYION_ERR_INVALID, "kv gather: block_tokens");
-    if (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B)
+    if (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B && kv_dtype != NYION_KV_F16)
         return set_error(NYION_ERR_INVALID, "kv gather: kv_dtype");
-    const long long row = kv_dtype == NYION_KV_F32 ? head_dim : q4_row_bytes(head_dim);
+    if (kv_dtype == NYION_KV_F16 && !aligned(pool, 16))
+        return set_error(NYION_ERR_INVALID, "kv gather: f16 pool must be 16-byte aligned");
+    const long long row = kv_dtype == NYION_KV_Q4_20B ? q4_row_bytes(head_dim) : head_dim;
     GatherArgs a{};
     a.pool = pool;
     a.table = block_table;
@@ -598,11 +635,14 @@ int nyion_rope_kv_append(float* d_q, const float* d_k, const float* d_v, const f
     a.w.rows = batch;
     a.w.per_seq = 1;
     const long long nq = (long long)batch * n_heads * (head_dim / 2);
-    const long long units = kv_dtype == NYION_KV_F32 ? head_dim / 2 : (head_dim + 31) / 32;
+    const long long units = kv_dtype == NYION_KV_Q4_20B ? (head_dim + 31) / 32 : head_dim / 2;
     const long long nkv = (long long)batch * n_kv_heads * units;
     const dim3 grid(grid_for(nq + nkv, 256));
     if (kv_dtype == NYION_KV_F32)
         hipLaunchKernelGGL(rope_kv_append_kernel<NYION_KV_F32>, grid, dim3(256), 0,
+                           (hipStream_t)stream, a, nq, nkv);
+    else if (kv_dtype == NYION_KV_F16)
+        hipLaunchKernelGGL(rope_kv_append_kernel<NYION_KV_F16>, grid, dim3(256), 0,
                            (hipStream_t)stream, a, nq, nkv);
     else
         hipLaunchKernelGGL(rope_kv_append_kernel<NYION_KV_Q4_20B>, grid, dim3(256), 0,

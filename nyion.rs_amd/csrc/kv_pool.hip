@@ -364,7 +364,7 @@ void* nyion_kv_pool_create(int n_layers, int n_kv_heads, int head_dim, int block
     if (require_device() != NYION_OK) return nullptr;
     if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || !is_pow2(block_tokens) ||
         hot_blocks <= 0 || cold_slots < 0 || max_pages <= 0 ||
-        (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B)) {
+        (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B && kv_dtype != NYION_KV_F16)) {
         set_error(NYION_ERR_INVALID, "kv pool: layers %d heads %d dim %d bt %d dtype %d hot %d cold %d "
                   "pages %d", n_layers, n_kv_heads, head_dim, block_tokens, kv_dtype, hot_blocks,
                   cold_slots, max_pages);
@@ -376,7 +376,9 @@ void* nyion_kv_pool_create(int n_layers, int n_kv_heads, int head_dim, int block
     p->head_dim = head_dim;
     p->block_tokens = block_tokens;
     p->kv_dtype = kv_dtype;
-    p->row_bytes = kv_dtype == NYION_KV_F32 ? 4LL * head_dim : q4_row_bytes(head_dim);
+    p->row_bytes = kv_dtype == NYION_KV_F32   ? 4LL * head_dim
+                   : kv_dtype == NYION_KV_F16 ? 2LL * head_dim
+                                              : q4_row_bytes(head_dim);
     p->block_bytes = p->row_bytes * block_tokens * n_kv_heads;
     if (p->block_bytes % 16) {
         set_error(NYION_ERR_UNSUPPORTED, "kv pool: block of %lld bytes (not a multiple of 16)",

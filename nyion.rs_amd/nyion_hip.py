@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libnyion_hip.so")
 
 KV_F32 = 0
 KV_Q4_20B = 1
+KV_F16 = 2
 
 MEM_HOST_PINNED = 0
 MEM_DEVICE_LOCAL = 1
@@ -128,6 +129,8 @@ SIGNATURES = {
     "gpu_graph_create_attention": (vp, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
     "gpu_graph_replay_attention": (i32, [vp, vp]),
     "gpu_graph_destroy": (None, [vp]),
+    "gpu_attention_streamed_half": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+    "gpu_graph_create_attention_half": (vp, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
     "nyion_rope_lut_init": (i32, [vp, i32, i32, vp]),
     "nyion_rope_kv_append": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, i32,
                                    i32, i32, i32, vp]),

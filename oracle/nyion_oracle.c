@@ -323,12 +323,18 @@ static inline int64_t row_index(const orc_kv_layout* kv, int64_t t, int64_t h) {
     return blk * kv->block_stride + h * kv->head_stride + (t % kv->block_tokens) * kv->token_stride;
 }
 
-/* Returns a pointer to the f32 row; Q4 rows are dequantised into tmp first,
+/* Returns a pointer to the f32 row; binary16 rows are widened into tmp, Q4
+ * rows dequantised into tmp first,
  * as the reference reads Q4 pages through their f32 view (cache.rs:338-405). */
 static inline const float* fetch_row(const orc_kv_layout* kv, const void* base, int64_t t,
                                      int64_t h, int head_dim, float* tmp) {
     int64_t idx = row_index(kv, t, h);
     if (kv->dtype == ORC_KV_F32) return (const float*)base + idx;
+    if (kv->dtype == ORC_KV_F16) {
+        const uint16_t* r = (const uint16_t*)base + idx;
+        for (int d = 0; d < head_dim; d++) tmp[d] = orc_f16_to_f32(r[d]);
+        return tmp;
+    }
     orc_q4_dequant_row((const uint8_t*)base + idx, head_dim, tmp);
     return tmp;
 }

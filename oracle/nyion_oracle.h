@@ -60,13 +60,14 @@
 extern "C" {
 #endif
 
-enum { ORC_KV_F32 = 0, ORC_KV_Q4 = 1 };
+enum { ORC_KV_F32 = 0, ORC_KV_Q4 = 1, ORC_KV_F16 = 2 };
 
 /* Row addressing shared by every attention restatement.
  * Row of token t, kv head h:
  *   base + table[t / block_tokens] * block_stride + h * head_stride
  *        + (t % block_tokens) * token_stride
- * Strides are in f32 elements for ORC_KV_F32 and in bytes for ORC_KV_Q4.
+ * Strides are in f32 elements for ORC_KV_F32, binary16 elements for
+ * ORC_KV_F16 (rows widened exactly to f32 before use) and bytes for ORC_KV_Q4.
  * table == NULL means block id 0 for every token (contiguous layouts use a
  * block_tokens larger than any position). */
 typedef struct orc_kv_layout {

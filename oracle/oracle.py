@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(HERE, "libnyion_oracle.so")
 
 KV_F32 = 0
 KV_Q4 = 1
+KV_F16 = 2
 CONTIGUOUS = 1 << 40  # block_tokens larger than any position
 
 
@@ -133,8 +134,8 @@ def _ptr(a: np.ndarray | None):
 
 def paged_layout(k_pool: np.ndarray, v_pool: np.ndarray, table: np.ndarray | None,
                  block_tokens: int, n_kv_heads: int, head_dim: int, dtype: int = KV_F32):
-    """Pool [num_blocks][Hkv][block_tokens][row] with row = D f32 or Q4 bytes."""
-    row = head_dim if dtype == KV_F32 else q4_row_bytes(head_dim)
+    """Pool [num_blocks][Hkv][block_tokens][row] with row = D f32, D binary16 or Q4 bytes."""
+    row = q4_row_bytes(head_dim) if dtype == KV_Q4 else head_dim
     lay = KVLayout(k_pool.ctypes.data, v_pool.ctypes.data,
                    None if table is None else table.ctypes.data, block_tokens,
                    n_kv_heads * block_tokens * row, block_tokens * row, row, dtype, 0)
@@ -145,7 +146,7 @@ def paged_layout(k_pool: np.ndarray, v_pool: np.ndarray, table: np.ndarray | Non
 def contiguous_layout(k: np.ndarray, v: np.ndarray, kv_stride: int, head_dim: int,
                       dtype: int = KV_F32):
     """[Hkv][kv_stride][row] (the Attention node / gpu_attention_device layout)."""
-    row = head_dim if dtype == KV_F32 else q4_row_bytes(head_dim)
+    row = q4_row_bytes(head_dim) if dtype == KV_Q4 else head_dim
     lay = KVLayout(k.ctypes.data, v.ctypes.data, None, CONTIGUOUS, 0, kv_stride * row, row,
                    dtype, 0)
     lay._keep = (k, v)

@@ -52,10 +52,12 @@ def gather(gpu, pool, layer, n_tokens, which):
 def expected_rows(x, kv_dtype):
     if kv_dtype == oracle.KV_F32:
         return x
+    if kv_dtype == oracle.KV_F16:  # written round-to-nearest-even, widened exactly
+        return x.astype(np.float16).astype(np.float32)
     return oracle.q4_dequant_rows(oracle.q4_quantize_rows(x), D)
 
 
-@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4, oracle.KV_F16])
 def test_spill_and_reload_round_trip(gpu, kv_dtype):
     n_pages, hot = 13, 4
     pool = gpu.KvPool(L, HKV, D, BT, kv_dtype, hot, 16, 32)

@@ -346,6 +346,25 @@ def test_attention_q4_equals_attention_on_dequantised_pool():
         assert np.array_equal(o4, of)
 
 
+def test_attention_f16_equals_attention_on_widened_pool():
+    """binary16 rows are widened exactly before use: the oracle on an f16 pool
+    equals the oracle on the f32 pool holding the same values, bit for bit."""
+    pb = W.paged_batch([300, 17], seed=4, kv_dtype=oracle.KV_F16)
+    kf = pb.k_pool.view(np.float16).astype(np.float32)
+    vf = pb.v_pool.view(np.float16).astype(np.float32)
+    for b in range(2):
+        lay_f = oracle.paged_layout(kf, vf, pb.tables[b], 16, 4, 64)
+        L = int(pb.ctx_lens[b])
+        a = oracle.attention(pb.q[b], pb.layout(b), L, L - 1, 32, 4, 64)
+        r = oracle.attention(pb.q[b], lay_f, L, L - 1, 32, 4, 64)
+        assert np.array_equal(a, r)
+    # and the f16 pool holds numpy's round-to-nearest-even of the f32 draw
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(1000, dtype=np.float32)
+    assert np.array_equal(np.array([oracle.f32_to_f16_bits(float(v)) for v in x], np.uint16),
+                          x.astype(np.float16).view(np.uint16))
+
+
 def test_attention_positions_matches_float64():
     pb = W.paged_batch([5000], seed=11)
     pos = oracle.sparse_positions(5000, 4999, 256, 64)

@@ -28,7 +28,7 @@ import oracle  # noqa: E402  (the checker)
 @dataclasses.dataclass
 class PagedBatch:
     q: np.ndarray            # [B][Hq][D] f32
-    k_pool: np.ndarray       # [NB][Hkv][bt][row] f32 or u8
+    k_pool: np.ndarray       # [NB][Hkv][bt][row] f32, u16 (binary16 bits) or u8 (Q4)
     v_pool: np.ndarray
     tables: np.ndarray       # [B][max_blocks] int32
     ctx_lens: np.ndarray     # [B] int32
@@ -49,8 +49,8 @@ class PagedBatch:
 
     def kv_bytes(self, attended=None) -> int:
         """Algorithmic K+V bytes read: every attended (token, kv head) row once."""
-        row = self.head_dim * 4 if self.kv_dtype == oracle.KV_F32 else oracle.q4_row_bytes(
-            self.head_dim)
+        row = {oracle.KV_F32: self.head_dim * 4, oracle.KV_F16: self.head_dim * 2}.get(
+            self.kv_dtype, oracle.q4_row_bytes(self.head_dim))
         toks = int(self.ctx_lens.sum()) if attended is None else int(attended)
         return 2 * toks * self.n_kv_heads * row
 
@@ -80,6 +80,9 @@ def paged_batch(ctx_lens, n_heads=32, n_kv_heads=4, head_dim=64, block_tokens=16
     if kv_dtype == oracle.KV_Q4:
         k = oracle.q4_quantize_rows(k)
         v = oracle.q4_quantize_rows(v)
+    elif kv_dtype == oracle.KV_F16:  # binary16 rows (bits), round to nearest even
+        k = k.astype(np.float16).view(np.uint16)
+        v = v.astype(np.float16).view(np.uint16)
     return PagedBatch(q, k, v, tables, ctx, n_heads, n_kv_heads, head_dim, block_tokens, kv_dtype,
                       seed)
 
