@@ -13,7 +13,8 @@ metric/unit: achieved algorithmic HBM bandwidth of the decode step in GB/s
 (K + V + q + out + block table bytes, counted once), with us/layer beside it.
 The other workloads are measured in the same run and reported under
 "configs", keyed by their --only selector: c1 (contiguous 128-position
-node), c3 (64-sequence continuous batch), c4 (4-bit KV, 131072 context,
+node), c3 (64-sequence continuous batch; c3h the same on binary16 KV),
+c4 (4-bit KV, 131072 context,
 window 4096), c5 (causal prefill of 8192 tokens, TFLOP/s against the bf16
 MFMA peak), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV
 pool with host spill).
@@ -52,7 +53,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c4,c5,gemv,gemv6,pool (default all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c3h,c4,c5,gemv,gemv6,pool (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true",
                     help="GEMV section: issue the launches directly instead of replaying graphs")
@@ -366,7 +367,9 @@ def bench_c1(nh, torch, steps, warmup):
     return {"us_per_layer": ms * 1e3, "call_us_event_mean": us, "bytes_per_layer": 278528}
 
 
-def bench_c3(nh, torch, steps, warmup, seed=0):
+def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
+    """64-sequence continuous batch; f16=True stores the same K/V draw as
+    binary16 rows (half the bytes)."""
     import workloads as W
 
     Hq, Hkv, D, bt = 32, 4, 64, 16
@@ -383,18 +386,22 @@ def bench_c3(nh, torch, steps, warmup, seed=0):
     g = torch.Generator(device="cuda").manual_seed(seed)
     kp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
     vp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
+    if f16:
+        kp, vp = kp.half(), vp.half()
     q = torch.randn((64, Hq, D), generator=g, device="cuda")
     tab = torch.from_numpy(tables).cuda()
     ctx = torch.from_numpy(lens).cuda()
     out = torch.empty_like(q)
     maxc = int(lens.max())
     ws = nh.alloc_workspace(nh.decode_workspace_size(64, Hq, Hkv, D, maxc))
+    kvt = nh.KV_F16 if f16 else nh.KV_F32
 
     def call(i):
-        nh.paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, max_ctx=maxc, workspace=ws)
+        nh.paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, kv_dtype=kvt, max_ctx=maxc,
+                        workspace=ws)
 
     toks = int(lens.sum())
-    nbytes = 2 * toks * Hkv * D * 4 + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
+    nbytes = 2 * toks * Hkv * D * (2 if f16 else 4) + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
     ms = timed(call, steps, warmup, torch)
     us = event_mean(call, steps, torch) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -402,7 +409,7 @@ def bench_c3(nh, torch, steps, warmup, seed=0):
             "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": pmc_traffic("c3")},
+                         "traffic": None if f16 else pmc_traffic("c3")},
             "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
 
 
@@ -709,7 +716,7 @@ def main():
     nh.init(0)
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4", "c5", "gemv", "gemv6", "pool"}
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -729,6 +736,10 @@ def main():
     if "c3" in only:
         log("64-sequence continuous batch")
         res["c3"] = bench_c3(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
+    if "c3h" in only:
+        log("64-sequence continuous batch, binary16 KV")
+        res["c3h"] = bench_c3(nh, torch, steps, warmup, f16=True)
         torch.cuda.empty_cache()
     if "c4" in only:
         log("Q4 KV, ctx 131072, window 4096")
