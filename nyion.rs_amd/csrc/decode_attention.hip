@@ -53,6 +53,10 @@ namespace nyion {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+// 16 bytes at 8-byte alignment (binary16 rows): one dwordx4 load
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(8)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 enum DecodeMode { MODE_FULL = 0, MODE_WINDOW = 1, MODE_LIST = 2 };
 
@@ -163,12 +167,17 @@ __device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e,
 // K operand of lane (row i, quad kq): NC = D/4 values, one per QK MFMA.
 //   f32: call c = 4x+y holds dim 16x + 4kq + y  (per x, the 4 quads of a row
 //        read 64 contiguous bytes)
+//   f16: value c = 8x+4e+y (binary16 MFMA 2x+e, element y) holds dim
+//        32x + 8kq + 4e + y  (per x, the 4 quads of a row read 64 contiguous
+//        bytes)
 //   Q4 : call c holds dim kq*D/4 + c            (contiguous nibbles)
 // The Q operand uses the same map (qk_dim).  V operand of lane (col j, quad
 // kq), row 4kq+r: DPL = D/16 consecutive dims from DPL*j.
 template <int D, int KVT>
 __device__ __forceinline__ int qk_dim(int c, int kq) {
-    if constexpr (KVT != NYION_KV_Q4_20B)
+    if constexpr (KVT == NYION_KV_F16)
+        return 32 * (c >> 3) + 8 * kq + 4 * ((c >> 2) & 1) + (c & 3);
+    else if constexpr (KVT == NYION_KV_F32)
         return 16 * (c >> 2) + 4 * kq + (c & 3);
     else
         return kq * (D / 4) + c;
@@ -186,8 +195,8 @@ struct Tile<D, NYION_KV_F32> {
 
 template <int D>
 struct Tile<D, NYION_KV_F16> {
-    u32x2 k[D / 16];          // K row j: dims 16x + 4kq .. +3, four binary16 values
-    u32x2 v[4][D / 64];       // V rows 4kq+r: dims DPL*j + 4x .. +3
+    u32x4a k[D / 32];         // K row j: dims 32x + 8kq .. +7, eight binary16 values
+    uint32_t v[4][D / 32];    // V rows 4kq+r: dims DPL*j .. +DPL-1, two per word
 };
 
 template <int D>
@@ -207,14 +216,20 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
     if constexpr (KVT == NYION_KV_F16) {
         const uint16_t* kr = (const uint16_t*)kb + koff;
 #pragma unroll
-        for (int x = 0; x < D / 16; x++)
-            t.k[x] = __builtin_nontemporal_load((const u32x2*)(kr + 16 * x + 4 * kq));
+        for (int x = 0; x < D / 32; x++)
+            t.k[x] = __builtin_nontemporal_load((const u32x4a*)(kr + 32 * x + 8 * kq));
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint16_t* vr = (const uint16_t*)vb + voff[r] + (D / 16) * j;
+            if constexpr (D == 64) {
+                const u32x2 w = __builtin_nontemporal_load((const u32x2*)vr);
+                t.v[r][0] = w[0];
+                t.v[r][1] = w[1];
+            } else {
+                const u32x4a w = __builtin_nontemporal_load((const u32x4a*)vr);
 #pragma unroll
-            for (int x = 0; x < D / 64; x++)
-                t.v[r][x] = __builtin_nontemporal_load((const u32x2*)(vr + 4 * x));
+                for (int i = 0; i < 4; i++) t.v[r][i] = w[i];
+            }
         }
     } else if constexpr (KVT == NYION_KV_F32) {
         const float* kr = (const float*)kb + koff;
@@ -249,24 +264,9 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
     }
 }
 
-// Four binary16 values (two words) -> f32, exact.  The words are copied to
-// scalars first: this compiler's __builtin_bit_cast of a vector element
-// (w[1]) yields the bits of element 0.
-__device__ __forceinline__ void f16x4_to_f32(u32x2 w, float* out) {
-    const uint32_t w0 = w[0], w1 = w[1];
-    const halfx2 lo = __builtin_bit_cast(halfx2, w0), hi = __builtin_bit_cast(halfx2, w1);
-    out[0] = (float)lo[0];
-    out[1] = (float)lo[1];
-    out[2] = (float)hi[0];
-    out[3] = (float)hi[1];
-}
-
 template <int D, int KVT>
 __device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
-    if constexpr (KVT == NYION_KV_F16) {
-#pragma unroll
-        for (int x = 0; x < D / 16; x++) f16x4_to_f32(t.k[x], kv + 4 * x);
-    } else if constexpr (KVT == NYION_KV_F32) {
+    if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
         for (int x = 0; x < D / 16; x++) {
             kv[4 * x + 0] = t.k[x].x;
@@ -283,10 +283,7 @@ __device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
 
 template <int D, int KVT>
 __device__ __forceinline__ void decode_v(const Tile<D, KVT>& t, int r, float* vv) {
-    if constexpr (KVT == NYION_KV_F16) {
-#pragma unroll
-        for (int x = 0; x < D / 64; x++) f16x4_to_f32(t.v[r][x], vv + 4 * x);
-    } else if constexpr (KVT == NYION_KV_F32) {
+    if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
         for (int x = 0; x < D / 64; x++) {
             vv[4 * x + 0] = t.v[r][x].x;
@@ -326,11 +323,30 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
                                              const int* pos) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
-    float kv[NC];
-    decode_k<D, KVT>(t, kv);
     floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KVT == NYION_KV_F16) {
+        // binary16 K as stored against q split into binary16 high and low
+        // parts (qv words 4x, 4x+1 and 4x+2, 4x+3): the products are exact in
+        // f32, so S keeps f32 accuracy at a quarter of the f32 MFMA cycles.
+        // Call x takes words 2(x&1), +1 of K load x/2 (dims 32(x/2) + 8kq +
+        // 4(x&1) .. +3).  The words are copied to scalars first: this
+        // compiler's __builtin_bit_cast of a vector element yields the bits
+        // of element 0.
 #pragma unroll
-    for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
+        for (int x = 0; x < D / 16; x++) {
+            const uint32_t k0 = t.k[x >> 1][2 * (x & 1)], k1 = t.k[x >> 1][2 * (x & 1) + 1];
+            const halfx4 kx = __builtin_bit_cast(halfx4, u32x2{k0, k1});
+            const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
+            const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, s, 0, 0, 0);
+        }
+    } else {
+        float kv[NC];
+        decode_k<D, KVT>(t, kv);
+#pragma unroll
+        for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
+    }
 
     float sv[4];
 #pragma unroll
@@ -362,18 +378,44 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
 #pragma unroll
     for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - st.m);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (KVT == NYION_KV_F16) {
+        // O += P.V on binary16 MFMAs: A = this lane's four p (tokens 4kq..+3
+        // of head j), rounded to binary16 (relative error <= 2^-12, p <= 2^8);
+        // B of output dim DPL*j + z = the four rows' value of that dim, one
+        // 16-bit half of each row's word (z/2)
+        const halfx4 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
+        uint32_t vw[4][DPL / 2];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float vv[DPL];
-        decode_v<D, KVT>(t, r, vv);
-        if (MASKED) {  // masked rows may hold uninitialised slots: keep NaN out
-            const bool ok = (mask >> (4 * kq + r)) & 1u;
+        for (int r = 0; r < 4; r++) {
+            const bool ok = !MASKED || ((mask >> (4 * kq + r)) & 1u);
 #pragma unroll
-            for (int x = 0; x < DPL; x++) vv[x] = ok ? vv[x] : 0.f;
+            for (int w = 0; w < DPL / 2; w++)
+                vw[r][w] = ok ? t.v[r][w] : 0u;  // masked rows may hold uninitialised slots
         }
 #pragma unroll
-        for (int x = 0; x < DPL; x++)
-            st.acc[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv[x], st.acc[x], 0, 0, 0);
+        for (int z = 0; z < DPL; z++) {
+            const int w = z >> 1;
+            const uint32_t b01 = (z & 1) ? (vw[0][w] >> 16) | (vw[1][w] & 0xffff0000u)
+                                         : (vw[0][w] & 0xffffu) | (vw[1][w] << 16);
+            const uint32_t b23 = (z & 1) ? (vw[2][w] >> 16) | (vw[3][w] & 0xffff0000u)
+                                         : (vw[2][w] & 0xffffu) | (vw[3][w] << 16);
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                pa, __builtin_bit_cast(halfx4, u32x2{b01, b23}), st.acc[z], 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float vv[DPL];
+            decode_v<D, KVT>(t, r, vv);
+            if (MASKED) {  // masked rows may hold uninitialised slots: keep NaN out
+                const bool ok = (mask >> (4 * kq + r)) & 1u;
+#pragma unroll
+                for (int x = 0; x < DPL; x++) vv[x] = ok ? vv[x] : 0.f;
+            }
+#pragma unroll
+            for (int x = 0; x < DPL; x++)
+                st.acc[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv[x], st.acc[x], 0, 0, 0);
+        }
     }
 }
 
@@ -715,6 +757,22 @@ void decode_kernel(DecodeArgs a) {
             const bool ok = j < g_local;
 #pragma unroll
             for (int cc = 0; cc < NC; cc++) qv[cc] = ok ? qrow[qk_dim<D, KVT>(cc, kq)] : 0.f;
+            if constexpr (KVT == NYION_KV_F16) {
+                // words 4x, 4x+1: the four values as binary16; 4x+2, 4x+3: the
+                // binary16 residuals (q within the binary16 range)
+#pragma unroll
+                for (int x = 0; x < D / 16; x++) {
+                    const float* v = qv + 4 * x;
+                    const halfx4 hi = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                    const halfx4 lo = {(_Float16)(v[0] - (float)hi[0]), (_Float16)(v[1] - (float)hi[1]),
+                                       (_Float16)(v[2] - (float)hi[2]), (_Float16)(v[3] - (float)hi[3])};
+                    const floatx2 hw = __builtin_bit_cast(floatx2, hi), lw = __builtin_bit_cast(floatx2, lo);
+                    qv[4 * x] = hw[0];
+                    qv[4 * x + 1] = hw[1];
+                    qv[4 * x + 2] = lw[0];
+                    qv[4 * x + 3] = lw[1];
+                }
+            }
         }
 
         State<D> st;
