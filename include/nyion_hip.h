@@ -22,6 +22,10 @@
  *   reference's Q4-20B groups (NYION_KV_Q4_20B: f16 d, f16 dmin, 16 nibble
  *   bytes; element i of a group in byte 4+i/2, low nibble when i is even;
  *   swamp-engine/src/cache.rs:637-663, 375-394).
+ *   Attention over binary16 rows multiplies them on binary16 matrix cores:
+ *   q is split into binary16 high and low parts (so |q| must stay below
+ *   65504) and the softmax weights are rounded to binary16 (relative error
+ *   <= 2^-12 per weight) before the product with V.
  *   Token t of sequence b lives in block block_tables[b*max_blocks_per_seq +
  *   t/block_tokens], slot t%block_tokens.  block_tokens is a power of two.
  */
@@ -114,7 +118,9 @@ void gpu_graph_destroy(void* graph_handle);
 /* The same two on binary16 K/V caches (NYION_KV_F16 rows, [n_kv_heads]
  * [kv_stride][head_dim], 8-byte aligned): gpu_attention_streamed_half
  * (fused_attention.cu:534-545) and gpu_graph_create_attention_half
- * (fused_attention.cu:672-717).  K/V values are widened to f32 exactly. */
+ * (fused_attention.cu:672-717).  K/V values are used as stored (binary16
+ * products, f32 accumulation; q and the softmax weights as in the pool
+ * layout note above). */
 int gpu_attention_streamed_half(const float* d_q, const uint16_t* d_k_cache,
                                 const uint16_t* d_v_cache, float* d_output, int n_heads,
                                 int n_kv_heads, int seq_len, int head_dim, int kv_stride,

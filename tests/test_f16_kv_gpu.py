@@ -5,8 +5,11 @@ against the oracle on the same binary16 rows; the KV writer's rounding, the
 gathers' widening and the RoPE epilogue bit-exactly.
 
 Attention tolerance: max-abs-err <= 2e-3 and rel-err (max|diff| / max|ref|)
-<= 1e-3, the same as for f32 caches (the rows are widened exactly; only the
-summation order differs from the oracle)."""
+<= 1e-3, the same as for f32 caches.  The kernel multiplies the binary16
+rows as stored, with q split into binary16 high and low parts (scores at f32
+accuracy) and the softmax weights rounded to binary16 (relative error <=
+2^-12 each), so besides the summation order only that rounding separates it
+from the oracle."""
 import numpy as np
 import pytest
 import torch
