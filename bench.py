@@ -409,7 +409,7 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
             "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": None if f16 else pmc_traffic("c3")},
+                         "traffic": pmc_traffic("c3h" if f16 else "c3")},
             "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
 
 
