@@ -60,6 +60,54 @@ def test_paged_decode_f16(gpu, ctx, hq, hkv, hd, bt):
     assert_close(run_paged(gpu, pb), W.reference_decode(pb, threads=8), f"f16 decode {ctx}")
 
 
+@pytest.mark.parametrize("bt", [4, 8])
+def test_paged_decode_f16_small_pages(gpu, bt):
+    """Pages under 16 tokens take the per-row gather path."""
+    pb = W.paged_batch([1, 17, 300, 777], block_tokens=bt, seed=bt, kv_dtype=oracle.KV_F16)
+    assert_close(run_paged(gpu, pb), W.reference_decode(pb), f"f16 block_tokens {bt}")
+
+
+def test_tracked_f16(gpu):
+    """ops::attention_tracked on binary16 rows: outputs and importance[t] =
+    sum_h p_h[t] against the oracle on the same rows."""
+    pb = W.paged_batch([300, 4096, 2000], seed=21, kv_dtype=oracle.KV_F16)
+    q_pos = [250, 4095, 1500]
+    q, kp, vp = to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    out = torch.full_like(q, float("nan"))
+    imp = torch.zeros((pb.batch, 4096 + 2), dtype=torch.float64, device="cuda")
+    gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out, imp, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                             pb.block_tokens, kv_dtype=F16,
+                             q_pos=to_dev(np.asarray(q_pos, np.int32)))
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), W.reference_decode(pb, q_pos=q_pos), "f16 tracked out")
+    got = imp.cpu().numpy()
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, q_pos[b], pb.n_heads,
+                                      pb.n_kv_heads, pb.head_dim, importance=True)
+        assert np.max(np.abs(got[b, :L] - ref_imp)) <= 1e-4 * pb.n_heads, f"f16 importance b={b}"
+        assert np.all(got[b, q_pos[b] + 1:] == 0.0), f"f16 importance past valid_end b={b}"
+
+
+def test_positions_f16(gpu):
+    """Explicit position lists (the Fugu set) over binary16 rows."""
+    pb = W.paged_batch([6000, 2500], seed=23, kv_dtype=oracle.KV_F16)
+    sets = [oracle.fugu_positions(6000, 5999, 256, 64, [5, 77, 5990, 3000, 4]),
+            oracle.fugu_positions(2500, 2499, 1024, 0, [17, 18, 2499])]
+    pos = np.zeros((2, max(len(x) for x in sets)), np.int32)
+    npos = np.array([len(x) for x in sets], np.int32)
+    for b, x in enumerate(sets):
+        pos[b, :len(x)] = x
+    out = torch.full((2, 32, 64), float("nan"), device="cuda")
+    gpu.paged_decode_positions(to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool), to_dev(pb.tables),
+                               to_dev(pos), to_dev(npos), out, 32, 4, 64, 16, kv_dtype=F16)
+    torch.cuda.synchronize()
+    ref = np.stack([oracle.attention_positions(pb.q[b], pb.layout(b), sets[b], 32, 4, 64).reshape(
+        32, 64) for b in range(2)])
+    assert_close(out.cpu().numpy(), ref, "f16 positions")
+
+
 @pytest.mark.parametrize("stride", [0, 64])
 def test_window_decode_f16(gpu, stride):
     pb = W.paged_batch([9000, 4200], seed=7, kv_dtype=oracle.KV_F16)
