@@ -1,5 +1,6 @@
-"""Binary16 KV caches on the GPU (gpu): paged decode, window decode, the
-attention node and the project ABI's f16 names (gpu_attention_streamed_half,
+"""Binary16 KV caches on the GPU (gpu): paged decode (block walk and, for
+pages under 16 tokens, per-row gather), tracked decode with importance,
+position lists, window decode, the attention node and the project ABI's f16 names (gpu_attention_streamed_half,
 gpu_graph_create_attention_half, fused_attention.cu:534-545, 672-717)
 against the oracle on the same binary16 rows; the KV writer's rounding, the
 gathers' widening and the RoPE epilogue bit-exactly.
