@@ -375,6 +375,10 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
                 pa[t2][e + 1] = pp[1];
             }
         lrun += psum;
+        // P and the row sum are needed only after the rescale branch, and
+        // the compiler would otherwise place the exps behind it, where no S
+        // MFMA is left to hide them; this empty use keeps them ahead of it
+        asm volatile("" : : "v"(pa[0]), "v"(pa[1]), "v"(lrun));
         // B operands of the PV product: V^T row 32dt + j, the 8 keys of
         // k-step t = 2kb + t2
         const unsigned char* vp = vs + j * L::VROW + 16 * h + 64 * kb;
