@@ -20,7 +20,11 @@
 //   O[16 heads][D]     += P[16 heads][16 tok] . V_tile      (D/4 MFMAs)
 // The MFMA output layout of S (lane = head + 16*token_quad, reg = token in
 // quad) is exactly the A-operand layout P needs in the second product, so the
-// probabilities never leave registers.
+// probabilities never leave registers.  Binary16 rows use
+// v_mfma_f32_16x16x16_f16 for both products instead: K as stored against q
+// split into binary16 high and low parts, P rounded to binary16 against V as
+// stored (a quarter of the f32 MFMA cycles; half the bytes per tile would
+// otherwise leave the chain, not HBM, as the limit).
 //
 // Memory.  Tiles are aligned to 16 positions, so with blocks of >= 16 tokens
 // a tile lies in one block: its block id is one wave-uniform value, read from
