@@ -116,6 +116,10 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
 struct Q4kFormat {
     static constexpr int kBlockBytes = 144;
     static constexpr int kRunGap = 32;  // x distance from the low run to the high run
+    // one buffer copied forward per step: alternating the two takes more
+    // registers and costs the four-row kernel a wavefront per SIMD
+    // (8B-shaped gate/up 22.5 -> 25.5 us)
+    static constexpr bool kAlternateBuffers = false;
     static constexpr const char* kName = "gemv q4k";
     // the block's 16-byte header and the chunk's 16 nibble bytes
     struct Raw {
@@ -167,6 +171,10 @@ __device__ __forceinline__ float q6k_scale_to_f32(uint32_t v) {
 struct Q6kFormat {
     static constexpr int kBlockBytes = 210;
     static constexpr int kRunGap = 64;
+    // the two buffers alternate by step parity, saving the copy of the raw
+    // words between steps at the same occupancy (output projection 19.5 ->
+    // 18.9 us)
+    static constexpr bool kAlternateBuffers = true;
     static constexpr const char* kName = "gemv q6k";
     // dword-aligned words covering the chunk's 16 ql bytes and 16 qh bytes
     // (four plus one each), its two scales and the word holding d, and the
@@ -293,15 +301,15 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
     const int units_here = (int)blockIdx.x < U ? (U - (int)blockIdx.x + G - 1) / G : 0;
     const int T = units_here * npass;
     if (npass == 1) load_x(lane + 64 * kp);  // the same chunk positions for every row
-    GemvStep<F, R> cur, nxt;
-    if (T > 0) load_w(0, cur);
+    GemvStep<F, R> buf[2];  // current and next step's raw weights
+    if (T > 0) load_w(0, buf[0]);
     float acc[R][B];
 #pragma unroll
     for (int i = 0; i < R; i++)
 #pragma unroll
         for (int b = 0; b < B; b++) acc[i][b] = 0.f;
 
-    for (int t = 0; t < T; t++) {
+    auto step = [&](int t, const GemvStep<F, R>& cur, GemvStep<F, R>& nxt) __attribute__((always_inline)) {
         if (t + 1 < T) load_w(t + 1, nxt);  // next step's weights in flight
         const int pass = t % npass;
         const int c = lane + 64 * (kp + P * pass);
@@ -372,7 +380,17 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
 #pragma unroll
                 for (int b = 0; b < B; b++) acc[i][b] = 0.f;
         }
-        cur = nxt;
+    };
+    if constexpr (F::kAlternateBuffers) {
+        for (int t = 0; t < T; t += 2) {
+            step(t, buf[0], buf[1]);
+            if (t + 1 < T) step(t + 1, buf[1], buf[0]);
+        }
+    } else {
+        for (int t = 0; t < T; t++) {
+            step(t, buf[0], buf[1]);
+            buf[0] = buf[1];
+        }
     }
 }
 
