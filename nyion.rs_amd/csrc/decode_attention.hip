@@ -494,6 +494,65 @@ __device__ __forceinline__ uint32_t gather_offsets(const DecodeArgs& a, const Ex
     return mask;
 }
 
+// Block ids of the strided globals one wavefront gathers (virtual indices
+// v0 .. v0 + 127; a sequence has at most 128), loaded in one batch so that
+// each gathered tile costs one round trip instead of a table load followed
+// by its row loads: lane l holds those of v0 + l and v0 + 64 + l, -1 past the
+// list, past the table or outside [0, num_blocks) (row_offset's rules).
+struct GlobalBlocks {
+    int b[2];
+};
+
+__device__ __forceinline__ GlobalBlocks load_global_blocks(const DecodeArgs& a, const Extent& e,
+                                                           const RowMap& m, int v0, int lane) {
+    GlobalBlocks g;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int v = v0 + 64 * k + lane;
+        int blk = -1;
+        if (v < e.n_glob) {
+            const int t = v * a.global_stride;
+            if (!m.table) {
+                blk = 0;
+            } else if ((t >> m.bt_log2) < m.table_len) {
+                blk = m.table[t >> m.bt_log2];
+                if ((unsigned)blk >= (unsigned)m.num_blocks) blk = -1;
+            }
+        }
+        g.b[k] = blk;
+    }
+    return g;
+}
+
+// Offsets of gathered global tile i (virtual indices v0 + 16i .. +15, i < 8)
+// from the preloaded block ids: the same rows, positions and mask as
+// gather_offsets with globals = true.  Invalid rows point at offset 0 and are
+// masked.
+__device__ __forceinline__ uint32_t global_offsets(const DecodeArgs& a, const Extent& e,
+                                                   const RowMap& m, const GlobalBlocks& g, int kvh,
+                                                   int v0, int i, int j, int kq, long long& koff,
+                                                   long long* voff, int* pos) {
+    const int src = i < 4 ? g.b[0] : g.b[1];  // i is wave-uniform
+    auto row = [&](int rel, int& p) -> long long {
+        const int blk = __shfl(src, rel & 63);  // every lane takes part
+        const int v = v0 + rel;
+        p = v < e.n_glob ? v * a.global_stride : -1;
+        if (p < 0 || blk < 0) return -1;
+        return (long long)blk * m.block_stride + (long long)kvh * m.head_stride +
+               (long long)(p & ((1 << m.bt_log2) - 1)) * m.token_stride;
+    };
+    int pk;
+    koff = row(16 * i + j, pk);
+    const uint32_t mask = (uint32_t)(__ballot(koff >= 0) & 0xffffu);
+    koff = koff < 0 ? 0 : koff;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const long long o = row(16 * i + 4 * kq + r, pos[r]);
+        voff[r] = o < 0 ? 0 : o;
+    }
+    return mask;
+}
+
 // Walk `n` tiles with the next tile's loads in flight during each MFMA chain.
 // Every step issues exactly one tile of loads (at the end, a repeat of the
 // last tile that is never consumed), so the number of loads in flight is the
@@ -664,12 +723,18 @@ __device__ __forceinline__ int sload(const int* p) { return __builtin_amdgcn_rea
 
 // Occupancy target, which bounds the registers the compiler may use: two
 // workgroups (8 wavefronts) per CU, except f32 KV at head_dim 128, whose two
-// register-resident 16-token tiles alone take 128 VGPRs per lane (one).  Two
-// tiles of loads in flight per wavefront at this occupancy keep ~32 MB of
-// reads outstanding, more than HBM latency x bandwidth.
+// register-resident 16-token tiles alone take 128 VGPRs per lane (one), and
+// the smaller binary16 and 4-bit tiles at head_dim 64 (three).  Two tiles of
+// loads in flight per wavefront at this occupancy keep ~32 MB of f32 reads
+// outstanding, more than HBM latency x bandwidth.
+template <int D, int KVT>
+constexpr int decode_waves_per_eu() {
+    return (D == 128 && KVT == NYION_KV_F32) ? 1 : (D == 64 && KVT != NYION_KV_F32) ? 3 : 2;
+}
+
 template <int D, int KVT, bool ALIGNED, bool TRACK>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu((D == 128 && KVT == NYION_KV_F32) ? 1 : 2)))
+__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, KVT>())))
 void decode_kernel(DecodeArgs a) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
@@ -811,12 +876,15 @@ void decode_kernel(DecodeArgs a) {
                                          me - wa, lane, j, kq, srow);
             const int ga = max(wa, mt) - mt;
             const int gb = wb - mt;
-            walk_tiles<D, KVT, TRACK>(st, a, qv, gb - ga, j, kq, srow,
-                                      [&](int i, long long& ko, long long* vo, int* pos) {
-                                          return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (ga + i),
-                                                                        e.n_glob, true, j, kq, ko, vo,
-                                                                        pos);
-                                      });
+            if (ga < gb) {
+                // the block ids of all this wavefront's globals in one batch
+                const GlobalBlocks gbk = load_global_blocks(a, e, m, 16 * ga, lane);
+                walk_tiles<D, KVT, TRACK>(st, a, qv, gb - ga, j, kq, srow,
+                                          [&](int i, long long& ko, long long* vo, int* pos) {
+                                              return global_offsets(a, e, m, gbk, kvh, 16 * ga, i, j,
+                                                                    kq, ko, vo, pos);
+                                          });
+            }
         } else {
             walk_tiles<D, KVT, TRACK>(st, a, qv, wb - wa, j, kq, srow,
                                       [&](int i, long long& ko, long long* vo, int* pos) {
