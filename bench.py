@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c3h,c4,c5,gemv,gemv6,pool (default all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c2t,c3,c3h,c4,c5,gemv,gemv6,pool (default all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true",
                     help="GEMV section: issue the launches directly instead of replaying graphs")
@@ -178,6 +178,48 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
         "partition_tokens": nh.partition_tokens(1, Hkv, D, ctx),
         "workspace_bytes": ws_bytes,
     }
+
+
+def bench_c2_tracked(nh, torch, steps, seed=0):
+    """The 22-layer C2 step through the tracked form (ops::attention_tracked,
+    the executor's Full decode call, executor.rs:742-755): per layer the
+    decode launch also stores the scores, and a second launch adds
+    importance[t] = sum_h p_h[t] in f64.  Replayed from a HIP graph (no host
+    overhead), 3 rotated caches as for C2."""
+    L, ctx, Hq, Hkv, D, bt = 22, 4096, 32, 4, 64, 16
+    R = 3
+    nblk = ctx // bt
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    sets = []
+    for r in range(R):
+        for layer in range(L):
+            kp = torch.randn((nblk, Hkv, bt, D), generator=g, device="cuda")
+            vp = torch.randn((nblk, Hkv, bt, D), generator=g, device="cuda")
+            tab = torch.from_numpy(paged_tables(rng, 1, nblk, nblk)).cuda()
+            q = torch.randn((1, Hq, D), generator=g, device="cuda")
+            sets.append((q, kp, vp, tab))
+    ctx_t = torch.full((1,), ctx, dtype=torch.int32, device="cuda")
+    out = torch.empty((1, Hq, D), device="cuda")
+    imp = torch.zeros((L, 1, ctx + 2), dtype=torch.float64, device="cuda")
+    scores = torch.empty((1, Hq, ctx + 2), dtype=torch.float32, device="cuda")
+    ws = nh.alloc_workspace(nh.decode_workspace_size(1, Hq, Hkv, D, ctx))
+
+    def step_of(r):
+        def step():
+            for layer in range(L):
+                q, kp, vp, tab = sets[r * L + layer]
+                nh.paged_decode_tracked(q, kp, vp, tab, ctx_t, out, imp[layer], Hq, Hkv, D, bt,
+                                        max_ctx=ctx, workspace=ws, scores=scores)
+        return step
+
+    us = [_graph_us(torch, step_of(r), max(steps // R, 5)) for r in range(R)]
+    step_us = float(np.mean(us))
+    bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
+    return {"timing": "graph replay" if USE_GRAPHS else "direct launches",
+            "ms_per_step": step_us * 1e-3, "us_per_layer": step_us / L,
+            "gbs": L * bytes_layer / (step_us * 1e-6) / 1e9, "bytes_per_layer": bytes_layer,
+            "score_and_importance_bytes_per_layer": Hq * (ctx + 2) * 4 * 2 + (ctx + 2) * 8 * 2}
 
 
 def cpu_baseline_c2(seed=0):
@@ -716,7 +758,7 @@ def main():
     nh.init(0)
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool"}
+    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool"}
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -730,6 +772,10 @@ def main():
     if "c2" in only:
         log("22-layer decode step, ctx 4096")
         res["c2"] = bench_c2(nh, torch, steps, warmup)
+    if "c2t" in only:
+        log("22-layer decode step, tracked form (scores + importance)")
+        res["c2_tracked"] = bench_c2_tracked(nh, torch, steps)
+        torch.cuda.empty_cache()
     if "c1" in only:
         log("contiguous 128-position node")
         res["c1"] = bench_c1(nh, torch, steps, warmup)
