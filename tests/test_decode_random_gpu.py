@@ -1,0 +1,71 @@
+"""Seeded random sweep of paged decode against the oracle (gpu).
+
+Each case draws a configuration the fixed-shape tests leave out: KV format
+(f32, binary16, Q4-20B), head_dim 64 or 128, kv heads and GQA group (up to
+32 q heads per kv head), page size 4..64 tokens (the per-row gather path
+below 16), batch 1..6 with context lengths 1..3000, and full, sliding-window
+or window-plus-strided-globals position sets (ops::attention and
+ops::attention_sparse, swamp-engine/src/ops.rs:170-278, 85-168), with and
+without explicit q positions.  Tolerance as for every attention output:
+max-abs-err <= 2e-3 and max|diff| / max|ref| <= 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-3
+N_CASES = 64
+
+
+def to_dev(x):
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.uint16:
+        return torch.from_numpy(x.view(np.int16)).cuda()
+    return torch.from_numpy(x).cuda()
+
+
+def draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    kv = [oracle.KV_F32, oracle.KV_F16, oracle.KV_Q4][seed % 3]
+    hd = int(rng.choice([64, 128]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8, 16, 32]))
+    while hkv * group > 64:
+        group //= 2
+    bt = int(rng.choice([4, 8, 16, 32, 64]))
+    batch = int(rng.integers(1, 7))
+    ctx = [int(x) for x in rng.integers(1, 3001, size=batch)]
+    mode = ["full", "window", "globals"][int(rng.integers(0, 3))]
+    window = int(rng.choice([16, 100, 512, 1024])) if mode != "full" else 0
+    stride = int(rng.choice([16, 64])) if mode == "globals" else 0
+    q_pos = [int(rng.integers(0, c)) for c in ctx] if rng.random() < 0.4 else None
+    return dict(kv=kv, hd=hd, hkv=hkv, hq=hkv * group, bt=bt, ctx=ctx, window=window,
+                stride=stride, q_pos=q_pos)
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_decode(gpu, seed):
+    c = draw(seed)
+    print(f"case {seed}: {c}", flush=True)
+    pb = W.paged_batch(c["ctx"], n_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"],
+                       block_tokens=c["bt"], seed=seed, kv_dtype=c["kv"])
+    q = to_dev(pb.q)
+    kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    qp = None if c["q_pos"] is None else to_dev(np.asarray(c["q_pos"], np.int32))
+    out = torch.full_like(q, float("nan"))
+    gpu.paged_decode(q, kp, vp, tab, ctx, out, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                     pb.block_tokens, kv_dtype=pb.kv_dtype, window=c["window"],
+                     global_stride=c["stride"], max_ctx=int(pb.ctx_lens.max()), q_pos=qp)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    ref = W.reference_decode(pb, window=c["window"], global_stride=c["stride"], q_pos=c["q_pos"],
+                             threads=8).astype(np.float64)
+    assert np.all(np.isfinite(got)), c
+    err = np.max(np.abs(got - ref))
+    rel = err / max(np.max(np.abs(ref)), 1e-30)
+    assert err <= ATOL and rel <= RTOL, f"{c}: max-abs {err:.3e} rel {rel:.3e}"
