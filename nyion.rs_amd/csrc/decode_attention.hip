@@ -996,38 +996,49 @@ void decode_kernel(DecodeArgs a) {
 __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
     // (m, l) of up to 256 heads at a time, staged in LDS by vector loads (as
     // wave-uniform scalar loads behind the per-head guard the compiler
-    // issued them one head, and one round trip, at a time)
+    // issued them one head, and one round trip, at a time).  A barrier waits
+    // for every load in flight, so the sequence's length, the chunk's (m, l)
+    // and the first 32 heads' scores are all requested before the first one.
+    constexpr int HB = 32;  // score loads issued together
     __shared__ float2 sml[256];
     const int t = blockIdx.x * 256 + threadIdx.x;
+    const int tt = min(t, a.scores_stride - 3);  // in-row address for any thread
     for (int b = blockIdx.y; b < a.batch; b += gridDim.y) {
-        const Extent e = lane_extent<true>(a, b);
-        const bool in_window = t >= e.lo && t <= e.hi;
-        const bool global = e.n_glob > 0 && t % a.global_stride == 0 && t / a.global_stride < e.n_glob;
-        const bool active = in_window || global;
         const float* rows = a.scores + (long long)b * a.n_heads * a.scores_stride;
+        const Extent e = lane_extent<true>(a, b);
         double acc = 0.0;
+        bool active = false;
         for (int h0 = 0; h0 < a.n_heads; h0 += 256) {
             const int hn = min(256, a.n_heads - h0);
-            __syncthreads();  // the previous chunk's readers are done
+            float2 ml = float2{0.f, 1.f};
             if ((int)threadIdx.x < hn) {
                 const float* row = rows + (long long)(h0 + threadIdx.x) * a.scores_stride;
-                sml[threadIdx.x] = float2{row[a.scores_stride - 2], row[a.scores_stride - 1]};
+                ml = float2{row[a.scores_stride - 2], row[a.scores_stride - 1]};
             }
-            __syncthreads();
-            if (!active) continue;
-            // heads in ascending order, 32 score loads issued before any is
-            // used
-            constexpr int HB = 32;
-            for (int k0 = 0; k0 < hn; k0 += HB) {
-                float sv[HB];
+            float sv[HB];
 #pragma unroll
-                for (int k = 0; k < HB; k++)
-                    sv[k] = rows[(long long)(h0 + min(k0 + k, hn - 1)) * a.scores_stride + t];
+            for (int k = 0; k < HB; k++)
+                sv[k] = rows[(long long)(h0 + min(k, hn - 1)) * a.scores_stride + tt];
+            __syncthreads();  // the previous chunk's readers are done
+            if ((int)threadIdx.x < hn) sml[threadIdx.x] = ml;
+            __syncthreads();
+            const bool in_window = t >= e.lo && t <= e.hi;
+            const bool global =
+                e.n_glob > 0 && t % a.global_stride == 0 && t / a.global_stride < e.n_glob;
+            active = in_window || global;
+            if (!active) continue;
+            // heads in ascending order
+            for (int k0 = 0; k0 < hn; k0 += HB) {
+                if (k0 > 0) {
+#pragma unroll
+                    for (int k = 0; k < HB; k++)
+                        sv[k] = rows[(long long)(h0 + min(k0 + k, hn - 1)) * a.scores_stride + t];
+                }
 #pragma unroll
                 for (int k = 0; k < HB; k++)
                     if (k0 + k < hn) {
-                        const float2 ml = sml[k0 + k];
-                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - ml.x) / ml.y);
+                        const float2 m = sml[k0 + k];
+                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) / m.y);
                     }
             }
         }
