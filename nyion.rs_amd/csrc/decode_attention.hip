@@ -1518,10 +1518,16 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
     if ((rc = plan_common(pl, 1, (int)n_heads, (int)n_kv_heads, (int)head_dim, kv_dtype,
                           (int)seq_len, false, true, 0.f)) != NYION_OK)
         return rc;
-    // The node's scores buffer (n_heads*kv_stride floats, the reference's
-    // ScratchBuffers::d_scores) holds the split-K partials when it is large
-    // enough; otherwise one workgroup covers each head group.
+    // The host knows the length: a segment is exactly ceil(seq_len/16) tiles
+    // from position 0.  When one workgroup's share covers that, the launch
+    // runs whole segments (grid = units): no partials, no counters, and so
+    // no counter-clearing launch.
     DecodeArgs& a = pl.a;
+    pl.tiles_max = (int)((seq_len + 15) / 16);
+    if (pl.tiles_max <= wg_tiles_for((long long)a.n_kv_heads * a.n_hg * pl.tiles_max)) pl.ws_bytes = 0;
+    // Otherwise the node's scores buffer (n_heads*kv_stride floats, the
+    // reference's ScratchBuffers::d_scores) holds the split-K partials when
+    // it is large enough; failing that, one workgroup covers each head group.
     const size_t scores_bytes =
         d_scores && aligned(d_scores, 256) ? (size_t)n_heads * kv_stride * sizeof(float) : 0;
     const int units = a.n_kv_heads * a.n_hg;
