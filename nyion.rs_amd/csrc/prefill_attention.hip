@@ -64,8 +64,8 @@ struct PrefillArgs {
     int n_heads;
     int n_kv_heads;
     int group;     // q heads per kv head
-    int hw;        // q heads per workgroup (min(group, 4))
-    int rb_per_wg; // 32-row blocks per workgroup (4 / hw)
+    int hw;        // q heads per workgroup (4, 2 or 1: the largest dividing the group)
+    int rb_per_wg; // 32-row blocks per workgroup (wavefronts / hw)
     int n_rbg;     // row-block groups
     int n_items;   // kv heads x head subsets x row-block groups
     int causal;
@@ -507,11 +507,12 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
         (long long)n_hist + n + 2 * BN >= (1LL << 31))
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: history of %d tokens too large", n_hist);
     const int group = n_heads / n_kv_heads;
-    const int hw = group < 4 ? group : 4;
+    // q heads per workgroup: 4, 2 or 1, the largest that divides the group
+    // (and so also the wavefront count); the remaining wavefronts take more
+    // row blocks of the same heads
+    int hw = 4;
+    while (group % hw) hw /= 2;
     const int waves = (head_dim == 128 ? 512 : 256) / 64;
-    if (4 % hw || group % hw)
-        return set_error(NYION_ERR_UNSUPPORTED, "prefill: GQA group %d (need 1, 2 or a multiple of 4)",
-                         group);
     PrefillArgs a{};
     a.q = q;
     a.k = k;

@@ -1,6 +1,7 @@
 """Seeded random sweep of causal prefill against the oracle (gpu).
 
-Each case draws kv heads (1..8), a GQA group of 1..16 q heads per kv head,
+Each case draws kv heads (1..8), a GQA group of 1..16 q heads per kv head
+(odd groups included: 3, 5 and 7 run one q head per workgroup),
 head_dim 64 or 128, a chunk of 1..400 rows and, in two cases of three, a
 cached history of 1..400 tokens before it (the chunked prefill of
 swamp-engine/src/executor.rs:85-137: row i attends to keys [0, n_hist + i]),
@@ -21,7 +22,7 @@ N_CASES = 24
 def draw(seed):
     rng = np.random.default_rng(2000 + seed)
     hkv = int(rng.choice([1, 2, 4, 8]))
-    group = int(rng.choice([1, 2, 4, 8, 16]))
+    group = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 12, 16]))
     while hkv * group > 32:
         group //= 2
     d = int(rng.choice([64, 128]))
