@@ -1006,6 +1006,10 @@ __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* i
     for (int b = blockIdx.y; b < a.batch; b += gridDim.y) {
         const float* rows = a.scores + (long long)b * a.n_heads * a.scores_stride;
         const Extent e = lane_extent<true>(a, b);
+        // the accumulated value, read with the other loads (written back below
+        // only by the threads of attended positions)
+        double* dst = imp + (long long)b * imp_stride + min(t, imp_stride - 1);
+        const double prev = *dst;
         double acc = 0.0;
         bool active = false;
         for (int h0 = 0; h0 < a.n_heads; h0 += 256) {
@@ -1042,7 +1046,7 @@ __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* i
                     }
             }
         }
-        if (active) imp[(long long)b * imp_stride + t] += acc;
+        if (active) *dst = prev + acc;
     }
 }
 
