@@ -1,29 +1,36 @@
 """Benchmark of the MI355X attention path (one GPU).
 
-Workload of the headline line: one full 22-layer decode
-step at TinyLlama-1.1B attention shape -- batch 1, 32 q / 4 kv heads,
-head_dim 64, f32 KV context 4096 in a paged cache of 16-token blocks with a
-seeded random permutation block table.  A step is 22 calls of
-nyion_paged_decode_attention, one per layer, each on its own K/V pools.
-Inputs are resident in HBM before timing.  Three independent copies of the
-22-layer cache (555 MB) are rotated step to step, so the 185 MB of one step
-never sits in the 256 MB Infinity Cache from the previous step.
+Headline workload (the configuration the >= 70 % HBM target is quoted on):
+continuous-batching decode, 64 sequences, 32 q / 4 kv heads, head_dim 64,
+per-sequence context lengths drawn uniform in [512, 32768] (numpy PCG64,
+seed 0), paged f32 KV in 16-token blocks with shuffled block tables in one
+shared pool.  A step is one nyion_paged_decode_attention call over the whole
+batch (one decode launch).  Inputs are resident in HBM before timing; the
+2.2 GB the call reads is far larger than the 256 MB Infinity Cache.
 
-metric/unit: achieved algorithmic HBM bandwidth of the decode step in GB/s
-(K + V + q + out + block table bytes, counted once), with us/layer beside it.
-The other workloads are measured in the same run and reported under
-"configs", keyed by their --only selector: c1 (contiguous 128-position
-node), c3 (64-sequence continuous batch; c3h the same on binary16 KV),
-c4 (4-bit KV, 131072 context,
-window 4096), c5 (causal prefill of 8192 tokens, TFLOP/s against the bf16
-MFMA peak), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV
-pool with host spill).
+metric/unit: achieved algorithmic HBM bandwidth of the decode call in GB/s
+(K + V + q + out + block-table bytes, each counted once), with the call's
+microseconds beside it.  The other workloads are measured in the same run
+and reported under "configs", keyed by their --only selector: c1
+(contiguous 128-position node), c2 (22-layer TinyLlama decode step, ctx
+4096; c2t the same through the tracked form), c3h (the headline batch on
+binary16 KV), c4 (4-bit KV, 131072 context, window 4096, cold), c5 (causal
+prefill of 8192 tokens with its paged KV write, TFLOP/s against the bf16
+MFMA peak), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV pool
+with host spill).
 
-roofline: the decode call (one decode kernel launch, split-K merge fused) timed with
-HIP events on the stream it is launched on, against 8 TB/s.
+Timing: `ms_per_step` is the wall clock over exactly K calls bracketed by
+device synchronisation; per-call statistics (median, p10, p90) come from
+an event pair recorded around each of >= 20 further calls on the launching
+stream; `roofline.achieved` divides the algorithmic bytes (or FLOPs) of one
+launch by the mean launch duration over back-to-back calls timed with HIP
+events on the launching stream, which is what the rocprofv3 kernel-trace
+average under profiles/ measures.
 cpu_baseline: the C restatement of ops::attention (oracle/, the reference's
-AVX-512 dot/axpy order, OpenMP over heads) on the host cores, one layer of
-the headline workload at a time, 6 threads (the reference executor's rayon pool) and all cores.
+AVX-512 dot/axpy order, OpenMP over heads) on the host cores, on a bounded
+sample of the headline batch (the first sequences, scaled by attended
+tokens), at all host cores and at 6 threads (the reference executor's rayon
+pool).
 """
 from __future__ import annotations
 
@@ -42,6 +49,7 @@ for sub in ("nyion.rs_amd", "oracle", "tests"):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = ("decode-attn µs/layer + achieved HBM GB/s (% peak); prefill TFLOP/s (% MFMA)")
+ALL = ("c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool")
 
 
 def log(msg):
@@ -53,8 +61,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c2t,c3,c3h,c4,c5,gemv,gemv6,pool (default all)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of " + ",".join(ALL) + " (default all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-graph", action="store_true",
                     help="GEMV section: issue the launches directly instead of replaying graphs")
     ap.add_argument("--calib-copy", action="store_true",
@@ -68,8 +76,8 @@ def parse():
 
 def timed(fn, steps, warmup, torch):
     """W untimed, then K timed; synchronize on both sides; ms per call."""
-    for _ in range(warmup):
-        fn(0)
+    for i in range(warmup):
+        fn(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -94,18 +102,49 @@ def event_mean(fn, reps, torch):
     return a.elapsed_time(b) / reps
 
 
-def pmc_traffic(workload):
-    """HBM bytes per launch of the decode kernel for `workload`, from the
-    calibrated FETCH_SIZE + WRITE_SIZE passes summarised under profiles/."""
-    path = os.path.join(ROOT, "profiles", "decode_hbm_traffic_pmc.txt")
+def event_pcts(fn, reps, torch):
+    """Per-call device time (ms): an event pair on the launching stream
+    around each of `reps` calls; returns p10, median, p90."""
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    fn(0)
+    torch.cuda.synchronize()
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(st)
+        fn(i)
+        e1.record(st)
+    torch.cuda.synchronize()
+    p10, p50, p90 = np.percentile([e0.elapsed_time(e1) for e0, e1 in evs], [10, 50, 90])
+    return float(p10), float(p50), float(p90)
+
+
+def _us3(p):
+    return [round(x * 1e3, 3) for x in p]
+
+
+def _profile_value(fname, key, workload):
+    """A machine-readable line `key workload value` of a summary under profiles/."""
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, "profiles", fname)):
             f = line.split()
-            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == workload:
+            if len(f) == 3 and f[0] == key and f[1] == workload:
                 return float(f[2])
     except OSError:
         pass
     return None
+
+
+def pmc_traffic(workload):
+    """HBM bytes per launch of the decode kernel for `workload`, from the
+    calibrated FETCH_SIZE + WRITE_SIZE passes summarised under profiles/."""
+    return _profile_value("decode_hbm_traffic_pmc.txt", "traffic_bytes_per_launch", workload)
+
+
+def hbm_roofline(nbytes, us, traffic):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
 
 
 def paged_tables(rng, n_seqs, nblk, total):
@@ -113,13 +152,127 @@ def paged_tables(rng, n_seqs, nblk, total):
     return perm[: n_seqs * nblk].reshape(n_seqs, nblk)
 
 
+def _cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _cpu_time(fn, budget_s=2.0, max_calls=2000):
+    """Mean seconds per call of fn after one warm call, over about budget_s."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= max_calls:
+            return el / n, n
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 # ----------------------------------------------------------------------------
-# 22-layer decode step, ctx 4096 (headline; selector c2)
+# continuous batch (headline; selector c3, c3h on binary16 KV)
+# ----------------------------------------------------------------------------
+
+C3_HQ, C3_HKV, C3_D, C3_BT = 32, 4, 64, 16
+
+
+def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
+    """64-sequence continuous batch; f16=True stores the same K/V draw as
+    binary16 rows (half the bytes)."""
+    import workloads as W
+
+    Hq, Hkv, D, bt = C3_HQ, C3_HKV, C3_D, C3_BT
+    lens = W.c3_lengths(seed=seed)
+    nblk = (lens + bt - 1) // bt
+    total = int(nblk.sum())
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.zeros((64, int(nblk.max())), np.int32)
+    off = 0
+    for b in range(64):
+        tables[b, : nblk[b]] = perm[off: off + nblk[b]]
+        off += nblk[b]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
+    vp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
+    if f16:
+        kp, vp = kp.half(), vp.half()
+    q = torch.randn((64, Hq, D), generator=g, device="cuda")
+    tab = torch.from_numpy(tables).cuda()
+    ctx = torch.from_numpy(lens).cuda()
+    out = torch.empty_like(q)
+    maxc = int(lens.max())
+    ws = nh.alloc_workspace(nh.decode_workspace_size(64, Hq, Hkv, D, maxc))
+    kvt = nh.KV_F16 if f16 else nh.KV_F32
+    call1 = nh.prepare_paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, maxc, kv_dtype=kvt,
+                                    workspace=ws)
+
+    def call(i):
+        call1()
+
+    toks = int(lens.sum())
+    nbytes = 2 * toks * Hkv * D * (2 if f16 else 4) + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
+    ms = timed(call, steps, warmup, torch)
+    reps = max(steps, 20)
+    us = event_mean(call, reps, torch) * 1e3
+    pct = event_pcts(call, reps, torch)
+    return {"ms_per_call_wall": ms, "us_per_layer": us, "us_p10_p50_p90": _us3(pct),
+            "reps": reps, "bytes": nbytes, "tokens": toks,
+            "gbs_wall": nbytes / (ms * 1e-3) / 1e9, "gbs": nbytes / (us * 1e-6) / 1e9,
+            "gbs_median": nbytes / (pct[1] * 1e-3) / 1e9,
+            "roofline": hbm_roofline(nbytes, us, pmc_traffic("c3h" if f16 else "c3")),
+            "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
+
+
+def cpu_baseline_c3(seed=0, n_sample=2, budget_s=5.0):
+    """Oracle on the first n_sample sequences of the 64-sequence batch (same
+    context lengths), scaled by attended tokens to the batch; at all host
+    cores and at 6 threads."""
+    import oracle
+    import workloads as W
+
+    lens = W.c3_lengths(seed=seed)
+    pb = W.paged_batch([int(x) for x in lens[:n_sample]], seed=seed)
+    toks_sample, toks_all = int(lens[:n_sample].sum()), int(lens.sum())
+    nbytes = 2 * toks_all * 4 * 64 * 4 + int(((lens + 15) // 16).sum()) * 4 + 2 * 64 * 32 * 64 * 4
+    res = {}
+    for label, thr in (("all", _cores()), ("6", 6)):
+        def run():
+            for b in range(n_sample):
+                oracle.attention(pb.q[b], pb.layout(b), int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
+                                 threads=thr)
+        dt, n = _cpu_time(run, budget_s=budget_s)
+        res[label] = (thr, n, dt, dt * toks_all / toks_sample)
+    thr, n, dt, est = res["all"]
+    thr6, n6, dt6, est6 = res["6"]
+    return {"value": round(nbytes / est / 1e9, 3), "unit": "GB/s", "cores": thr, "kind": "port",
+            "sample": (f"{n} runs over sequences 0-{n_sample - 1} of the batch ({toks_sample} tokens, "
+                       f"{dt * 1e3:.1f} ms per run at {thr} threads), scaled by attended tokens to "
+                       f"the batch's {toks_all}: {est * 1e3:.1f} ms per call; at 6 threads "
+                       f"{est6 * 1e3:.1f} ms ({nbytes / est6 / 1e9:.2f} GB/s)"),
+            "us_per_layer": est * 1e6, "us_per_layer_6_threads": est6 * 1e6,
+            "cpu_model": _cpu_model()}
+
+
+# ----------------------------------------------------------------------------
+# 22-layer decode step, ctx 4096 (selector c2)
 # ----------------------------------------------------------------------------
 
 def bench_c2(nh, torch, steps, warmup, seed=0):
     L, ctx, Hq, Hkv, D, bt = 22, 4096, 32, 4, 64, 16
-    R = 3  # rotated copies of the whole 22-layer cache
+    R = 3  # rotated copies of the whole 22-layer cache (555 MB > the 256 MB MALL)
     nblk = ctx // bt
     rng = np.random.default_rng(seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -144,37 +297,26 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
                                       workspace=ws)
               for layer, (q, kp, vp, tab) in enumerate(layers[r])] for r in range(R)]
 
-    def layer_call(r, layer):
-        calls[r][layer]()
-
     def step(i):
-        r = i % R
-        for layer in range(L):
-            layer_call(r, layer)
+        for c in calls[i % R]:
+            c()
 
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
     ms = timed(step, steps, warmup, torch)
-    # spread of the step time: each of another `steps` steps between two events
-    st = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
-    for i, (e0, e1) in enumerate(evs):
-        e0.record(st)
-        step(i)
-        e1.record(st)
-    torch.cuda.synchronize()
-    p10, p50, p90 = np.percentile([e0.elapsed_time(e1) for e0, e1 in evs], [10, 50, 90])
-    # roofline: decode calls timed with HIP events on the launching stream
-    us_call = event_mean(lambda i: layer_call(i % R, i % L), steps * L, torch) * 1e3
-    achieved = bytes_layer / (us_call * 1e-6) / 1e9
+    pct_step = event_pcts(step, max(steps, 20), torch)
+    reps = max(steps, 20) * L
+    one = lambda i: calls[i % R][i % L]()  # noqa: E731
+    us_call = event_mean(one, reps, torch) * 1e3
+    pct = event_pcts(one, max(steps, 20) * 3, torch)
     return {
         "ms_per_step": ms,
-        "step_ms_p10_p50_p90": [round(float(x), 4) for x in (p10, p50, p90)],
+        "step_ms_p10_p50_p90": [round(x, 4) for x in pct_step],
         "us_per_layer": ms * 1e3 / L,
         "gbs": L * bytes_layer / (ms * 1e-3) / 1e9,
         "bytes_per_layer": bytes_layer,
         "call_us_event_mean": us_call,
-        "achieved_call_gbs": achieved,
+        "call_us_p10_p50_p90": _us3(pct),
+        "roofline": hbm_roofline(bytes_layer, us_call, pmc_traffic("c2")),
         "partition_tokens": nh.partition_tokens(1, Hkv, D, ctx),
         "workspace_bytes": ws_bytes,
     }
@@ -205,25 +347,33 @@ def bench_c2_tracked(nh, torch, steps, seed=0):
     scores = torch.empty((1, Hq, ctx + 2), dtype=torch.float32, device="cuda")
     ws = nh.alloc_workspace(nh.decode_workspace_size(1, Hq, Hkv, D, ctx))
 
-    def step_of(r):
+    def step_of(r, tracked):
         def step():
             for layer in range(L):
                 q, kp, vp, tab = sets[r * L + layer]
-                nh.paged_decode_tracked(q, kp, vp, tab, ctx_t, out, imp[layer], Hq, Hkv, D, bt,
-                                        max_ctx=ctx, workspace=ws, scores=scores)
+                if tracked:
+                    nh.paged_decode_tracked(q, kp, vp, tab, ctx_t, out, imp[layer], Hq, Hkv, D,
+                                            bt, max_ctx=ctx, workspace=ws, scores=scores)
+                else:
+                    nh.paged_decode(q, kp, vp, tab, ctx_t, out, Hq, Hkv, D, bt, max_ctx=ctx,
+                                    workspace=ws)
         return step
 
-    us = [_graph_us(torch, step_of(r), max(steps // R, 5)) for r in range(R)]
-    step_us = float(np.mean(us))
+    reps = max(steps // R, 5)
+    us = [_graph_us(torch, step_of(r, True), reps) for r in range(R)]
+    us_plain = [_graph_us(torch, step_of(r, False), reps) for r in range(R)]
+    step_us, plain_us = float(np.mean(us)), float(np.mean(us_plain))
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
     return {"timing": "graph replay" if USE_GRAPHS else "direct launches",
             "ms_per_step": step_us * 1e-3, "us_per_layer": step_us / L,
+            "untracked_us_per_layer_same_timing": plain_us / L,
+            "tracked_over_untracked": step_us / plain_us,
             "gbs": L * bytes_layer / (step_us * 1e-6) / 1e9, "bytes_per_layer": bytes_layer,
             "score_and_importance_bytes_per_layer": Hq * (ctx + 2) * 4 * 2 + (ctx + 2) * 8 * 2}
 
 
 def cpu_baseline_c2(seed=0):
-    """Oracle (C restatement of ops::attention) on headline-workload layers, host cores."""
+    """Oracle (C restatement of ops::attention) on one C2 layer at a time."""
     import oracle
     import workloads as W
 
@@ -231,55 +381,16 @@ def cpu_baseline_c2(seed=0):
     lay = pb.layout(0)
     bytes_layer = 2 * 4096 * 4 * 64 * 4 + 256 * 4 + 2 * 32 * 64 * 4
     res = {}
-    ncores = os.cpu_count() or 1
-    try:
-        ncores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        pass
-    for label, thr in (("6", 6), ("all", ncores)):
-        oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr)  # warm
-        n, t0 = 0, time.perf_counter()
-        while True:
-            oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr)
-            n += 1
-            el = time.perf_counter() - t0
-            if el > 5.0 or n >= 2000:
-                break
-        res[label] = (thr, n, el / n * 1e6)
+    for label, thr in (("6", 6), ("all", _cores())):
+        dt, n = _cpu_time(lambda: oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr),
+                          budget_s=3.0)
+        res[label] = (thr, n, dt * 1e6)
     thr6, n6, us6 = res["6"]
     thra, na, usa = res["all"]
-    return {
-        "value": bytes_layer / (us6 * 1e-6) / 1e9,
-        "unit": "GB/s",
-        "cores": thr6,
-        "kind": "port",
-        "sample": (f"{n6} single-layer decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
-                   f"at {thr6} threads: {us6:.0f} us/layer; all {thra} cores: {usa:.0f} us/layer "
-                   f"({bytes_layer / (usa * 1e-6) / 1e9:.2f} GB/s)"),
-        "us_per_layer": us6,
-        "us_per_layer_all_cores": usa,
-        "cores_all": thra,
-        "cpu_model": _cpu_model(),
-    }
-
-
-def _cores():
-    try:
-        return len(os.sched_getaffinity(0))
-    except AttributeError:
-        return os.cpu_count() or 1
-
-
-def _cpu_time(fn, budget_s=2.0, max_calls=2000):
-    """Mean seconds per call of fn after one warm call, over about budget_s."""
-    fn()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        n += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or n >= max_calls:
-            return el / n, n
+    return {"value": bytes_layer / (usa * 1e-6) / 1e9, "unit": "GB/s", "cores": thra, "kind": "port",
+            "sample": (f"{na} single-layer decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
+                       f"at {thra} threads: {usa:.0f} us/layer; at 6 threads {us6:.0f} us/layer"),
+            "us_per_layer": usa, "us_per_layer_6_threads": us6}
 
 
 def cpu_baseline_c1():
@@ -297,29 +408,80 @@ def cpu_baseline_c1():
             "sample": f"{n} calls of the whole node (32/4 heads, D=64, 128 positions)"}
 
 
-def cpu_baseline_c3(seed=0, n_sample=2):
-    """Oracle on the first n_sample sequences of the 64-sequence batch (same
-    context lengths), extrapolated to the batch by attended tokens."""
-    import oracle
-    import workloads as W
+# ----------------------------------------------------------------------------
+# 4-bit KV, ctx 131072, window 4096 (selector c4)
+# ----------------------------------------------------------------------------
 
-    lens = W.c3_lengths(seed=seed)
-    pb = W.paged_batch([int(x) for x in lens[:n_sample]], seed=seed)
-    thr = _cores()
+C4_R = 64  # rotated block tables: 63 other windows (>= 660 MB) are read between two uses of one
 
-    def run():
-        for b in range(n_sample):
-            oracle.attention(pb.q[b], pb.layout(b), int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
-                             threads=thr)
 
-    dt, n = _cpu_time(run)
-    toks_sample, toks_all = int(lens[:n_sample].sum()), int(lens.sum())
-    est = dt * toks_all / toks_sample
-    nbytes = 2 * toks_all * 4 * 64 * 4
-    return {"value": est * 1e6, "unit": "us/layer (extrapolated)", "cores": thr, "kind": "port",
-            "gbs": nbytes / est / 1e9,
-            "sample": (f"{n} runs over sequences 0-{n_sample - 1} ({toks_sample} tokens, "
-                       f"{dt * 1e6:.0f} us), scaled by tokens to the batch's {toks_all}")}
+def c4_tables(rng, R, B, nblk, w, bt, stride):
+    """Block tables of R rotation sets for B sequences of nblk logical blocks:
+    the blocks a call attends (the window's w/bt last blocks and, with global
+    stride s, the blocks of positions s*g, g < 128) get distinct physical
+    blocks per (set, sequence), shuffled within that region; all other
+    entries point at the region's first block (never read).  Returns
+    ([R][B][nblk] int32, physical blocks)."""
+    att = list(range(nblk - w // bt, nblk))
+    if stride:
+        att = sorted(set(att) | {(stride * g) // bt for g in range(128)})
+    na = len(att)
+    tabs = np.zeros((R, B, nblk), np.int32)
+    for r in range(R):
+        for b in range(B):
+            base = (r * B + b) * na
+            tabs[r, b, :] = base
+            tabs[r, b, att] = base + rng.permutation(na)
+    return tabs, R * B * na
+
+
+def bench_c4(nh, torch, steps, warmup, seed=0):
+    B, ctx, w, Hq, Hkv, D, bt = 8, 131072, 4096, 32, 4, 64, 16
+    nblk = ctx // bt
+    rb = 40
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((B, Hq, D), generator=g, device="cuda")
+    ctxt = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    res = {}
+    for stride in (0, 64):
+        tabs, total = c4_tables(rng, C4_R, B, nblk, w, bt, stride)
+        kp = torch.empty((total, Hkv, bt, rb), dtype=torch.uint8, device="cuda")
+        vp = torch.empty_like(kp)
+        rows = total * Hkv * bt
+        chunk = 1 << 22
+        for pool in (kp, vp):
+            flat = pool.view(-1, rb)
+            for s in range(0, rows, chunk):
+                n = min(chunk, rows - s)
+                x = torch.randn((n, D), generator=g, device="cuda")
+                nh.q4_quantize(x, n, D, flat[s: s + n])
+        tab = torch.from_numpy(tabs).cuda()
+        torch.cuda.synchronize()
+        ws = nh.alloc_workspace(nh.decode_workspace_size(B, Hq, Hkv, D, ctx, w, stride))
+        calls = [nh.prepare_paged_decode(q, kp, vp, tab[r], ctxt, out, Hq, Hkv, D, bt, ctx,
+                                         kv_dtype=nh.KV_Q4_20B, window=w, global_stride=stride,
+                                         workspace=ws) for r in range(C4_R)]
+
+        def call(i):
+            calls[i % C4_R]()
+
+        n_pos = w + (128 if stride else 0)
+        nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4 + B * (n_pos // bt + 8) * 4
+        ms = timed(call, max(steps, C4_R), warmup, torch)
+        reps = max(steps, 2 * C4_R)
+        us = event_mean(call, reps, torch) * 1e3
+        pct = event_pcts(call, reps, torch)
+        res[f"stride{stride}"] = {
+            "us_per_layer": us, "us_per_layer_wall": ms * 1e3, "us_p10_p50_p90": _us3(pct),
+            "reps": reps, "bytes_packed": nbytes, "gbs_packed": nbytes / (us * 1e-6) / 1e9,
+            "cold": f"{C4_R} rotated block tables over {total} physical blocks "
+                    f"({2 * total * Hkv * bt * rb / 1e6:.0f} MB of K+V pools)",
+            "roofline": hbm_roofline(nbytes, us, pmc_traffic("c4" if stride == 0 else "c4s64"))}
+        del kp, vp, tab, calls, ws
+        torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline_c4(seed=0):
@@ -355,6 +517,50 @@ def cpu_baseline_c4(seed=0):
             "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0"}
 
 
+# ----------------------------------------------------------------------------
+# causal prefill, 8192 tokens (selector c5)
+# ----------------------------------------------------------------------------
+
+def bench_c5(nh, torch, steps, warmup, seed=0):
+    n, Hq, Hkv, D, bt = 8192, 32, 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((n, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((n, Hq, D), device="cuda")
+    nblk = n // bt
+    tab = torch.from_numpy(np.random.default_rng(seed).permutation(nblk).astype(np.int32)).cuda()
+    kp = torch.empty((nblk, Hkv, bt, D), device="cuda")
+    vp = torch.empty_like(kp)
+    flops = 4 * Hq * D * n * (n + 1) / 2
+
+    def attn(i):
+        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D)
+
+    def attn_kv(i):  # the configuration's work: prefill plus the paged KV write of the chunk
+        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D, k_pool=kp, v_pool=vp, block_table=tab,
+                        block_tokens=bt)
+
+    reps = max(20, steps)
+    ms_kv = timed(attn_kv, reps, max(2, warmup // 5), torch)
+    us = event_mean(attn, reps, torch) * 1e3
+    pct = event_pcts(attn, reps, torch)
+    us_kv = event_mean(attn_kv, reps, torch) * 1e3
+    pct_kv = event_pcts(attn_kv, reps, torch)
+    tf = flops / (us * 1e-6) / 1e12
+    busy = _profile_value("prefill_c5_mfma_counters.txt", "mfma_busy_frac", "c5")
+    return {"us_with_kv_write": us_kv, "us_with_kv_write_p10_p50_p90": _us3(pct_kv),
+            "us_with_kv_write_wall": ms_kv * 1e3,
+            "tflops_with_kv_write": flops / (us_kv * 1e-6) / 1e12,
+            "mfma_frac_with_kv_write": flops / (us_kv * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+            "us_prefill_kernel": us, "us_prefill_kernel_p10_p50_p90": _us3(pct), "reps": reps,
+            "flops": flops, "tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
+            "kv_write_bytes": 2 * n * Hkv * D * (2 + 4),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "traffic": None, "mfma_busy_frac_counters": busy}}
+
+
 def cpu_baseline_c5(seed=0, n_rows=256):
     """The reference's prefill: one decode call per row (executor.rs:132-137),
     timed on n_rows rows spread over the 8192 and scaled by attended keys."""
@@ -380,16 +586,6 @@ def cpu_baseline_c5(seed=0, n_rows=256):
                        f"({dt * 1e3:.1f} ms), scaled by attended keys to all 8192 rows")}
 
 
-def _cpu_model():
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
-
-
 # ----------------------------------------------------------------------------
 # other configs
 # ----------------------------------------------------------------------------
@@ -406,123 +602,9 @@ def bench_c1(nh, torch, steps, warmup):
 
     ms = timed(call, steps * 10, warmup, torch)
     us = event_mean(call, steps * 4, torch) * 1e3
-    return {"us_per_layer": ms * 1e3, "call_us_event_mean": us, "bytes_per_layer": 278528}
-
-
-def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
-    """64-sequence continuous batch; f16=True stores the same K/V draw as
-    binary16 rows (half the bytes)."""
-    import workloads as W
-
-    Hq, Hkv, D, bt = 32, 4, 64, 16
-    lens = W.c3_lengths(seed=seed)
-    nblk = (lens + bt - 1) // bt
-    total = int(nblk.sum())
-    rng = np.random.default_rng(seed)
-    perm = rng.permutation(total).astype(np.int32)
-    tables = np.zeros((64, int(nblk.max())), np.int32)
-    off = 0
-    for b in range(64):
-        tables[b, : nblk[b]] = perm[off: off + nblk[b]]
-        off += nblk[b]
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    kp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
-    vp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
-    if f16:
-        kp, vp = kp.half(), vp.half()
-    q = torch.randn((64, Hq, D), generator=g, device="cuda")
-    tab = torch.from_numpy(tables).cuda()
-    ctx = torch.from_numpy(lens).cuda()
-    out = torch.empty_like(q)
-    maxc = int(lens.max())
-    ws = nh.alloc_workspace(nh.decode_workspace_size(64, Hq, Hkv, D, maxc))
-    kvt = nh.KV_F16 if f16 else nh.KV_F32
-
-    def call(i):
-        nh.paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, kv_dtype=kvt, max_ctx=maxc,
-                        workspace=ws)
-
-    toks = int(lens.sum())
-    nbytes = 2 * toks * Hkv * D * (2 if f16 else 4) + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
-    ms = timed(call, steps, warmup, torch)
-    us = event_mean(call, steps, torch) * 1e3
-    gbs = nbytes / (us * 1e-6) / 1e9
-    return {"us_per_layer": us, "us_per_layer_wall": ms * 1e3, "bytes": nbytes, "tokens": toks,
-            "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": pmc_traffic("c3h" if f16 else "c3")},
-            "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
-
-
-def bench_c4(nh, torch, steps, warmup, seed=0):
-    B, ctx, w, Hq, Hkv, D, bt = 8, 131072, 4096, 32, 4, 64, 16
-    nblk = ctx // bt
-    total = B * nblk
-    rng = np.random.default_rng(seed)
-    tables = rng.permutation(total).astype(np.int32).reshape(B, nblk)
-    rb = 40
-    kp = torch.empty((total, Hkv, bt, rb), dtype=torch.uint8, device="cuda")
-    vp = torch.empty_like(kp)
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    rows = total * Hkv * bt
-    chunk = 1 << 22
-    for pool in (kp, vp):
-        flat = pool.view(-1, rb)
-        for s in range(0, rows, chunk):
-            n = min(chunk, rows - s)
-            x = torch.randn((n, D), generator=g, device="cuda")
-            nh.q4_quantize(x, n, D, flat[s: s + n])
-    torch.cuda.synchronize()
-    q = torch.randn((B, Hq, D), generator=g, device="cuda")
-    tab = torch.from_numpy(tables).cuda()
-    ctxt = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
-    out = torch.empty_like(q)
-    res = {}
-    for stride in (0, 64):
-        ws = nh.alloc_workspace(nh.decode_workspace_size(B, Hq, Hkv, D, ctx, w, stride))
-
-        def call(i):
-            nh.paged_decode(q, kp, vp, tab, ctxt, out, Hq, Hkv, D, bt, kv_dtype=nh.KV_Q4_20B,
-                            window=w, global_stride=stride, max_ctx=ctx, workspace=ws)
-
-        n_pos = w + (128 if stride else 0)
-        nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4 + B * (n_pos // bt + 8) * 4
-        ms = timed(call, steps, warmup, torch)
-        us = event_mean(call, steps, torch) * 1e3
-        res[f"stride{stride}"] = {"us_per_layer": us, "us_per_layer_wall": ms * 1e3,
-                                  "bytes_packed": nbytes,
-                                  "gbs_packed": nbytes / (us * 1e-6) / 1e9}
-    return res
-
-
-def bench_c5(nh, torch, steps, warmup, seed=0):
-    n, Hq, Hkv, D, bt = 8192, 32, 8, 128, 16
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    q = torch.randn((n, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
-    k = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
-    v = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
-    out = torch.empty((n, Hq, D), device="cuda")
-    nblk = n // bt
-    tab = torch.from_numpy(np.random.default_rng(seed).permutation(nblk).astype(np.int32)).cuda()
-    kp = torch.empty((nblk, Hkv, bt, D), device="cuda")
-    vp = torch.empty_like(kp)
-    flops = 4 * Hq * D * n * (n + 1) / 2
-
-    def attn(i):
-        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D)
-
-    def attn_kv(i):
-        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D, k_pool=kp, v_pool=vp, block_table=tab,
-                        block_tokens=bt)
-
-    s = max(3, steps // 5)
-    ms = timed(attn, s, max(1, warmup // 5), torch)
-    us = event_mean(attn, s, torch) * 1e3
-    ms_kv = timed(attn_kv, s, 1, torch)
-    tf = flops / (us * 1e-6) / 1e12
-    return {"us": us, "us_wall": ms * 1e3, "us_with_kv_write": ms_kv * 1e3, "flops": flops,
-            "tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+    pct = event_pcts(call, max(steps, 20), torch)
+    return {"us_per_layer": ms * 1e3, "call_us_event_mean": us, "call_us_p10_p50_p90": _us3(pct),
+            "bytes_per_layer": 278528}
 
 
 def _q4k_random(torch, rows, cols, seed):
@@ -758,7 +840,7 @@ def main():
     nh.init(0)
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
-    only = set(filter(None, args.only.split(","))) or {"c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool"}
+    only = set(filter(None, args.only.split(","))) or set(ALL)
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     res = {}
     if args.calib_copy:
@@ -769,9 +851,18 @@ def main():
         torch.cuda.synchronize()
         log("calibration copy: 3 x 512 MiB")
         del a, b
+    if "c3" in only:
+        log("64-sequence continuous batch (headline)")
+        res["c3"] = bench_c3(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
+    if "c3h" in only:
+        log("64-sequence continuous batch, binary16 KV")
+        res["c3h"] = bench_c3(nh, torch, steps, warmup, f16=True)
+        torch.cuda.empty_cache()
     if "c2" in only:
         log("22-layer decode step, ctx 4096")
         res["c2"] = bench_c2(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
     if "c2t" in only:
         log("22-layer decode step, tracked form (scores + importance)")
         res["c2_tracked"] = bench_c2_tracked(nh, torch, steps)
@@ -779,21 +870,14 @@ def main():
     if "c1" in only:
         log("contiguous 128-position node")
         res["c1"] = bench_c1(nh, torch, steps, warmup)
-    if "c3" in only:
-        log("64-sequence continuous batch")
-        res["c3"] = bench_c3(nh, torch, steps, warmup)
-        torch.cuda.empty_cache()
-    if "c3h" in only:
-        log("64-sequence continuous batch, binary16 KV")
-        res["c3h"] = bench_c3(nh, torch, steps, warmup, f16=True)
-        torch.cuda.empty_cache()
     if "c4" in only:
-        log("Q4 KV, ctx 131072, window 4096")
+        log("Q4 KV, ctx 131072, window 4096 (cold: rotated tables)")
         res["c4"] = bench_c4(nh, torch, steps, warmup)
         torch.cuda.empty_cache()
     if "c5" in only:
-        log("causal prefill N=8192")
+        log("causal prefill N=8192 with paged KV write")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
     if "pool" in only:
         log("paged KV pool: cold-page round trips over the host link")
         res["kv_pool"] = bench_kv_pool(nh, torch, steps, warmup)
@@ -803,52 +887,47 @@ def main():
     if "gemv6" in only:
         log("Q6_K weight GEMV: TinyLlama output projection, Q4_K_M-style decode step")
         res["gemv_q6k"] = bench_gemv_q6k(nh, torch, steps, warmup, cpu=not args.no_cpu)
+    cpu = None
     if not args.no_cpu:
-        for key, fn in (("c1", cpu_baseline_c1), ("c3", cpu_baseline_c3), ("c4", cpu_baseline_c4),
+        for key, fn in (("c1", cpu_baseline_c1), ("c2", cpu_baseline_c2), ("c4", cpu_baseline_c4),
                         ("c5", cpu_baseline_c5)):
             if key in res:
                 log(f"CPU baseline (oracle) for {key}")
                 res[key]["cpu_baseline"] = fn()
-    cpu = None
-    if not args.no_cpu and "c2" in only:
-        log("CPU baseline (oracle) on headline-workload layers")
-        cpu = cpu_baseline_c2()
+        if "c3" in res:
+            log("CPU baseline (oracle) on a sample of the headline batch")
+            cpu = cpu_baseline_c3()
 
-    c2 = res.get("c2")
+    c3 = res.get("c3")
     line = {
         "metric": METRIC,
-        "value": round(c2["gbs"], 2) if c2 else None,
+        "value": round(c3["gbs_wall"], 2) if c3 else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(c2["ms_per_step"], 4) if c2 else None,
+        "ms_per_step": round(c3["ms_per_call_wall"], 4) if c3 else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded N(0,1); paged 16-token blocks, shuffled tables)",
-        "config": {"workload": "decode-22-layer-tinyllama-ctx4096-paged16-f32", "batch": 1,
-                   "layers": 22, "n_heads": 32, "n_kv_heads": 4, "head_dim": 64,
-                   "context": 4096, "block_tokens": 16, "parallelism": "single-gpu"},
+        "config": {"workload": "decode-continuous-batch-64seq-ctx512-32768-paged16-f32",
+                   "batch": 64, "n_heads": C3_HQ, "n_kv_heads": C3_HKV, "head_dim": C3_D,
+                   "context": "uniform [512, 32768], numpy PCG64 seed 0",
+                   "block_tokens": C3_BT, "parallelism": "single-gpu"},
     }
-    if c2:
-        line["us_per_layer"] = round(c2["us_per_layer"], 3)
-        line["ms_per_step_p10_p50_p90"] = c2["step_ms_p10_p50_p90"]
-        line["roofline"] = {
-            "bound": "hbm",
-            "achieved": round(c2["achieved_call_gbs"], 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(c2["achieved_call_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": pmc_traffic("c2"),
-            "kernel": "decode_kernel<64,f32,aligned> (one launch per decode call)",
-            "bytes_per_launch": c2["bytes_per_layer"],
-            "launch_us": round(c2["call_us_event_mean"], 3),
-        }
+    if c3:
+        line["us_per_layer"] = round(c3["us_per_layer"], 3)
+        line["us_p10_p50_p90"] = c3["us_p10_p50_p90"]
+        line["config"]["tokens"] = c3["tokens"]
+        rl = dict(c3["roofline"])
+        rl.update({"kernel": "decode_kernel<64,f32,aligned> (one launch per decode call)",
+                   "bytes_per_launch": c3["bytes"], "launch_us": round(c3["us_per_layer"], 3)})
+        line["roofline"] = rl
     if cpu:
         line["cpu_baseline"] = cpu
-    line["configs"] = {k: v for k, v in res.items()}
+    line["configs"] = {k: v for k, v in res.items() if k != "c3"}
     print(json.dumps(line), flush=True)
 
 
