@@ -48,7 +48,8 @@ enum nyion_status {
     NYION_ERR_NO_DEVICE = -3,   /* no HIP device / not gfx950 */
     NYION_ERR_OOM = -4,         /* allocation failed (arena or HIP) */
     NYION_ERR_LAUNCH = -5,      /* HIP launch or runtime error */
-    NYION_ERR_WORKSPACE = -6    /* caller workspace too small */
+    NYION_ERR_WORKSPACE = -6,   /* caller workspace too small */
+    NYION_ERR_RANGE = -7        /* an input exceeded a reduced-precision operand (nyion_take_status) */
 };
 
 /* KV row formats: f32; the reference's Q4-20B groups; IEEE binary16 (the
@@ -69,6 +70,19 @@ int nyion_sync(void);
 /* Library version string. */
 const char* nyion_version(void);
 
+/* Range report of the current device.  Kernels that carry an input in a
+ * narrower format than the reference's f32 record, in a per-device sticky
+ * word, when an input does not fit it: prefill's V (binary16 in the P.V
+ * product: |v| >= 65520 or infinite) and binary16-KV decode's q (binary16
+ * high part: |q| >= 65520).  This call orders itself after the work on
+ * `stream`, waits for it, takes (reads and clears) the word and returns
+ * NYION_OK, or NYION_ERR_RANGE with nyion_last_error() naming what
+ * overflowed since the last take.  The word is per device, not per stream:
+ * work on other streams of the device lands in the same word.  No
+ * counterpart in the reference, whose CPU path computes in f32 throughout
+ * (swamp-engine/src/ops.rs:170-278). */
+int nyion_take_status(nyion_stream_t stream);
+
 /* ------------------------------------------------------ decode attention */
 
 /* The ComputeGraph Attention node, executed now on `stream`.
@@ -80,13 +94,25 @@ const char* nyion_version(void);
  * token at q_pos = seq_len-1: out[h] = softmax(q[h].K[kv(h)]^T / sqrt(D)) V,
  * kv(h) = h / (n_heads/n_kv_heads).
  * Layout: d_q, d_out [n_heads][head_dim] f32; d_k, d_v [n_kv_heads][kv_stride][row].
- * d_scores: optional f32 scratch of n_heads*kv_stride floats (the node's
- * scores buffer, swamp-gpu/src/lib.rs:317); when given it holds the split-K
- * partial results, when NULL the node runs one partition per head group. */
+ * d_scores: optional f32 scratch of at least n_heads*seq_len floats (the
+ * node's scores buffer: ScratchBuffers::d_scores holds n_heads*window_size,
+ * swamp-gpu/src/lib.rs:317; the CUDA path n_heads*seq_len,
+ * fused_attention.cu:206), 256-byte aligned; when given, its first
+ * nyion_attention_node_scratch_bytes(...) bytes hold the split-K partial
+ * results, when NULL the node runs one workgroup per (kv head, group of up
+ * to 16 q heads). */
 int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v,
                          float* d_scores, float* d_out, uint32_t n_heads,
                          uint32_t n_kv_heads, uint32_t seq_len, uint32_t head_dim,
                          uint32_t kv_stride, int kv_dtype, nyion_stream_t stream);
+
+/* Bytes at the start of a node's d_scores buffer (n_heads*seq_len floats)
+ * that nyion_attention_node uses for its split-K partials and counters:
+ * never more than 4*n_heads*seq_len; 0 when the node runs whole segments.
+ * Host only (on a machine without a device it plans for 256 compute units).
+ * Same sizing rule as the node; no counterpart in the reference. */
+size_t nyion_attention_node_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq_len,
+                                          uint32_t head_dim);
 
 /* Project ABI names of the unlinked CUDA file, same arguments (f32 KV,
  * [n_kv_heads][kv_stride][head_dim]): gpu_attention_device
@@ -103,7 +129,7 @@ int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float
 /* The node captured once into a HIP graph and replayed (the project ABI of
  * fused_attention.cu:595-663: gpu_graph_create_attention,
  * gpu_graph_replay_attention, gpu_graph_destroy).  Every argument is fixed at
- * creation; d_scores (n_heads*kv_stride floats, 256-byte aligned, or NULL)
+ * creation; d_scores (n_heads*seq_len floats, 256-byte aligned, or NULL)
  * is the node's scratch as for nyion_attention_node, its counters cleared
  * inside the graph by a fill kernel.  create returns NULL on error (message
  * in nyion_last_error()); replay returns 0 / -1.  Replays of one graph on
@@ -509,8 +535,16 @@ const void*    nyion_kv_pool_cold_slot(void* pool, int slot);
 
 /* The HeterogeneousMemoryAllocator contract (swamp-tensors/src/hma.rs:5-9,
  * 30-36, 215-260): DeviceLocal allocations are carved from one hipMalloc
- * region (first-fit free list, 256-byte aligned), HostPinned from one
- * hipHostMalloc region, UnifiedMapped from hipMallocManaged. */
+ * region (first-fit free list, 256-byte aligned; a free merges with free
+ * neighbours), HostPinned from one hipHostMalloc region the same way,
+ * UnifiedMapped from hipMallocManaged per allocation.  A full region is
+ * NYION_ERR_OOM with a message.  Without a device (no HIP device, or not a
+ * gfx950) create still succeeds, as the reference's allocator without a
+ * DeviceAllocator (hma.rs:243-260): the host region is ordinary memory, and
+ * DeviceLocal and UnifiedMapped requests fall back to it, returned as
+ * HostPinned allocations with device_handle 0; nyion_hma_has_device tells
+ * the two modes apart.  upload/download copy at most the live allocation's
+ * size; reset frees every allocation at once. */
 enum nyion_mem_location {
     NYION_MEM_HOST_PINNED = 0,
     NYION_MEM_DEVICE_LOCAL = 1,
@@ -531,6 +565,7 @@ int   nyion_hma_upload(void* hma, const nyion_allocation* dst, const void* src, 
 int   nyion_hma_download(void* hma, void* dst, const nyion_allocation* src, size_t bytes);
 int   nyion_hma_reset(void* hma);
 int   nyion_hma_stats(void* hma, int location, size_t* used, size_t* capacity);
+int   nyion_hma_has_device(void* hma);
 void  nyion_hma_destroy(void* hma);
 
 /* ------------------------------------------------- swamp-kernels C-ABI */

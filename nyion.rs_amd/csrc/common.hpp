@@ -8,16 +8,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/nyion_hip.h"
+#include "host_status.hpp"
 
 namespace nyion {
 
 // ------------------------------------------------------------ errors
-
-int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-void clear_error();
 
 #define NYION_CHECK_HIP(expr)                                                                \
     do {                                                                                     \
@@ -32,6 +31,45 @@ int check_launch(const char* what);
 
 // True when the current device is a gfx950 (cached per device).
 int require_device();
+
+// ------------------------------------------------------------ per device
+
+constexpr int kMaxDevices = 64;
+
+// The current HIP device, or -1 (no device, or an id beyond kMaxDevices).
+int current_device();
+
+// A value computed once per device by `make` (an int > 0; `fallback` when
+// there is no device or `make` fails).  Concurrent first calls on one device
+// may both compute it; they store the same value.
+template <typename F>
+int per_device_value(std::atomic<int>* cache, F make, int fallback) {
+    const int dev = current_device();
+    if (dev < 0) return fallback;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    v = make();
+    if (v <= 0) return fallback;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+
+// Compute units of the current device (256 without one).
+int device_cu_count();
+
+// Range-status word of the current device: kernels OR a kRange* bit into it
+// when an input lies outside what a reduced-precision operand can hold;
+// nyion_take_status reads and clears it.  nullptr when there is no device.
+enum : unsigned { kRangePrefillV = 1u, kRangeDecodeQ = 2u };
+unsigned* device_status_word();
+
+// Sets `bit` in the status word from one lane when any lane of the
+// wavefront has `bad` (vector atomic on global memory).
+__device__ __forceinline__ void report_range(unsigned* status, bool bad, unsigned bit) {
+    const unsigned long long any = __ballot(bad);
+    if (any && status && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(any))
+        __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 static inline bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
 static inline int ilog2(long long x) {

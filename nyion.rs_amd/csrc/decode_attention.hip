@@ -97,6 +97,7 @@ struct DecodeArgs {
     int mode;
     int max_len;    // host bound on attended positions per sequence
     float scale_log2;  // scale * log2(e)
+    unsigned* status;  // the device's range-status word (binary16 q overflow)
 };
 
 // Sequences per launch: the per-sequence tile prefix sums live in LDS.
@@ -828,7 +829,12 @@ void decode_kernel(DecodeArgs a) {
             for (int cc = 0; cc < NC; cc++) qv[cc] = ok ? qrow[qk_dim<D, KVT>(cc, kq)] : 0.f;
             if constexpr (KVT == NYION_KV_F16) {
                 // words 4x, 4x+1: the four values as binary16; 4x+2, 4x+3: the
-                // binary16 residuals (q within the binary16 range)
+                // binary16 residuals.  |q| >= 65520 rounds the high part to
+                // infinity: reported through the status word.
+                bool big = false;
+#pragma unroll
+                for (int cc = 0; cc < NC; cc++) big |= fabsf(qv[cc]) >= 65520.f;
+                report_range(a.status, big, kRangeDecodeQ);
 #pragma unroll
                 for (int x = 0; x < D / 16; x++) {
                     const float* v = qv + 4 * x;
@@ -1068,7 +1074,10 @@ constexpr int kDefaultWgTiles = 16;
 constexpr int kSmallWgTiles = 8;
 constexpr int kMinWgTiles = 4;
 constexpr int kMaxGrid = 2048;  // workgroups per launch (partial slots are sized for it)
-static int g_wg_tiles_override = 0;
+// Tuning override of the tiles per workgroup (0 = default), set by
+// nyion_set_decode_partition_tokens for the whole process and read once per
+// call; an atomic, so a concurrent change takes effect at a call boundary.
+static std::atomic<int> g_wg_tiles_override{0};
 
 struct DecodePlan {
     DecodeArgs a;      // batch field: set per launch
@@ -1121,6 +1130,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
     a.max_len = max_main;
+    a.status = device_status_word();
     const long long units = (long long)n_kv_heads * a.n_hg;
     // aligned: main tiles <= max_main/16 + 2, globals (<= 128) <= 8 tiles;
     // gather: the globals are part of the list
@@ -1166,41 +1176,29 @@ static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes) {
     return NYION_OK;
 }
 
-// Workgroups of one kernel instance resident on the whole device.
+// Workgroups of one kernel instance resident on the whole device (per
+// device, computed on first use there).
 template <int D, int KVT, bool AL, bool TR>
 static int resident_capacity() {
-    static int cap = 0;
-    if (cap == 0) {
-        int per_cu = 0, cus = 0, dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL, TR>, 256,
-                                                         0) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-            (void)hipGetLastError();
-            return 256;
-        }
-        cap = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-    }
-    return cap;
-}
-
-static int cu_count() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0, c = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) {
-            (void)hipGetLastError();
-            return 256;
-        }
-        n = c;
-    }
-    return n;
+    static std::atomic<int> cache[kMaxDevices];
+    return per_device_value(
+        cache,
+        [] {
+            int per_cu = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL, TR>,
+                                                             256, 0) != hipSuccess) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            return (per_cu > 0 ? per_cu : 1) * device_cu_count();
+        },
+        256);
 }
 
 static int wg_tiles_for(long long total_tiles) {
-    if (g_wg_tiles_override > 0) return g_wg_tiles_override;
-    const long long per_cu = total_tiles / cu_count();
+    const int ov = g_wg_tiles_override.load(std::memory_order_relaxed);
+    if (ov > 0) return ov;
+    const long long per_cu = total_tiles / device_cu_count();
     return per_cu < kSmallWgTiles ? kSmallWgTiles : per_cu > kDefaultWgTiles ? kDefaultWgTiles : (int)per_cu;
 }
 
@@ -1288,7 +1286,7 @@ int nyion_set_decode_partition_tokens(int tokens) {
         return set_error(NYION_ERR_INVALID,
                          "partition tokens %d: power of two in [%d, 4096] or 0", tokens,
                          16 * kMinWgTiles);
-    g_wg_tiles_override = tokens / 16;
+    g_wg_tiles_override.store(tokens / 16, std::memory_order_relaxed);
     return NYION_OK;
 }
 
@@ -1296,7 +1294,8 @@ int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, i
     if (batch <= 0 || n_kv_heads <= 0 || max_len <= 0) return 0;
     const long long tiles = (long long)batch * n_kv_heads * (max_len / 16 + 2);
     int cap = kMaxGrid;
-    int wg_tiles = g_wg_tiles_override > 0 ? g_wg_tiles_override : kDefaultWgTiles;
+    const int ov = g_wg_tiles_override.load(std::memory_order_relaxed);
+    int wg_tiles = ov > 0 ? ov : kDefaultWgTiles;
     if (require_device() == NYION_OK) {
         cap = head_dim == 128 ? resident_capacity<128, NYION_KV_F32, true, false>()
                               : resident_capacity<64, NYION_KV_F32, true, false>();
@@ -1415,6 +1414,31 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
     return check_launch("decode importance");
 }
 
+// Plan of the attention node over scratch_bytes of its scores buffer.  The
+// host knows the length: a segment is exactly ceil(seq_len/16) tiles from
+// position 0.  When one workgroup's share covers that, the launch runs whole
+// segments (grid = units): no partials, no counters, and so no
+// counter-clearing launch.  Otherwise the scores buffer holds the split-K
+// partials when it is large enough (halving the grid until the partials fit
+// it); failing that, one workgroup covers each head group.
+static int node_plan(DecodePlan& pl, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq_len,
+                     uint32_t head_dim, int kv_dtype, size_t scratch_bytes) {
+    int rc;
+    if ((rc = plan_common(pl, 1, (int)n_heads, (int)n_kv_heads, (int)head_dim, kv_dtype, (int)seq_len,
+                          false, true, 0.f)) != NYION_OK)
+        return rc;
+    DecodeArgs& a = pl.a;
+    pl.tiles_max = (int)((seq_len + 15) / 16);
+    if (pl.tiles_max <= wg_tiles_for((long long)a.n_kv_heads * a.n_hg * pl.tiles_max)) pl.ws_bytes = 0;
+    const int units = a.n_kv_heads * a.n_hg;
+    while (pl.ws_bytes > scratch_bytes && pl.grid_bound > units) {
+        pl.grid_bound = pl.grid_bound / 2 > units ? pl.grid_bound / 2 : units;
+        pl.ws_bytes = ws_layout(pl.grid_bound + units, units, (int)head_dim, nullptr, nullptr);
+    }
+    if (pl.ws_bytes > scratch_bytes) pl.ws_bytes = 0;  // whole segments: grid = units
+    return NYION_OK;
+}
+
 extern "C" {
 
 int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
@@ -1518,28 +1542,14 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
                          seq_len, kv_stride);
     if (n_heads > 4096 || n_kv_heads == 0)
         return set_error(NYION_ERR_INVALID, "attention node: head counts");
-    DecodePlan pl;
-    if ((rc = plan_common(pl, 1, (int)n_heads, (int)n_kv_heads, (int)head_dim, kv_dtype,
-                          (int)seq_len, false, true, 0.f)) != NYION_OK)
-        return rc;
-    // The host knows the length: a segment is exactly ceil(seq_len/16) tiles
-    // from position 0.  When one workgroup's share covers that, the launch
-    // runs whole segments (grid = units): no partials, no counters, and so
-    // no counter-clearing launch.
-    DecodeArgs& a = pl.a;
-    pl.tiles_max = (int)((seq_len + 15) / 16);
-    if (pl.tiles_max <= wg_tiles_for((long long)a.n_kv_heads * a.n_hg * pl.tiles_max)) pl.ws_bytes = 0;
-    // Otherwise the node's scores buffer (n_heads*kv_stride floats, the
-    // reference's ScratchBuffers::d_scores) holds the split-K partials when
-    // it is large enough; failing that, one workgroup covers each head group.
+    // the node's scores buffer: n_heads*seq_len floats, the least any
+    // reference caller provides
     const size_t scores_bytes =
-        d_scores && aligned(d_scores, 256) ? (size_t)n_heads * kv_stride * sizeof(float) : 0;
-    const int units = a.n_kv_heads * a.n_hg;
-    while (pl.ws_bytes > scores_bytes && pl.grid_bound > units) {
-        pl.grid_bound = pl.grid_bound / 2 > units ? pl.grid_bound / 2 : units;
-        pl.ws_bytes = ws_layout(pl.grid_bound + units, units, (int)head_dim, nullptr, nullptr);
-    }
-    if (pl.ws_bytes > scores_bytes) pl.ws_bytes = 0;  // whole segments: grid = units
+        d_scores && aligned(d_scores, 256) ? (size_t)n_heads * seq_len * sizeof(float) : 0;
+    DecodePlan pl;
+    if ((rc = node_plan(pl, n_heads, n_kv_heads, seq_len, head_dim, kv_dtype, scores_bytes)) != NYION_OK)
+        return rc;
+    DecodeArgs& a = pl.a;
     if ((rc = attach_workspace(pl, d_scores, scores_bytes)) != NYION_OK) return rc;
     const long long row = row_elems((int)head_dim, kv_dtype);
     a.q = d_q;
@@ -1580,6 +1590,15 @@ int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* 
                          int kv_stride) {
     return gpu_attention_streamed(d_q, d_k_cache, d_v_cache, d_output, n_heads, n_kv_heads, seq_len,
                                   head_dim, kv_stride, nullptr);
+}
+
+size_t nyion_attention_node_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq_len,
+                                          uint32_t head_dim) {
+    DecodePlan pl;
+    const size_t avail = (size_t)n_heads * seq_len * sizeof(float);
+    const int rc = node_plan(pl, n_heads, n_kv_heads, seq_len, head_dim, NYION_KV_F32, avail);
+    clear_error();
+    return rc == NYION_OK ? pl.ws_bytes : 0;
 }
 
 }  // extern "C"

@@ -394,22 +394,23 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
     }
 }
 
-// Resident workgroups of one instantiation on this device.
+// Resident workgroups of one instantiation on the current device (per
+// device, computed on first use there).
 template <class F, int R, int B, int P>
 static int gemv_capacity() {
-    static int cap = 0;
-    if (cap == 0) {
-        int per_cu = 0, cus = 0, dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_kquant_kernel<F, R, B, P>, 64 * P,
-                                                         0) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-            (void)hipGetLastError();
-            return 1024;
-        }
-        cap = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-    }
-    return cap;
+    static std::atomic<int> cache[kMaxDevices];
+    return per_device_value(
+        cache,
+        [] {
+            int per_cu = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_kquant_kernel<F, R, B, P>,
+                                                             64 * P, 0) != hipSuccess) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            return (per_cu > 0 ? per_cu : 1) * device_cu_count();
+        },
+        1024);
 }
 
 template <class F, int R, int B, int P>

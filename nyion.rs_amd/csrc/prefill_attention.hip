@@ -70,6 +70,7 @@ struct PrefillArgs {
     int n_items;   // kv heads x head subsets x row-block groups
     int causal;
     float scale_log2;
+    unsigned* status;  // the device's range-status word (V outside binary16)
 };
 
 constexpr int BN = 64;  // keys per tile
@@ -220,8 +221,11 @@ __device__ __forceinline__ void stage_store_k(const KStage<D>& st, unsigned char
     }
 }
 
+// vmax: running max of |v| over the values this thread has staged (a V value
+// of magnitude >= 65520 becomes infinity in binary16).
 template <int D>
-__device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char* vslot, int tid) {
+__device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char* vslot, int tid,
+                                              float& vmax) {
     using L = PrefillLds<D>;
 #pragma unroll
     for (int u = 0; u < VStage<D>::UNITS; u++) {
@@ -237,6 +241,7 @@ __device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char
             const uint32_t x0 = st.v0[u][e >> 1], x1 = st.v1[u][e >> 1];
             const float lo = __uint_as_float((e & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
             const float hi = __uint_as_float((e & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
+            vmax = fmaxf(vmax, fmaxf(fabsf(lo), fabsf(hi)));
             *(uint32_t*)(vslot + (8 * dc + e) * L::VROW + 2 * col) = pack_f16x2(lo, hi);
         }
     }
@@ -309,6 +314,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     unsigned char* const vslot0 = lds + 3 * L::KBYTES;
     KStage<D> kst;
     VStage<D> vst;
+    float vmax = 0.f;
 
     // S^T of 32-key half kb of the tile in K slot `ks` (K rows kb*32 + j,
     // chunk 2s + h)
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0, tid);
     load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0, tid);
     stage_store_k<D>(kst, kslot0, tid);
-    stage_store_v<D>(vst, vslot0, tid);
+    stage_store_v<D>(vst, vslot0, tid, vmax);
     if (n_tiles > 1) {
         load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + BN, tid);
         stage_store_k<D>(kst, kslot0 + L::KBYTES, tid);
@@ -439,7 +445,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         consume_half(s1, vs, 1);
         // a slot past the last tile is written and never read
         stage_store_k<D>(kst, kslot(it + 2), tid);
-        stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid);
+        stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid, vmax);
         if (it + 3 < n_tiles) load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt + 3 * BN, tid);
         if (it + 2 < n_tiles) load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt + 2 * BN, tid);
         __syncthreads();
@@ -460,6 +466,8 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         consume_half(s0, vs, 0);
         consume_half(s1, vs, 1);
     }
+
+    report_range(a.status, vmax >= 65520.f, kRangePrefillV);
 
     // epilogue: divide by the row sums and store
     const float lt = lrun + __shfl_xor(lrun, 32);
@@ -536,6 +544,7 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     a.causal = causal ? 1 : 0;
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
+    a.status = device_status_word();
     dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
     if (head_dim == 128)

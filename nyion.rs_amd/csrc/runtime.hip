@@ -7,14 +7,20 @@
 // hipMalloc region carved first-fit with 256-byte alignment (the paged KV
 // pools and decode workspaces of one model live in it), HostPinned from one
 // hipHostMalloc region, UnifiedMapped from hipMallocManaged per allocation.
+// Without a device the arena behaves as the reference's allocator with no
+// DeviceAllocator (hma.rs:243-260): the host region is ordinary memory and
+// DeviceLocal / UnifiedMapped requests are served from it as host
+// allocations (location HostPinned, no device handle).
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
 #include <mutex>
 #include <string>
 
+#include "arena.hpp"
 #include "common.hpp"
 
 namespace nyion {
@@ -70,72 +76,76 @@ int require_device() {
                           dev, prop.gcnArchName);
 }
 
-// ------------------------------------------------------------- arena
+// ------------------------------------------------------------- per device
 
-// First-fit free-list over one contiguous region.
-struct Region {
-    char* base = nullptr;
-    size_t cap = 0;
-    size_t used = 0;
-    std::map<size_t, size_t> free_;  // offset -> size
-    std::map<size_t, size_t> live;   // offset -> size
-
-    void init(void* b, size_t c) {
-        base = (char*)b;
-        cap = c;
-        used = 0;
-        free_.clear();
-        live.clear();
-        if (c) free_[0] = c;
+int current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
     }
-    void* alloc(size_t size) {
-        size = (size + 255) & ~(size_t)255;
-        if (size == 0) size = 256;
-        for (auto it = free_.begin(); it != free_.end(); ++it) {
-            if (it->second >= size) {
-                size_t off = it->first, rem = it->second - size;
-                free_.erase(it);
-                if (rem) free_[off + size] = rem;
-                live[off] = size;
-                used += size;
-                return base + off;
+    return dev >= 0 && dev < kMaxDevices ? dev : -1;
+}
+
+int device_cu_count() {
+    static std::atomic<int> cache[kMaxDevices];
+    return per_device_value(
+        cache,
+        [] {
+            int c = 0;
+            if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, current_device()) !=
+                hipSuccess) {
+                (void)hipGetLastError();
+                return 0;
             }
-        }
+            return c;
+        },
+        256);
+}
+
+// Word 0: the sticky range flags (kRange* bits); word 1: where
+// status_take_kernel leaves what it took.  Each device holds its own copy.
+__device__ unsigned g_status_words[2];
+
+unsigned* device_status_word() {
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    uintptr_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v) return (unsigned*)v;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_status_words)) != hipSuccess || !p) {
+        (void)hipGetLastError();
         return nullptr;
     }
-    bool release(void* p) {
-        if (!base || (char*)p < base || (char*)p >= base + cap) return false;
-        size_t off = (size_t)((char*)p - base);
-        auto it = live.find(off);
-        if (it == live.end()) return false;
-        size_t size = it->second;
-        live.erase(it);
-        used -= size;
-        auto nx = free_.lower_bound(off);
-        if (nx != free_.end() && nx->first == off + size) {
-            size += nx->second;
-            free_.erase(nx);
-        }
-        auto pv = free_.lower_bound(off);
-        if (pv != free_.begin()) {
-            --pv;
-            if (pv->first + pv->second == off) {
-                pv->second += size;
-                return true;
-            }
-        }
-        free_[off] = size;
-        return true;
-    }
-    void reset() { init(base, cap); }
-};
+    cache[dev].store((uintptr_t)p, std::memory_order_relaxed);
+    return (unsigned*)p;
+}
+
+__global__ void status_take_kernel(unsigned* w) {
+    w[1] = __hip_atomic_exchange(&w[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------- arena
 
 struct Hma {
     std::mutex mu;
     int device = 0;
+    bool no_device = false;  // host-only arena: device requests fall back to host
     Region dev, host;
     std::map<void*, size_t> managed;
 };
+
+// Bytes of the live allocation `a` names (0 if it names none).
+static size_t live_bytes(Hma* h, const nyion_allocation* a) {
+    if (a->location == NYION_MEM_DEVICE_LOCAL) return h->dev.live_size(a->ptr);
+    if (a->location == NYION_MEM_HOST_PINNED) return h->host.live_size(a->ptr);
+    if (a->location == NYION_MEM_UNIFIED_MAPPED) {
+        auto it = h->managed.find(a->ptr);
+        return it == h->managed.end() ? 0 : it->second;
+    }
+    return 0;
+}
 
 }  // namespace nyion
 
@@ -171,14 +181,38 @@ int nyion_sync(void) {
     return NYION_OK;
 }
 
+int nyion_take_status(nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    unsigned* w = device_status_word();
+    if (!w) return set_error(NYION_ERR_LAUNCH, "status word of the current device is unavailable");
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(status_take_kernel, dim3(1), dim3(1), 0, st, w);
+    if ((rc = check_launch("status")) != NYION_OK) return rc;
+    unsigned got = 0;
+    NYION_CHECK_HIP(hipMemcpyAsync(&got, w + 1, sizeof got, hipMemcpyDeviceToHost, st));
+    NYION_CHECK_HIP(hipStreamSynchronize(st));
+    if (!got) return NYION_OK;
+    std::string msg;
+    if (got & kRangePrefillV)
+        msg += "prefill: a V value of magnitude >= 65520 (or infinite) does not fit the binary16 "
+               "operand of the P.V product; rows attending to it are not valid. ";
+    if (got & kRangeDecodeQ)
+        msg += "binary16-KV decode: a q value of magnitude >= 65520 overflows the binary16 high "
+               "part of q; the heads holding it are not valid. ";
+    return set_error(NYION_ERR_RANGE, "%s", msg.c_str());
+}
+
 void* nyion_hma_create(size_t device_bytes, size_t host_pinned_bytes) {
     clear_error();
-    if (device_bytes && require_device() != NYION_OK) return nullptr;
     Hma* h = new Hma();
-    (void)hipGetDevice(&h->device);
+    h->no_device = require_device() != NYION_OK;
+    clear_error();
+    if (!h->no_device) (void)hipGetDevice(&h->device);
     void* d = nullptr;
     void* p = nullptr;
-    if (device_bytes) {
+    if (device_bytes && !h->no_device) {
         if (hipMalloc(&d, device_bytes) != hipSuccess) {
             (void)hipGetLastError();
             set_error(NYION_ERR_OOM, "hma: hipMalloc(%zu) failed", device_bytes);
@@ -187,15 +221,19 @@ void* nyion_hma_create(size_t device_bytes, size_t host_pinned_bytes) {
         }
     }
     if (host_pinned_bytes) {
-        if (hipHostMalloc(&p, host_pinned_bytes, hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
+        const bool ok = h->no_device
+                            ? (p = aligned_alloc(Region::kAlign, (host_pinned_bytes + Region::kAlign - 1) &
+                                                                     ~(Region::kAlign - 1))) != nullptr
+                            : hipHostMalloc(&p, host_pinned_bytes, hipHostMallocDefault) == hipSuccess;
+        if (!ok) {
+            if (!h->no_device) (void)hipGetLastError();
             if (d) (void)hipFree(d);
-            set_error(NYION_ERR_OOM, "hma: hipHostMalloc(%zu) failed", host_pinned_bytes);
+            set_error(NYION_ERR_OOM, "hma: host region of %zu bytes: allocation failed", host_pinned_bytes);
             delete h;
             return nullptr;
         }
     }
-    h->dev.init(d, device_bytes);
+    h->dev.init(d, h->no_device ? 0 : device_bytes);
     h->host.init(p, host_pinned_bytes);
     return h;
 }
@@ -205,7 +243,12 @@ int nyion_hma_alloc(void* hma, size_t size, int location, nyion_allocation* out)
     Hma* h = (Hma*)hma;
     if (!h || !out) return set_error(NYION_ERR_INVALID, "hma alloc: null handle/out");
     memset(out, 0, sizeof *out);
+    if (location != NYION_MEM_DEVICE_LOCAL && location != NYION_MEM_HOST_PINNED &&
+        location != NYION_MEM_UNIFIED_MAPPED)
+        return set_error(NYION_ERR_INVALID, "hma alloc: location %d", location);
     std::lock_guard<std::mutex> g(h->mu);
+    // no device: device requests are served by the host region (hma.rs:249-256)
+    if (h->no_device) location = NYION_MEM_HOST_PINNED;
     void* p = nullptr;
     switch (location) {
         case NYION_MEM_DEVICE_LOCAL:
@@ -216,9 +259,10 @@ int nyion_hma_alloc(void* hma, size_t size, int location, nyion_allocation* out)
             break;
         case NYION_MEM_HOST_PINNED:
             p = h->host.alloc(size);
-            if (!p) return set_error(NYION_ERR_OOM, "hma: pinned arena exhausted (%zu requested)", size);
+            if (!p) return set_error(NYION_ERR_OOM, "hma: host arena exhausted (%zu requested, %zu/%zu used)",
+                                     size, h->host.used, h->host.cap);
             break;
-        case NYION_MEM_UNIFIED_MAPPED:
+        default:  // NYION_MEM_UNIFIED_MAPPED
             if (hipMallocManaged(&p, size ? size : 1) != hipSuccess) {
                 (void)hipGetLastError();
                 return set_error(NYION_ERR_OOM, "hma: hipMallocManaged(%zu) failed", size);
@@ -226,8 +270,6 @@ int nyion_hma_alloc(void* hma, size_t size, int location, nyion_allocation* out)
             h->managed[p] = size;
             out->device_handle = (uint64_t)(uintptr_t)p;
             break;
-        default:
-            return set_error(NYION_ERR_INVALID, "hma alloc: location %d", location);
     }
     out->ptr = p;
     out->size = size;
@@ -255,28 +297,37 @@ int nyion_hma_free(void* hma, const nyion_allocation* a) {
     return ok ? NYION_OK : set_error(NYION_ERR_INVALID, "hma free: %p is not a live allocation", a->ptr);
 }
 
-int nyion_hma_upload(void* hma, const nyion_allocation* dst, const void* src, size_t bytes) {
+// Host <-> allocation copies; host-region allocations are plain memcpy, the
+// others synchronous hipMemcpy.  `bytes` may not exceed the live allocation.
+static int hma_copy(void* hma, void* host, const nyion_allocation* a, size_t bytes, bool up) {
     clear_error();
-    if (!hma || !dst || !src || !dst->ptr) return set_error(NYION_ERR_INVALID, "hma upload: null");
-    if (bytes > dst->size) return set_error(NYION_ERR_INVALID, "hma upload: %zu > allocation %zu", bytes, dst->size);
-    if (dst->location == NYION_MEM_HOST_PINNED) {
-        memcpy(dst->ptr, src, bytes);
+    Hma* h = (Hma*)hma;
+    const char* what = up ? "hma upload" : "hma download";
+    if (!h || !a || !host || !a->ptr) return set_error(NYION_ERR_INVALID, "%s: null argument", what);
+    size_t live;
+    {
+        std::lock_guard<std::mutex> g(h->mu);
+        live = live_bytes(h, a);
+    }
+    if (live == 0) return set_error(NYION_ERR_INVALID, "%s: %p is not a live allocation", what, a->ptr);
+    if (bytes > a->size || bytes > live)
+        return set_error(NYION_ERR_INVALID, "%s: %zu bytes > allocation of %zu", what, bytes, a->size);
+    if (a->location == NYION_MEM_HOST_PINNED) {
+        if (up) memcpy(a->ptr, host, bytes);
+        else memcpy(host, a->ptr, bytes);
         return NYION_OK;
     }
-    NYION_CHECK_HIP(hipMemcpy(dst->ptr, src, bytes, hipMemcpyHostToDevice));
+    if (up) NYION_CHECK_HIP(hipMemcpy(a->ptr, host, bytes, hipMemcpyHostToDevice));
+    else NYION_CHECK_HIP(hipMemcpy(host, a->ptr, bytes, hipMemcpyDeviceToHost));
     return NYION_OK;
 }
 
+int nyion_hma_upload(void* hma, const nyion_allocation* dst, const void* src, size_t bytes) {
+    return hma_copy(hma, (void*)src, dst, bytes, true);
+}
+
 int nyion_hma_download(void* hma, void* dst, const nyion_allocation* src, size_t bytes) {
-    clear_error();
-    if (!hma || !dst || !src || !src->ptr) return set_error(NYION_ERR_INVALID, "hma download: null");
-    if (bytes > src->size) return set_error(NYION_ERR_INVALID, "hma download: %zu > allocation %zu", bytes, src->size);
-    if (src->location == NYION_MEM_HOST_PINNED) {
-        memcpy(dst, src->ptr, bytes);
-        return NYION_OK;
-    }
-    NYION_CHECK_HIP(hipMemcpy(dst, src->ptr, bytes, hipMemcpyDeviceToHost));
-    return NYION_OK;
+    return hma_copy(hma, dst, src, bytes, false);
 }
 
 int nyion_hma_reset(void* hma) {
@@ -306,11 +357,19 @@ int nyion_hma_stats(void* hma, int location, size_t* used, size_t* capacity) {
     return NYION_OK;
 }
 
+int nyion_hma_has_device(void* hma) {
+    Hma* h = (Hma*)hma;
+    return h && !h->no_device ? 1 : 0;
+}
+
 void nyion_hma_destroy(void* hma) {
     Hma* h = (Hma*)hma;
     if (!h) return;
     if (h->dev.base) (void)hipFree(h->dev.base);
-    if (h->host.base) (void)hipHostFree(h->host.base);
+    if (h->host.base) {
+        if (h->no_device) free(h->host.base);
+        else (void)hipHostFree(h->host.base);
+    }
     for (auto& kv : h->managed) (void)hipFree(kv.first);
     delete h;
 }

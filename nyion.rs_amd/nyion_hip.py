@@ -28,6 +28,7 @@ ERR_NO_DEVICE = -3
 ERR_OOM = -4
 ERR_LAUNCH = -5
 ERR_WORKSPACE = -6
+ERR_RANGE = -7
 
 
 class NyionError(RuntimeError):
@@ -69,6 +70,8 @@ SIGNATURES = {
     "nyion_device_count": (i32, []),
     "nyion_sync": (i32, []),
     "nyion_version": (C.c_char_p, []),
+    "nyion_take_status": (i32, [vp]),
+    "nyion_attention_node_scratch_bytes": (sz, [u32, u32, u32, u32]),
     "nyion_attention_node": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, i32, vp]),
     "gpu_attention_device": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32]),
     "gpu_attention_streamed": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
@@ -143,6 +146,7 @@ SIGNATURES = {
     "nyion_hma_download": (i32, [vp, vp, C.POINTER(Allocation), sz]),
     "nyion_hma_reset": (i32, [vp]),
     "nyion_hma_stats": (i32, [vp, i32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "nyion_hma_has_device": (i32, [vp]),
     "nyion_hma_destroy": (None, [vp]),
     "mojo_softmax_padic": (None, [vp, vp, i32, f32]),
     "mojo_stokes_init": (vp, [i32]),
@@ -201,6 +205,19 @@ def stream_handle(stream=None) -> int | None:
 
 def init(device: int = 0) -> None:
     check(load().nyion_init(device), "nyion_init")
+
+
+def take_status(stream=None) -> tuple[int, str]:
+    """Waits for `stream`, takes the device's range-status word: (0, "") or
+    (ERR_RANGE, message)."""
+    rc = load().nyion_take_status(stream_handle(stream))
+    if rc not in (OK, ERR_RANGE):
+        check(rc, "nyion_take_status")
+    return rc, ("" if rc == OK else last_error())
+
+
+def node_scratch_bytes(n_heads, n_kv_heads, seq_len, head_dim) -> int:
+    return int(load().nyion_attention_node_scratch_bytes(n_heads, n_kv_heads, seq_len, head_dim))
 
 
 # ----------------------------------------------------------------------------
@@ -691,4 +708,65 @@ class KvPool:
         try:
             self.close()
         except Exception:  # interpreter shutdown: the library may be gone
+            pass
+
+
+# ----------------------------------------------------------------------------
+# HMA arena
+# ----------------------------------------------------------------------------
+
+class Hma:
+    """The HeterogeneousMemoryAllocator arena (nyion_hma_*).  alloc returns an
+    Allocation; upload/download take bytes-like host data."""
+
+    def __init__(self, device_bytes: int, host_bytes: int):
+        self.h = load().nyion_hma_create(device_bytes, host_bytes)
+        if not self.h:
+            raise NyionError(ERR_OOM, f"nyion_hma_create: {last_error()}")
+
+    @property
+    def has_device(self) -> bool:
+        return bool(load().nyion_hma_has_device(self.h))
+
+    def alloc(self, size: int, location: int) -> Allocation:
+        a = Allocation()
+        check(load().nyion_hma_alloc(self.h, size, location, C.byref(a)), "nyion_hma_alloc")
+        return a
+
+    def try_alloc(self, size: int, location: int):
+        """(rc, Allocation) without raising."""
+        a = Allocation()
+        return load().nyion_hma_alloc(self.h, size, location, C.byref(a)), a
+
+    def free(self, a: Allocation) -> int:
+        return load().nyion_hma_free(self.h, C.byref(a))
+
+    def upload(self, a: Allocation, data: bytes) -> int:
+        buf = C.create_string_buffer(bytes(data), len(data))
+        return load().nyion_hma_upload(self.h, C.byref(a), buf, len(data))
+
+    def download(self, a: Allocation, nbytes: int):
+        """(rc, bytes)"""
+        buf = C.create_string_buffer(nbytes)
+        rc = load().nyion_hma_download(self.h, buf, C.byref(a), nbytes)
+        return rc, buf.raw
+
+    def reset(self) -> int:
+        return load().nyion_hma_reset(self.h)
+
+    def stats(self, location: int):
+        used, cap = C.c_size_t(), C.c_size_t()
+        check(load().nyion_hma_stats(self.h, location, C.byref(used), C.byref(cap)),
+              "nyion_hma_stats")
+        return used.value, cap.value
+
+    def close(self):
+        if self.h:
+            load().nyion_hma_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
             pass

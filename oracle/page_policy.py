@@ -21,11 +21,15 @@ Followed line by line (paths relative to the reference repository root):
                     a cold page, then touch
   cache.rs:549-553  ensure_pages_hot: ensure_page over a range in order
   cache.rs:563-581  record_importance / reset_entropy
-Two points are this build's own and are restated, not followed:
+Three points are this build's own and are restated, not followed:
   * which physical block a hot page occupies (the reference allocates fresh
     host memory): blocks 0..hot_limit-1 on a LIFO free list, 0 first;
   * a full cold tier is an error (the reference overwrites the slot at its
-    cursor, losing that page); so is a range larger than the hot limit.
+    cursor, losing that page); so is a range larger than the hot limit;
+  * while ensure() makes a range hot, the range's pages are not eviction
+    candidates: the scan takes the first eight pages from the LRU tail that
+    lie outside the range (the reference would evict a page of the range
+    it is making hot and then read a missing page).
 The reference's own tiered tests (cache.rs:951-998) stay inside one page and
 do not exercise eviction; the tests pin this restatement with hand-worked
 cases instead.
@@ -53,6 +57,7 @@ class PagePolicy:
         self.free = list(range(hot_limit - 1, -1, -1))
         self.n_created = 0
         self.hot_count = 0
+        self.protected = range(0)
 
     # cache.rs:277-309
     def _create(self, ev):
@@ -70,7 +75,9 @@ class PagePolicy:
     def _evict_one(self, ev):
         if not self.lru:
             return
-        cands = list(reversed(self.lru))[:8]  # tail first
+        cands = [p for p in reversed(self.lru) if p not in self.protected][:8]  # tail first
+        if not cands:
+            raise PolicyError("every hot page is in the range being made hot")
         best = cands[0]
         for c in cands[1:]:
             if self.importance[c] < self.importance[best]:
@@ -127,11 +134,14 @@ class PagePolicy:
         ev = []
         if first > last or last - first + 1 > self.hot_limit:
             return False, ev
+        self.protected = range(first, last + 1)
         try:
             for q in range(first, last + 1):
                 self._ensure_page(q, ev)
         except PolicyError:
             return False, ev
+        finally:
+            self.protected = range(0)
         return True, ev
 
     # cache.rs:563-571

@@ -66,3 +66,20 @@ def test_workspace_sizes_are_host_only():
     # a single short sequence runs in one partition per head group: no workspace
     assert L.nyion_paged_decode_workspace_size(1, 32, 4, 64, 16, 0, 0) == 0
     assert L.nyion_paged_decode_workspace_size(1, 30, 4, 64, 16, 0, 0) == 0  # invalid heads
+
+
+def test_node_scratch_fits_the_reference_scores_buffer():
+    """The node uses at most the n_heads*seq_len floats any reference caller
+    gives its scores buffer (fused_attention.cu:206; ScratchBuffers
+    n_heads*window_size, lib.rs:317): planned on the host for a spread of
+    shapes, including lengths where split-K pays."""
+    L = nyion_hip.load()
+    seen_split = False
+    for hq, hkv in ((32, 4), (32, 8), (8, 8), (64, 4), (40, 8), (4, 1)):
+        for d in (64, 128):
+            for n in (1, 15, 16, 17, 128, 129, 1000, 2048, 4096, 4097, 16384, 65536, 131071):
+                used = nyion_hip.node_scratch_bytes(hq, hkv, n, d)
+                assert used <= 4 * hq * n, (hq, hkv, d, n, used)
+                seen_split |= used > 0
+    assert seen_split
+    assert L.nyion_attention_node_scratch_bytes(30, 4, 128, 64) == 0  # invalid heads

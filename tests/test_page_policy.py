@@ -89,6 +89,27 @@ def test_importance_rules():
     assert all(p.state(q)[2] == 0.0 for q in range(3))
 
 
+def test_range_pages_are_not_evicted_while_made_hot():
+    """Limit 4: ensure(0, 3), page 0 made important, then ensure(4, 7).  Each
+    new page of 4..7 evicts the least important unprotected page; creating
+    page 7 finds only page 0 (5.0) outside the range (4, 5, 6 are
+    protected), so page 0 goes and all of 4..7 end hot.  Without the
+    protection page 4 (importance 0) would be evicted by its own range."""
+    want_ev = [(E, 1, 1, 0), (C, 4, 1, -1), (E, 2, 2, 1), (C, 5, 2, -1),
+               (E, 3, 3, 2), (C, 6, 3, -1), (E, 0, 0, 3), (C, 7, 0, -1)]
+    p = nh.PagePolicy(4, 8, 16)
+    p.ensure(0, 3)
+    p.record(0, 5.0)
+    assert p.ensure(4, 7) == (0, want_ev)
+    assert all(p.state(q)[0] == nh.PAGE_HOT for q in range(4, 8))
+    assert p.lru() == [7, 6, 5, 4]
+    r = ref.PagePolicy(4, 8, 16)
+    r.ensure(0, 3)
+    r.record(0, 5.0)
+    assert r.ensure(4, 7) == (True, want_ev)
+    assert r.lru == [7, 6, 5, 4]
+
+
 @pytest.mark.parametrize("hot,cold,pages,seed", [(1, 3, 8, 0), (2, 2, 12, 1), (4, 8, 32, 2),
                                                  (8, 64, 64, 3), (10, 5, 40, 4), (16, 200, 200, 5)])
 def test_random_sequences_match_restatement(hot, cold, pages, seed):
