@@ -190,6 +190,28 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
                                  int max_ctx, float scale, float* d_out, void* d_workspace,
                                  size_t workspace_bytes, nyion_stream_t stream);
 
+/* No counterpart in the reference: nyion_paged_decode_attention for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  Same arguments and
+ * results without the workspace: the split-K partials and arrival counters
+ * live in a device array the library owns, NYION_DECODE_SCRATCH_BYTES per
+ * device, held until the process ends (its device address is looked up by
+ * nyion_init, or by the first call on a device).  The call allocates
+ * nothing; it clears the array's counters with a fill kernel on `stream`
+ * before the decode.  A call whose workspace
+ * (nyion_paged_decode_workspace_size) exceeds the array returns
+ * NYION_ERR_WORKSPACE.  All calls on one device share the array, which keeps
+ * the last call's contents: calls that overlap in time on one device (other
+ * streams or threads) race and must be serialised by the caller. */
+#define NYION_DECODE_SCRATCH_BYTES (32u << 20)
+int nyion_paged_decode_attention_noalloc(const float* d_q, const void* k_pool, const void* v_pool,
+                                         const int32_t* block_tables, int max_blocks_per_seq,
+                                         const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                         int n_heads, int n_kv_heads, int head_dim,
+                                         int block_tokens, int num_blocks, int kv_dtype, int window,
+                                         int global_stride, int max_ctx, float scale, float* d_out,
+                                         nyion_stream_t stream);
+
 /* Tracked decode: the executor's Full decode call, ops::attention_tracked
  * (ops.rs:283-401, called at executor.rs:742-749).  Same arguments and
  * output as nyion_paged_decode_attention, plus

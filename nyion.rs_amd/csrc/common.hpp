@@ -63,6 +63,10 @@ int device_cu_count();
 enum : unsigned { kRangePrefillV = 1u, kRangeDecodeQ = 2u };
 unsigned* device_status_word();
 
+// Device address of the no-allocation decode's scratch array on the current
+// device (looked up once per device; nullptr with the error set on failure).
+void* decode_scratch_ptr();
+
 // Sets `bit` in the status word from one lane when any lane of the
 // wavefront has `bad` (vector atomic on global memory).
 __device__ __forceinline__ void report_range(unsigned* status, bool bad, unsigned bit) {

@@ -1338,8 +1338,39 @@ int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion
 
 }  // extern "C"
 
+// Split-K scratch of nyion_paged_decode_attention_noalloc: a library-owned
+// device array (one per device, held until the process ends).  Host code
+// never passes the array's name to a kernel (on the host it names a
+// stand-in, not device memory): decode_scratch_ptr() gives the device
+// address, looked up once per device with that device current.
+constexpr size_t kScratchBytes = NYION_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace nyion {
+
+void* decode_scratch_ptr() {
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    uintptr_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v) return (void*)v;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        set_error(NYION_ERR_LAUNCH, "decode scratch: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(e));
+        return nullptr;
+    }
+    cache[dev].store((uintptr_t)ptr, std::memory_order_relaxed);
+    return ptr;
+}
+
+}  // namespace nyion
+
 // Shared body of the paged decode entry points; scores/imp non-null selects
-// the tracked form.
+// the tracked form; use_scratch takes the split-K workspace from the
+// library's scratch array (d_workspace is ignored) and clears its counters.
 static int paged_decode_common(const float* d_q, const void* k_pool, const void* v_pool,
                                const int32_t* block_tables, int max_blocks_per_seq,
                                const int32_t* ctx_lens, const int32_t* q_pos, int batch,
@@ -1347,7 +1378,8 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
                                int num_blocks, int kv_dtype, int window, int global_stride,
                                int max_ctx, float scale, float* d_out, void* d_workspace,
                                size_t workspace_bytes, float* d_scores, int scores_stride,
-                               double* d_importance, int importance_stride, hipStream_t stream) {
+                               double* d_importance, int importance_stride, hipStream_t stream,
+                               bool use_scratch = false) {
     clear_error();
     int rc;
     if ((rc = require_device()) != NYION_OK) return rc;
@@ -1383,7 +1415,26 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
                           window_main_len(max_ctx, window), window > 0 && global_stride > 0,
                           aligned_path, scale)) != NYION_OK)
         return rc;
+    if (use_scratch) {
+        if (pl.ws_bytes > kScratchBytes)
+            return set_error(NYION_ERR_WORKSPACE,
+                             "paged decode (no allocation): this call needs %zu bytes of split-K "
+                             "workspace, the library's scratch holds %zu; use "
+                             "nyion_paged_decode_attention with a workspace",
+                             pl.ws_bytes, kScratchBytes);
+        d_workspace = pl.ws_bytes ? decode_scratch_ptr() : nullptr;
+        if (pl.ws_bytes && !d_workspace) return NYION_ERR_LAUNCH;
+        workspace_bytes = kScratchBytes;
+    }
     if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
+    if (use_scratch && pl.ws_bytes) {
+        // the scratch keeps the previous call's contents (another layout may
+        // have put partials where this call's counters are): clear them
+        const long long n = (long long)pl.chunk * pl.a.n_kv_heads * pl.a.n_hg;
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64)),
+                           dim3(256), 0, stream, pl.a.counters, n);
+        if ((rc = check_launch("decode scratch counters")) != NYION_OK) return rc;
+    }
     pl.track = track;
     DecodeArgs& a = pl.a;
     const long long row = row_elems(head_dim, kv_dtype);
@@ -1453,6 +1504,19 @@ int nyion_paged_decode_attention(const float* d_q, const void* k_pool, const voi
                                num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
                                d_workspace, workspace_bytes, nullptr, 0, nullptr, 0,
                                (hipStream_t)stream);
+}
+
+int nyion_paged_decode_attention_noalloc(const float* d_q, const void* k_pool, const void* v_pool,
+                                         const int32_t* block_tables, int max_blocks_per_seq,
+                                         const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                         int n_heads, int n_kv_heads, int head_dim,
+                                         int block_tokens, int num_blocks, int kv_dtype, int window,
+                                         int global_stride, int max_ctx, float scale, float* d_out,
+                                         nyion_stream_t stream) {
+    return paged_decode_common(d_q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                               q_pos, batch, n_heads, n_kv_heads, head_dim, block_tokens,
+                               num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
+                               nullptr, 0, nullptr, 0, nullptr, 0, (hipStream_t)stream, true);
 }
 
 int nyion_paged_decode_attention_tracked(

@@ -172,7 +172,11 @@ int nyion_init(int device) {
     if (device < 0 || device >= n)
         return set_error(NYION_ERR_NO_DEVICE, "device %d not present (%d devices)", device, n);
     NYION_CHECK_HIP(hipSetDevice(device));
-    return require_device();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    // set-up of the device's scratch array (nyion_paged_decode_attention_noalloc)
+    if (!decode_scratch_ptr()) return NYION_ERR_LAUNCH;
+    return NYION_OK;
 }
 
 int nyion_sync(void) {

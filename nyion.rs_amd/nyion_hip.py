@@ -78,6 +78,8 @@ SIGNATURES = {
     "nyion_paged_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "nyion_paged_decode_attention": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32,
                                            i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
+    "nyion_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32,
+                                                   i32, i32, i32, i32, i32, i32, f32, vp, vp]),
     "nyion_paged_decode_attention_tracked": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32,
                                                    i32, i32, i32, i32, i32, i32, f32, vp, vp, sz,
                                                    vp, i32, vp, i32, vp]),

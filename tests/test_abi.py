@@ -15,6 +15,7 @@ def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
+    text = re.sub(r"^\s*#.*$", "", text, flags=re.M)  # preprocessor lines
     names = re.findall(r"\b([A-Za-z_]\w*)\s*\(([^;{]*?)\)\s*;", text)
     return sorted({n for n, _ in names if n not in ("sizeof",)})
 
