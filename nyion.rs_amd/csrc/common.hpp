@@ -63,6 +63,11 @@ int device_cu_count();
 enum : unsigned { kRangePrefillV = 1u, kRangeDecodeQ = 2u };
 unsigned* device_status_word();
 
+// Records in the status word whether some of the n bf16 values of v reaches
+// 65520 in magnitude (one launch on `stream`; n a multiple of 4, v 8-byte
+// aligned).
+int v_range_check(const uint16_t* v, long long n, hipStream_t stream);
+
 // Device address of the no-allocation decode's scratch array on the current
 // device (looked up once per device; nullptr with the error set on failure).
 void* decode_scratch_ptr();

@@ -72,6 +72,7 @@ struct WriteArgs {
     long long block_stride;  // row units
     long long head_stride;
     int token_stride;
+    unsigned* status;  // bf16 source: the device's range-status word (V beyond binary16)
 };
 
 __device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r, int h) {
@@ -97,18 +98,31 @@ __device__ __forceinline__ uint32_t f16x2_bits(float lo, float hi) {
 }
 
 // One thread per (row, head, 4 values): f32 rows, or binary16 rows (F16).
+// Largest |v| of four bf16 values (the bits of two words).
+__device__ __forceinline__ float v_absmax(uint2 w) {
+    const float a = __uint_as_float(w.x << 16), b = __uint_as_float(w.x & 0xffff0000u);
+    const float c = __uint_as_float(w.y << 16), d = __uint_as_float(w.y & 0xffff0000u);
+    return fmaxf(fmaxf(fabsf(a), fabsf(b)), fmaxf(fabsf(c), fabsf(d)));
+}
+
+// With a bf16 source the kernel also records, in the range-status word,
+// whether some V value reaches 65520 in magnitude: the prefill computed
+// P.V with V in binary16, which cannot hold it (checked here, where V is
+// read anyway, instead of in the prefill's inner loop).
 template <bool F16>
 __global__ void kv_write_flat_kernel(WriteArgs a) {
     const int vec = a.head_dim / 4;
     const long long n = (long long)a.rows * a.n_kv_heads * vec;
+    float vmax = 0.f;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
          i += (long long)gridDim.x * blockDim.x) {
         const int x = (int)(i % vec);
         const int h = (int)((i / vec) % a.n_kv_heads);
         const int r = (int)(i / ((long long)vec * a.n_kv_heads));
+        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 4 * x;
+        if (a.k16) vmax = fmaxf(vmax, v_absmax(*(const uint2*)(a.v16 + src)));
         const long long off = write_row_offset(a, r, h);
         if (off < 0) continue;
-        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 4 * x;
         float4 kk, vv;
         if (a.k16) {
             kk = bf16x4_to_f32(*(const uint2*)(a.k16 + src));
@@ -125,6 +139,27 @@ __global__ void kv_write_flat_kernel(WriteArgs a) {
             *(float4*)((float*)a.v_pool + off + 4 * x) = vv;
         }
     }
+    if (a.k16) report_range(a.status, vmax >= 65520.f, kRangePrefillV);
+}
+
+// The same V range check on its own, for a prefill without a KV write:
+// v [n] bf16 (n a multiple of 4, 8-byte aligned).
+__global__ void v_range_kernel(const uint16_t* v, long long n, unsigned* status) {
+    float vmax = 0.f;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; 4 * i < n;
+         i += (long long)gridDim.x * blockDim.x)
+        vmax = fmaxf(vmax, v_absmax(*(const uint2*)(v + 4 * i)));
+    report_range(status, vmax >= 65520.f, kRangePrefillV);
+}
+
+int v_range_check(const uint16_t* v, long long n, hipStream_t stream) {
+    unsigned* st = device_status_word();
+    if (!st) return NYION_OK;
+    long long g = (n / 4 + 255) / 256;
+    if (g > 2048) g = 2048;
+    if (g < 1) g = 1;
+    hipLaunchKernelGGL(v_range_kernel, dim3((unsigned)g), dim3(256), 0, stream, v, n, st);
+    return check_launch("prefill V range check");
 }
 
 // One thread per (row, head, group): quantise K and V groups.
@@ -465,6 +500,14 @@ int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, i
     a.start_pos = start_pos;
     a.rows = n_tokens;
     a.per_seq = 0;
+    // the V range check of the prefill: fused into the f32 / binary16
+    // write, on its own before a Q4 write
+    if (kv_dtype == NYION_KV_Q4_20B) {
+        if ((rc = v_range_check(v, (long long)n_tokens * n_kv_heads * head_dim, stream)) != NYION_OK)
+            return rc;
+    } else {
+        a.status = device_status_word();
+    }
     return launch_write(a, kv_dtype, stream);
 }
 

@@ -70,7 +70,6 @@ struct PrefillArgs {
     int n_items;   // kv heads x head subsets x row-block groups
     int causal;
     float scale_log2;
-    unsigned* status;  // the device's range-status word (V outside binary16)
 };
 
 constexpr int BN = 64;  // keys per tile
@@ -139,23 +138,33 @@ struct VStage {
     u32x4 v1[UNITS];
 };
 
+// Buffer descriptor of a K or V source: n tokens of tok_stride elements
+// from `base` (the bytes of one kv head's rows; the host keeps n *
+// n_kv_heads * head_dim below 2^30, so every byte offset fits 31 bits).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t source_rsrc(const uint16_t* base, int n,
+                                                               int tok_stride) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n * tok_stride * 2, 0x00020000);
+}
+
 // Loads of the tile whose first key is token kt of a source of n tokens
-// (kt may be negative for the first history tile).  Offsets are 32-bit
-// element offsets from the tile's first token (the host keeps n *
-// n_kv_heads * head_dim below 2^31), so a full tile costs one per-thread
-// base plus constant steps; only a tile that reaches outside [0, n) clamps
-// K rows and zeroes V rows.
+// (kt may be negative for the first history tile).  A tile inside [0, n)
+// is read with buffer loads (one per-thread offset, the tile offset in a
+// scalar register); only a tile that reaches outside clamps K rows and
+// zeroes V rows.
 template <int D>
 __device__ __forceinline__ void stage_load_k(KStage<D>& st, const uint16_t* kbase, int tok_stride,
                                              int n, int kt, int tid) {
     constexpr int CPR = D / 8;
     constexpr int STEP = KStage<D>::NT / CPR;  // keys between a thread's chunks
     if (kt >= 0 && kt + BN <= n) {
-        const uint16_t* kp = kbase + (long long)kt * tok_stride;
-        const int k_off = (tid / CPR) * tok_stride + 8 * (tid % CPR);
+        // buffer loads: the source's descriptor and the tile offset in scalar
+        // registers, one per-thread 32-bit offset (no per-lane address math)
+        const __amdgpu_buffer_rsrc_t r = source_rsrc(kbase, n, tok_stride);
+        const int off = ((tid / CPR) * tok_stride + 8 * (tid % CPR)) * 2;
+        const int t0 = kt * tok_stride * 2, step = STEP * tok_stride * 2;
 #pragma unroll
         for (int u = 0; u < KStage<D>::LOADS; u++)
-            st.k[u] = *(const u32x4*)(kp + k_off + u * STEP * tok_stride);
+            st.k[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off, t0 + u * step, 0);
         return;
     }
 #pragma unroll
@@ -172,11 +181,13 @@ __device__ __forceinline__ void stage_load_v(VStage<D>& st, const uint16_t* vbas
     const int t = kt + 2 * (tid % (BN / 2));
     const int d0 = 8 * (tid / (BN / 2));
     if (kt >= 0 && kt + BN <= n) {
-        const uint16_t* vp = vbase + (long long)t * tok_stride + d0;
+        const __amdgpu_buffer_rsrc_t r = source_rsrc(vbase, n, tok_stride);
+        const int off = ((t - kt) * tok_stride + d0) * 2;
+        const int t0 = kt * tok_stride * 2, row = tok_stride * 2;
 #pragma unroll
         for (int u = 0; u < VStage<D>::UNITS; u++) {
-            st.v0[u] = *(const u32x4*)(vp + STEP * u);
-            st.v1[u] = *(const u32x4*)(vp + STEP * u + tok_stride);
+            st.v0[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 2 * STEP * u, t0, 0);
+            st.v1[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off + 2 * STEP * u, t0 + row, 0);
         }
         return;
     }
@@ -221,11 +232,8 @@ __device__ __forceinline__ void stage_store_k(const KStage<D>& st, unsigned char
     }
 }
 
-// vmax: running max of |v| over the values this thread has staged (a V value
-// of magnitude >= 65520 becomes infinity in binary16).
 template <int D>
-__device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char* vslot, int tid,
-                                              float& vmax) {
+__device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char* vslot, int tid) {
     using L = PrefillLds<D>;
 #pragma unroll
     for (int u = 0; u < VStage<D>::UNITS; u++) {
@@ -241,7 +249,6 @@ __device__ __forceinline__ void stage_store_v(const VStage<D>& st, unsigned char
             const uint32_t x0 = st.v0[u][e >> 1], x1 = st.v1[u][e >> 1];
             const float lo = __uint_as_float((e & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
             const float hi = __uint_as_float((e & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
-            vmax = fmaxf(vmax, fmaxf(fabsf(lo), fabsf(hi)));
             *(uint32_t*)(vslot + (8 * dc + e) * L::VROW + 2 * col) = pack_f16x2(lo, hi);
         }
     }
@@ -314,7 +321,6 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     unsigned char* const vslot0 = lds + 3 * L::KBYTES;
     KStage<D> kst;
     VStage<D> vst;
-    float vmax = 0.f;
 
     // S^T of 32-key half kb of the tile in K slot `ks` (K rows kb*32 + j,
     // chunk 2s + h)
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0, tid);
     load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0, tid);
     stage_store_k<D>(kst, kslot0, tid);
-    stage_store_v<D>(vst, vslot0, tid, vmax);
+    stage_store_v<D>(vst, vslot0, tid);
     if (n_tiles > 1) {
         load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + BN, tid);
         stage_store_k<D>(kst, kslot0 + L::KBYTES, tid);
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         consume_half(s1, vs, 1);
         // a slot past the last tile is written and never read
         stage_store_k<D>(kst, kslot(it + 2), tid);
-        stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid, vmax);
+        stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid);
         if (it + 3 < n_tiles) load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt + 3 * BN, tid);
         if (it + 2 < n_tiles) load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt + 2 * BN, tid);
         __syncthreads();
@@ -466,8 +472,6 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         consume_half(s0, vs, 0);
         consume_half(s1, vs, 1);
     }
-
-    report_range(a.status, vmax >= 65520.f, kRangePrefillV);
 
     // epilogue: divide by the row sums and store
     const float lt = lrun + __shfl_xor(lrun, 32);
@@ -508,10 +512,11 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     if (n_hist < 0) return set_error(NYION_ERR_INVALID, "prefill: n_hist %d", n_hist);
     if (n_hist > 0 && (!k_hist || !v_hist || !aligned(k_hist, 16) || !aligned(v_hist, 16)))
         return set_error(NYION_ERR_INVALID, "prefill: history needs 16-byte aligned k_hist/v_hist");
-    if ((long long)n * n_kv_heads * head_dim >= (1LL << 31) ||
+    // K/V byte offsets are 32-bit (buffer loads): below 2^30 elements per source
+    if ((long long)n * n_kv_heads * head_dim >= (1LL << 30) ||
         (long long)n * n_heads * head_dim >= (1LL << 40))
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: chunk of %d tokens too large", n);
-    if ((long long)n_hist * n_kv_heads * head_dim >= (1LL << 31) ||
+    if ((long long)n_hist * n_kv_heads * head_dim >= (1LL << 30) ||
         (long long)n_hist + n + 2 * BN >= (1LL << 31))
         return set_error(NYION_ERR_UNSUPPORTED, "prefill: history of %d tokens too large", n_hist);
     const int group = n_heads / n_kv_heads;
@@ -544,7 +549,6 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     a.causal = causal ? 1 : 0;
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
-    a.status = device_status_word();
     dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
     if (head_dim == 128)
@@ -552,6 +556,13 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     else
         hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(prefill_threads<64>()), 0, st, a);
     if ((rc = check_launch("prefill")) != NYION_OK) return rc;
+    // V enters the P.V product as binary16: values of magnitude >= 65520 are
+    // reported through the status word (the chunk's V by the KV write when
+    // there is one, else by a check of its own; the history's always here)
+    if (n_hist > 0 &&
+        (rc = v_range_check(v_hist, (long long)n_hist * n_kv_heads * head_dim, st)) != NYION_OK)
+        return rc;
+    if (!k_pool && !v_pool) return v_range_check(v, (long long)n * n_kv_heads * head_dim, st);
     if (k_pool || v_pool) {
         if (!k_pool || !v_pool || !block_table)
             return set_error(NYION_ERR_INVALID, "prefill: KV write needs k_pool, v_pool and block_table");
@@ -584,3 +595,4 @@ extern "C" int nyion_prefill_attention_bf16_ctx(const uint16_t* q, const uint16_
                         scale, out, k_pool, v_pool, block_table, block_tokens, num_blocks,
                         kv_dtype, start_pos, stream);
 }
+
