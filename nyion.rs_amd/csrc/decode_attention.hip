@@ -50,6 +50,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace nyion {
@@ -61,6 +63,16 @@ typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 // 16 bytes at 8-byte alignment (binary16 rows): one dwordx4 load
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(8)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Split-K partials cross workgroups that may sit on different XCDs, whose
+// L2s are not coherent with each other: they are stored and loaded with the
+// sc1 cache policy (what agent-scope relaxed atomic loads and stores carry on
+// this target) through buffer instructions, 16 bytes per instruction.
+constexpr int kSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
 
 enum DecodeMode { MODE_FULL = 0, MODE_WINDOW = 1, MODE_LIST = 2 };
 
@@ -98,6 +110,8 @@ struct DecodeArgs {
     int max_len;    // host bound on attended positions per sequence
     float scale_log2;  // scale * log2(e)
     unsigned* status;  // the device's range-status word (binary16 q overflow)
+    int direct;        // > 0: direct partition, pieces per segment (else stream-K)
+    int seg_tiles;     // direct: host bound on the tiles of one segment
 };
 
 // Sequences per launch: the per-sequence tile prefix sums live in LDS.
@@ -597,20 +611,21 @@ __device__ __forceinline__ void merge_into(MergeAcc& x, float m, float l, const 
 // workgroup.  Partial p of head hh sits at acc0 + (p*16 + hh)*D and
 // ml0[p*16 + hh].  A thread owns one (head, 4-dim quad) item; when there are
 // fewer items than threads, R replicas of each item take partials
-// r, r+R, ... and combine through LDS, so up to 16*R partials need one
+// r, r+R, ... and combine through LDS, so up to CH*R partials need one
 // round of loads.  The partials come from other workgroups, so they are read
-// with device-coherent loads, 16 partials' worth (m, l and O quads) issued
-// before any is used.  `lds` holds 6 floats per thread; the function begins
-// and ends with a barrier.
-template <int D>
+// with sc1 loads, CH partials' worth (m, l and O quads) issued before any is
+// used.  `lds` holds 6 floats per thread; the function begins and ends with
+// a barrier.
+template <int D, int CH>
 __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int g_local, float* out,
                               int tid, float* score_rows, int scores_stride, float* lds) {
     constexpr int QPH = D / 4;  // quads per head
-    constexpr int CH = 16;      // partials per batch of loads
     const int items = g_local * QPH;
     const int R = items >= 256 ? 1 : 256 / items;
     const int nthr = items >= 256 ? 256 : R * items;
     const int r = tid / (items >= 256 ? 256 : items);
+    const __amdgpu_buffer_rsrc_t racc = partial_rsrc(acc0, (uint32_t)np * 16 * D * 4);
+    const __amdgpu_buffer_rsrc_t rml = partial_rsrc(ml0, (uint32_t)np * 16 * 8);
     __syncthreads();
     for (int base = 0; base < items; base += 256) {
         const int item = items >= 256 ? base + tid : tid % items;
@@ -620,36 +635,32 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
         const int dq = item - hh * QPH;
         if (active) {
             for (int p0 = r; p0 < np; p0 += CH * R) {
-                uint64_t mlv[CH], a01[CH], a23[CH];
+                u32x2 mlv[CH];
+                u32x4 av[CH];
 #pragma unroll
                 for (int q = 0; q < CH; q++) {
                     const int pq = p0 + q * R;
                     if (pq < np) {
-                        const long long e = (long long)pq * 16 + hh;
-                        const uint64_t* src = (const uint64_t*)(acc0 + e * D + 4 * dq);
-                        mlv[q] = __hip_atomic_load((const uint64_t*)(ml0 + e), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                        a01[q] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        a23[q] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const int e = pq * 16 + hh;
+                        mlv[q] = __builtin_amdgcn_raw_buffer_load_b64(rml, e * 8, 0, kSc1);
+                        av[q] = __builtin_amdgcn_raw_buffer_load_b128(racc, (e * D + 4 * dq) * 4, 0, kSc1);
                     } else {
-                        mlv[q] = (uint64_t)__float_as_uint(-INFINITY);  // m = -inf, l = 0
-                        a01[q] = a23[q] = 0;
+                        mlv[q] = u32x2{__float_as_uint(-INFINITY), 0u};  // m = -inf, l = 0
+                        av[q] = u32x4{0u, 0u, 0u, 0u};
                     }
                 }
                 float mc = -INFINITY;
 #pragma unroll
-                for (int q = 0; q < CH; q++) mc = fmaxf(mc, __uint_as_float((uint32_t)mlv[q]));
+                for (int q = 0; q < CH; q++) mc = fmaxf(mc, __uint_as_float(mlv[q][0]));
                 MergeAcc c{mc, 0.f, {0.f, 0.f, 0.f, 0.f}};
                 if (mc != -INFINITY) {
 #pragma unroll
                     for (int q = 0; q < CH; q++) {
-                        const float mq = __uint_as_float((uint32_t)mlv[q]);
+                        const float mq = __uint_as_float(mlv[q][0]);
                         const float w = mq == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mq - mc);
-                        c.l = __builtin_fmaf(w, __uint_as_float((uint32_t)(mlv[q] >> 32)), c.l);
-                        c.o[0] = __builtin_fmaf(w, __uint_as_float((uint32_t)a01[q]), c.o[0]);
-                        c.o[1] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a01[q] >> 32)), c.o[1]);
-                        c.o[2] = __builtin_fmaf(w, __uint_as_float((uint32_t)a23[q]), c.o[2]);
-                        c.o[3] = __builtin_fmaf(w, __uint_as_float((uint32_t)(a23[q] >> 32)), c.o[3]);
+                        c.l = __builtin_fmaf(w, __uint_as_float(mlv[q][1]), c.l);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) c.o[i] = __builtin_fmaf(w, __uint_as_float(av[q][i]), c.o[i]);
                     }
                 }
                 merge_into(x, c.m, c.l, c.o);
@@ -689,10 +700,26 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
 // Main tiles [first, first + n) of one segment on the aligned path, in runs of
 // at most 64 tiles: lane l holds the block id of the run's l-th block index
 // (with blocks of >= 16 tokens a run of 64 tiles spans at most 64 blocks).
+// Lane l's block id of block index bi_first + l, for the run of tiles
+// [f, f + nc) from position base (-1 past the run, past the table or out of
+// [0, num_blocks)).
+__device__ __forceinline__ int run_table_entry(const DecodeArgs& a, const int32_t* table, int base,
+                                               int f, int nc, int lane) {
+    const int bi = ((base + 16 * f) >> a.bt_log2) + lane;
+    const int bi_last = (base + 16 * (f + nc) - 1) >> a.bt_log2;
+    int blk = -1;
+    if (bi <= bi_last && bi < a.table_stride) {
+        blk = table[bi];
+        if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
+    }
+    return blk;
+}
+
 template <int D, int KVT, bool TRACK>
 __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, const float* qv,
                                           const Extent& e, const int32_t* table, long long head_off,
-                                          int first, int n, int lane, int j, int kq, float* srow) {
+                                          int first, int n, int lane, int j, int kq, float* srow,
+                                          bool have_pref = false, int tbl_pref = -1) {
     for (int c0 = 0; c0 < n; c0 += 64) {
         const int f = first + c0;
         const int nc = min(64, n - c0);
@@ -703,16 +730,10 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         w.head_off = head_off;
         w.bi_first = (w.base + 16 * f) >> a.bt_log2;
         w.tblv = 0;
-        if (table) {
-            const int bi = w.bi_first + lane;
-            const int bi_last = (w.base + 16 * (f + nc) - 1) >> a.bt_log2;
-            int blk = -1;
-            if (bi <= bi_last && bi < a.table_stride) {
-                blk = table[bi];
-                if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
-            }
-            w.tblv = blk;
-        }
+        // the first run's entries may have been loaded ahead (a superset of
+        // the run from the same first block index: entries past the run are
+        // never read)
+        if (table) w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
         walk_tiles<D, KVT, TRACK>(st, a, qv, nc, j, kq, srow,
                                   [&](int i, long long& ko, long long* vo, int* pos) {
                                       return aligned_offsets<D, KVT>(a, w, f + i, j, kq, ko, vo, pos);
@@ -753,80 +774,141 @@ void decode_kernel(DecodeArgs a) {
     const int kq = lane >> 4;
     const int U = a.n_kv_heads * a.n_hg;  // segments per sequence
 
-    // ---- tiles of one segment of each sequence, prefix-summed
-    int carry = 0;
-    if (threadIdx.x == 0) sm_pref[0] = 0;
-    for (int c0 = 0; c0 < a.batch; c0 += 256) {
-        const int b = c0 + threadIdx.x;
-        int t = 0;
-        if (b < a.batch) {
-            const int2 v = seq_values(a, b);
-            sm_seq[b] = v;
-            t = extent_of<ALIGNED>(a, v).tiles;
-        }
+    // Each iteration runs one piece of segment (b, u) -- its wavefronts take
+    // tiles [wa, wb) -- and ends with a merge: `whole` when the piece is the
+    // segment; otherwise its partial goes to slot `slot`, the segment's
+    // `pieces` partials sit in slots slot0 .. slot0 + pieces - 1 and the last
+    // to arrive merges them.  pref: this wavefront's first block-table
+    // entries were loaded ahead (tbl_pref).
+    //
+    // Direct partition (few segments, a.direct > 0): workgroup = piece
+    // `piece` of segment s, pieces of c tiles of the host's bound on a
+    // segment's tiles, one iteration, no per-workgroup prefix sums; with full
+    // context a tile's positions do not depend on the length, so this
+    // wavefront's block-table entries are requested before the length
+    // arrives.  Stream-K (otherwise): the segments' tile lists laid end to
+    // end and cut into equal ranges, one per workgroup, possibly spanning
+    // several segments.
+    const bool direct = a.direct > 0;
+    int g1 = 0, c = 1, pos = 0, b = 0;
+    if (!direct) {
+        // tiles of one segment of each sequence, prefix-summed into LDS
+        int carry = 0;
+        if (threadIdx.x == 0) sm_pref[0] = 0;
+        for (int c0 = 0; c0 < a.batch; c0 += 256) {
+            const int bb = c0 + threadIdx.x;
+            int t = 0;
+            if (bb < a.batch) {
+                const int2 v = seq_values(a, bb);
+                sm_seq[bb] = v;
+                t = extent_of<ALIGNED>(a, v).tiles;
+            }
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(t, o);
-            if (lane >= o) t += y;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(t, o);
+                if (lane >= o) t += y;
+            }
+            if (lane == 63) sm_wsum[wave] = t;
+            __syncthreads();
+            int off = carry;
+            for (int w = 0; w < wave; w++) off += sm_wsum[w];
+            if (bb < a.batch) sm_pref[bb + 1] = off + t;
+            carry += sm_wsum[0] + sm_wsum[1] + sm_wsum[2] + sm_wsum[3];
+            __syncthreads();
         }
-        if (lane == 63) sm_wsum[wave] = t;
-        __syncthreads();
-        int off = carry;
-        for (int w = 0; w < wave; w++) off += sm_wsum[w];
-        if (b < a.batch) sm_pref[b + 1] = off + t;
-        carry += sm_wsum[0] + sm_wsum[1] + sm_wsum[2] + sm_wsum[3];
-        __syncthreads();
-    }
-    // the host keeps batch * U * (tiles of the longest segment) below 2^31
-    const int T = __builtin_amdgcn_readfirstlane(carry) * U;
-    const int c = (T + (int)gridDim.x - 1) / (int)gridDim.x;  // tiles per workgroup
-    const int g0 = min((int)blockIdx.x * c, T);
-    const int g1 = min(g0 + c, T);
+        // the host keeps batch * U * (tiles of the longest segment) below 2^31
+        const int T = __builtin_amdgcn_readfirstlane(carry) * U;
+        c = (T + (int)gridDim.x - 1) / (int)gridDim.x;  // tiles per workgroup
+        const int g0 = min((int)blockIdx.x * c, T);
+        g1 = min(g0 + c, T);
 
-    // sequences with nothing to attend to (ctx_len <= 0, q_pos < 0, empty list)
-    for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
-        if (sload(&sm_pref[b + 1]) != sload(&sm_pref[b])) continue;
-        float* o = a.out + (long long)b * a.n_heads * D;
-        for (int i = threadIdx.x; i < a.n_heads * D; i += 256) o[i] = 0.f;
-    }
-    if (g0 >= g1) return;
+        // sequences with nothing to attend to (ctx_len <= 0, q_pos < 0, empty list)
+        for (int bb = blockIdx.x; bb < a.batch; bb += gridDim.x) {
+            if (sload(&sm_pref[bb + 1]) != sload(&sm_pref[bb])) continue;
+            float* o = a.out + (long long)bb * a.n_heads * D;
+            for (int i = threadIdx.x; i < a.n_heads * D; i += 256) o[i] = 0.f;
+        }
+        if (g0 >= g1) return;
 
-    // first sequence of the range: the largest b with U * prefix[b] <= g0
-    int b = 0;
-    {
+        // first sequence of the range: the largest b with U * prefix[b] <= g0
         int hi = a.batch - 1;
         while (b < hi) {
             const int mid = (b + hi + 1) >> 1;
             if (U * sload(&sm_pref[mid]) <= g0) b = mid;
             else hi = mid - 1;
         }
+        pos = g0;
     }
-
-    for (int pos = g0; pos < g1;) {
-        while (U * sload(&sm_pref[b + 1]) <= pos) b++;
-        const int pb = sload(&sm_pref[b]);
-        const int Tb = sload(&sm_pref[b + 1]) - pb;
-        const int u = (pos - U * pb) / Tb;
-        const int seg0 = U * pb + u * Tb;  // first global tile of segment (b, u)
-        const int t0 = pos - seg0;
-        const int t1 = min(Tb, t0 + (g1 - pos));
-        pos += t1 - t0;
+    for (;;) {
+        int u, wa, wb, pieces, slot;
+        long long slot0;
+        bool whole, pref = false;
+        int tbl_pref = -1;
+        Extent e;
+        if (direct) {
+            const int P = a.direct;
+            const int s = (int)blockIdx.x / P;
+            const int piece = (int)blockIdx.x - s * P;
+            b = s / U;
+            u = s - b * U;
+            const int cd = (a.seg_tiles + P - 1) / P;
+            const int t0 = piece * cd;
+            const int wa0 = t0 + (wave * cd) / 4, wb0 = t0 + ((wave + 1) * cd) / 4;
+            pref = ALIGNED && a.mode == MODE_FULL && a.tables && wb0 > wa0;
+            if (pref)
+                tbl_pref = run_table_entry(a, a.tables + (long long)b * a.table_stride, 0, wa0,
+                                           min(64, wb0 - wa0), lane);
+            const int len = a.ctx_lens ? sload(a.ctx_lens + b) : a.uniform_len;
+            const int qp = a.q_pos ? sload(a.q_pos + b) : len - 1;
+            e = extent_of<ALIGNED>(a, int2{len, qp});
+            wa = min(wa0, e.tiles);
+            wb = min(wb0, e.tiles);
+            whole = P == 1;
+            pieces = P;
+            slot = (int)blockIdx.x;
+            slot0 = (long long)s * P;
+        } else {
+            while (U * sload(&sm_pref[b + 1]) <= pos) b++;
+            const int pb = sload(&sm_pref[b]);
+            const int Tb = sload(&sm_pref[b + 1]) - pb;
+            u = (pos - U * pb) / Tb;
+            const int seg0 = U * pb + u * Tb;  // first global tile of segment (b, u)
+            const int t0 = pos - seg0;
+            const int t1 = min(Tb, t0 + (g1 - pos));
+            pos += t1 - t0;
+            // the sequence's values from LDS, in scalar registers, so that
+            // tile loop bounds and masks derived from them branch uniformly
+            e = extent_of<ALIGNED>(a, int2{sload(&sm_seq[b].x), sload(&sm_seq[b].y)});
+            const int n = t1 - t0;
+            wa = t0 + (wave * n) / 4;
+            wb = t0 + ((wave + 1) * n) / 4;
+            whole = n == Tb;
+            const int gf = seg0 / c;
+            pieces = (seg0 + Tb - 1) / c - gf + 1;
+            slot = (int)blockIdx.x + b * U + u;
+            slot0 = (long long)gf + b * U + u;
+        }
 
         const int kvh = u / a.n_hg;
         const int hg = u - kvh * a.n_hg;
         const int g_local = min(16, a.group - hg * 16);
         const int head0 = kvh * a.group + hg * 16;
-        // the sequence's values from LDS, in scalar registers, so that tile
-        // loop bounds and masks derived from them branch uniformly
-        const Extent e = extent_of<ALIGNED>(a, int2{sload(&sm_seq[b].x), sload(&sm_seq[b].y)});
 
         // Q operand (B of the QK product): head j, dims by qk_dim.
         float qv[NC];
         {
             const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
             const bool ok = j < g_local;
+            // the lane's dims come in runs of four (qk_dim(4i..4i+3) consecutive):
+            // one 16-byte load per run
 #pragma unroll
-            for (int cc = 0; cc < NC; cc++) qv[cc] = ok ? qrow[qk_dim<D, KVT>(cc, kq)] : 0.f;
+            for (int i = 0; i < NC / 4; i++) {
+                const float4 r4 = ok ? *(const float4*)(qrow + qk_dim<D, KVT>(4 * i, kq)) : float4{0.f, 0.f, 0.f, 0.f};
+                qv[4 * i] = r4.x;
+                qv[4 * i + 1] = r4.y;
+                qv[4 * i + 2] = r4.z;
+                qv[4 * i + 3] = r4.w;
+            }
             if constexpr (KVT == NYION_KV_F16) {
                 // words 4x, 4x+1: the four values as binary16; 4x+2, 4x+3: the
                 // binary16 residuals.  |q| >= 65520 rounds the high part to
@@ -870,16 +952,12 @@ void decode_kernel(DecodeArgs a) {
         m.num_blocks = a.num_blocks;
         m.table_len = a.table_stride;
 
-        // this wavefront's quarter of the piece [t0, t1)
-        const int n = t1 - t0;
-        const int wa = t0 + (wave * n) / 4;
-        const int wb = t0 + ((wave + 1) * n) / 4;
         if (ALIGNED) {
             const int mt = e.main_tiles;
             const int me = min(wb, mt);
             if (wa < me)
                 walk_main<D, KVT, TRACK>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa,
-                                         me - wa, lane, j, kq, srow);
+                                         me - wa, lane, j, kq, srow, pref, tbl_pref);
             const int ga = max(wa, mt) - mt;
             const int gb = wb - mt;
             if (ga < gb) {
@@ -911,10 +989,11 @@ void decode_kernel(DecodeArgs a) {
             sm_l[wave][j] = lt;
         }
         __syncthreads();
-        const bool whole = n == Tb;  // uniform: the segment is this piece
         const int s = b * U + u;
-        const int slot = (int)blockIdx.x + s;
         if (wave == 0) {
+            // this piece's partial slot (used when !whole)
+            const __amdgpu_buffer_rsrc_t racc = partial_rsrc(a.ws_acc + (long long)slot * 16 * D, 16 * D * 4);
+            const __amdgpu_buffer_rsrc_t rml = partial_rsrc(a.ws_ml + (long long)slot * 16, 16 * 8);
             float mh[4], lh[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -954,38 +1033,37 @@ void decode_kernel(DecodeArgs a) {
                         *(float4*)(o + 4 * x) = float4{st.acc[4 * x + 0][r] * inv, st.acc[4 * x + 1][r] * inv,
                                                        st.acc[4 * x + 2][r] * inv, st.acc[4 * x + 3][r] * inv};
                 } else {
-                    // device-coherent (write-through) stores: the merging workgroup
-                    // may run on another XCD, whose L2 does not see this one's
-                    float* o = a.ws_acc + ((long long)slot * 16 + hh) * D + DPL * j;
 #pragma unroll
-                    for (int x = 0; x < DPL; x++)
-                        __hip_atomic_store(o + x, st.acc[x][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (j == 0) {
-                        float* ml = (float*)(a.ws_ml + (long long)slot * 16 + hh);
-                        __hip_atomic_store(ml, mh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(ml + 1, lh[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int x = 0; x < DPL / 4; x++) {
+                        const u32x4 d = {__float_as_uint(st.acc[4 * x + 0][r]), __float_as_uint(st.acc[4 * x + 1][r]),
+                                         __float_as_uint(st.acc[4 * x + 2][r]), __float_as_uint(st.acc[4 * x + 3][r])};
+                        __builtin_amdgcn_raw_buffer_store_b128(d, racc, (hh * D + DPL * j + 4 * x) * 4, 0, kSc1);
                     }
+                    if (j == 0)
+                        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(mh[r]), __float_as_uint(lh[r])},
+                                                              rml, hh * 8, 0, kSc1);
                 }
             }
             if (!whole) {
                 // publish: the write-through stores complete before the arrival is
-                // counted; the last of the segment's pieces to arrive merges
+                // counted (the fence keeps the compiler from moving them past the
+                // wait); the last of the segment's pieces to arrive merges
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
                 __builtin_amdgcn_s_waitcnt(0);
                 int old = 0;
                 if (lane == 0)
                     old = __hip_atomic_fetch_add(a.counters + s, 1, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
                 old = __shfl(old, 0);
-                const int pieces = (seg0 + Tb - 1) / c - seg0 / c + 1;
                 if (lane == 0) sm_last = (old == pieces - 1);
             }
         }
         __syncthreads();  // also: LDS is free for the next piece
         if (!whole && sm_last) {
-            const int gf = seg0 / c;
-            const int np = (seg0 + Tb - 1) / c - gf + 1;
-            const long long slot0 = (long long)gf + s;
-            merge_segment<D>(a.ws_acc + slot0 * 16 * D, a.ws_ml + slot0 * 16, np, g_local,
+            // partials per batch of loads: 16, or 8 in kernels with three
+            // wavefronts per SIMD (168 VGPRs), where 16 would spill
+            constexpr int kMergeBatch = decode_waves_per_eu<D, KVT>() >= 3 ? 8 : 16;
+            merge_segment<D, kMergeBatch>(a.ws_acc + slot0 * 16 * D, a.ws_ml + slot0 * 16, pieces, g_local,
                              a.out + ((long long)b * a.n_heads + head0) * D, threadIdx.x,
                              TRACK ? a.scores + ((long long)b * a.n_heads + head0) * a.scores_stride
                                    : nullptr,
@@ -993,6 +1071,7 @@ void decode_kernel(DecodeArgs a) {
             if (threadIdx.x == 0)
                 __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (direct || pos >= g1) break;
     }
 }
 
@@ -1202,6 +1281,11 @@ static int wg_tiles_for(long long total_tiles) {
     return per_cu < kSmallWgTiles ? kSmallWgTiles : per_cu > kDefaultWgTiles ? kDefaultWgTiles : (int)per_cu;
 }
 
+// Segments of one launch up to which the direct partition is used: with few
+// segments the stream-K prologue (lengths, prefix sums, a search) is a
+// dependent round trip and two barriers that the direct form skips.
+constexpr int kDirectMaxSegments = 64;
+
 template <int D, int KVT, bool AL, bool TR>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
     const int units = pl.a.n_kv_heads * pl.a.n_hg;
@@ -1220,9 +1304,24 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
         if (a.n_pos) a.n_pos += b0;
         if (a.scores) a.scores += (long long)b0 * a.n_heads * a.scores_stride;
         const long long total = (long long)nb * units * pl.tiles_max;
-        int grid = grid_for(total, wg_tiles_for(total), cap);
+        const int wg = wg_tiles_for(total);
+        int grid = grid_for(total, wg, cap);
         if (grid > pl.grid_bound) grid = pl.grid_bound;
         if (pl.ws_bytes == 0 || (nb == 1 && grid <= units)) grid = units;  // whole segments
+        const long long segs = (long long)nb * units;
+        if (AL && a.mode != MODE_LIST && segs <= kDirectMaxSegments) {
+            // pieces per segment from the tiles per workgroup, within the
+            // partial slots the workspace holds (one per workgroup)
+            const int seg_tiles = a.mode == MODE_FULL ? (a.max_len + 15) / 16 : pl.tiles_max;
+            long long P = pl.ws_bytes == 0 ? 1 : (seg_tiles + wg - 1) / wg;
+            const long long limit = std::min<long long>(cap, pl.grid_bound);
+            if (P * segs > limit) P = std::max<long long>(1, limit / segs);
+            if (P > 1 || pl.ws_bytes == 0 || nb == 1) {
+                a.direct = (int)P;
+                a.seg_tiles = seg_tiles;
+                grid = (int)(P * segs);
+            }
+        }
         hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR>), dim3(grid), dim3(256), 0, stream, a);
     }
 }
