@@ -247,6 +247,63 @@ int nyion_paged_decode_attention_positions(
     int num_blocks, int kv_dtype, float scale, float* d_out, void* d_workspace,
     size_t workspace_bytes, nyion_stream_t stream);
 
+/* ------------------------------------------------- reference-shaped zones */
+
+/* A cache laid out as PagedKVCache's (swamp-engine/src/cache.rs:20-21 zone
+ * starts and page sizes, 185-237 flat page ids, 593-611 page_id /
+ * slot_in_page, 700-747 page pointers): positions [0, 4096) in 32-token
+ * pages, [4096, 131072) in 128-token pages, [131072, ...) in 1024-token
+ * pages, flat page ids 0.., 128.., 1120.. by zone.  A page holds every
+ * layer: row (layer, kv_head, slot) of a page of `bs` tokens starts
+ * ((layer * n_kv_heads + kv_head) * bs + slot) rows into the page, a row
+ * being head_dim f32 / binary16 elements or ceil(head_dim/32)*20 Q4-20B
+ * bytes (cache.rs:365, 689, 711 f32; 627, 665, 733 Q4).
+ *
+ * The reference keeps one heap pointer per page (k_pages / v_pages,
+ * cache.rs:33-36); here pages live in two device pools of pool_units units
+ * each (elements for f32 / binary16, bytes for Q4-20B) and page_base[p]
+ * holds flat page p's offset in units, the same in the K and the V pool.
+ * A page whose offset is negative (absent), not a multiple of 4 units (f32,
+ * Q4-20B) or 8 units (binary16), or whose extent passes pool_units is
+ * absent: decode skips its rows, the gather returns NaN for them, the write
+ * leaves them unwritten. */
+
+/* Flat page id and page size (tokens) of position pos (host helpers for
+ * building page_base; page_id of cache.rs:593-598, block_size_for
+ * cache.rs:235-237).  pos < 0 gives -1. */
+int64_t nyion_zone_page_id(int64_t pos);
+int nyion_zone_page_tokens(int64_t pos);
+
+/* PagedKVCache::save_at for one layer (cache.rs:749-811; f32 copy, Q4-20B
+ * quantised byte-identically to save): tokens start_pos .. start_pos +
+ * n_tokens - 1 from k, v [n_tokens][n_kv_heads][head_dim] f32. */
+int nyion_zone_kv_write(void* k_pool, void* v_pool, int64_t pool_units, const int64_t* page_base,
+                        int n_pages, int n_layers, int layer, int n_kv_heads, int head_dim,
+                        int kv_dtype, int start_pos, int n_tokens, const float* k, const float* v,
+                        nyion_stream_t stream);
+
+/* Tokens [0, n_tokens) of one layer of a zone pool (the rows k_page_ptr /
+ * v_page_ptr address, cache.rs:705-725, Q4 dequantised as dequant_block)
+ * as [n_kv_heads][n_tokens][head_dim] f32, like nyion_kv_gather. */
+int nyion_zone_kv_gather(const void* pool, int64_t pool_units, const int64_t* page_base,
+                         int n_pages, int n_layers, int layer, int n_kv_heads, int head_dim,
+                         int kv_dtype, int n_tokens, float* out, nyion_stream_t stream);
+
+/* nyion_paged_decode_attention over one layer of zone pools: ops::attention
+ * / ops::attention_sparse semantics as documented there, reading K/V
+ * through k_page_ptr / v_page_ptr's addressing (ops.rs:210, 221).
+ * page_bases: [batch][max_pages_per_seq] int64; max_ctx must be covered by
+ * the table (nyion_zone_page_id(max_ctx - 1) < max_pages_per_seq).  The
+ * workspace is sized by nyion_paged_decode_workspace_size with the same
+ * arguments. */
+int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
+                                int64_t pool_units, const int64_t* page_bases, int max_pages_per_seq,
+                                int n_layers, int layer, const int32_t* ctx_lens,
+                                const int32_t* q_pos, int batch, int n_heads, int n_kv_heads,
+                                int head_dim, int kv_dtype, int window, int global_stride,
+                                int max_ctx, float scale, float* d_out, void* d_workspace,
+                                size_t workspace_bytes, nyion_stream_t stream);
+
 /* ------------------------------------------ per-layer ring and Fugu policy */
 
 /* Sliding-window KV rings of the GPU decode path: PerLayerGpuState

@@ -131,6 +131,88 @@ __device__ __forceinline__ void q4_dequant4(uint32_t w, float d, float dmin, flo
     out[3] = q4_dequant(d, dmin, (w >> 12) & 0xfu);
 }
 
+// ------------------------------------------------------------ zone pages
+
+// PagedKVCache's zone geometry (swamp-engine/src/cache.rs:20-21 zone starts
+// and page sizes, 185-237 flat page ids, 593-611 page_id / slot_in_page):
+// positions [0, 4096) in 32-token pages, [4096, 131072) in 128-token pages,
+// [131072, ...) in 1024-token pages; flat page id = the zone's first page
+// (0, 128, 1120: the pages of the zones before it) + (pos - zone start) /
+// page tokens.  A page holds every layer: row (layer, kv head, slot) sits at
+// ((layer * n_kv_heads + kv_head) * page_tokens + slot) rows from the page's
+// start (cache.rs:700-712 f32, 728-736 Q4-20B).
+constexpr int kZoneStart1 = 4096, kZoneStart2 = 131072;
+
+struct ZonePos {
+    int page;       // flat page id
+    int slot;       // row within the page's (layer, kv head) block
+    int page_log2;  // log2(page tokens)
+};
+
+__host__ __device__ __forceinline__ ZonePos zone_pos(int t) {
+    ZonePos z;
+    if (t < kZoneStart1) {
+        z.page_log2 = 5;
+        z.page = t >> 5;
+        z.slot = t & 31;
+    } else if (t < kZoneStart2) {
+        z.page_log2 = 7;
+        z.page = 128 + ((t - kZoneStart1) >> 7);
+        z.slot = (t - kZoneStart1) & 127;
+    } else {
+        z.page_log2 = 10;
+        z.page = 1120 + ((t - kZoneStart2) >> 10);
+        z.slot = (t - kZoneStart2) & 1023;
+    }
+    return z;
+}
+
+// One sequence's zone pages.  Offsets and sizes are in row units (f32 or
+// binary16 elements, bytes for Q4-20B).
+struct ZoneMap {
+    const int64_t* page_base;  // offset of each flat page in the pool, < 0 absent;
+                               // nullptr: block-table geometry
+    int n_pages;               // entries of page_base
+    int layer_rows;            // layer * n_kv_heads
+    int slot_rows;             // n_layers * n_kv_heads: rows per page slot
+    int align;                 // offsets must be multiples of this
+    long long pool_units;      // size of each pool
+};
+
+// Validates the host-side description of a zone pool and fills `z` (its
+// page_base left null: each kernel sets its sequence's).  The offset
+// alignment keeps every row on the boundary its loads and stores need:
+// 16 bytes for f32 and binary16 rows, 4 bytes for Q4-20B rows.
+static inline int make_zone_map(ZoneMap& z, long long pool_units, int n_pages, int n_layers,
+                                int layer, int n_kv_heads, int kv_dtype, const char* what) {
+    if (pool_units <= 0 || n_pages <= 0 || n_layers <= 0 || n_kv_heads <= 0)
+        return set_error(NYION_ERR_INVALID, "%s: pool_units, n_pages, n_layers, n_kv_heads must be positive",
+                         what);
+    if (layer < 0 || layer >= n_layers)
+        return set_error(NYION_ERR_INVALID, "%s: layer %d outside [0, %d)", what, layer, n_layers);
+    if ((long long)n_layers * n_kv_heads > (1 << 20))
+        return set_error(NYION_ERR_UNSUPPORTED, "%s: n_layers * n_kv_heads %lld", what,
+                         (long long)n_layers * n_kv_heads);
+    z.page_base = nullptr;
+    z.n_pages = n_pages;
+    z.layer_rows = layer * n_kv_heads;
+    z.slot_rows = n_layers * n_kv_heads;
+    z.align = kv_dtype == NYION_KV_F16 ? 8 : 4;
+    z.pool_units = pool_units;
+    return NYION_OK;
+}
+
+// Offset of row (t, h), or -1 when its page is past the table, absent,
+// misaligned or not inside the pool.
+__device__ __forceinline__ long long zone_row_offset(const ZoneMap& z, int t, int h, int row) {
+    const ZonePos p = zone_pos(t);
+    if (p.page >= z.n_pages) return -1;
+    const long long base = z.page_base[p.page];
+    const long long page_units = ((long long)z.slot_rows << p.page_log2) * row;
+    if (base < 0 || base % z.align || base > z.pool_units - page_units) return -1;
+    return base + ((((long long)(z.layer_rows + h)) << p.page_log2) + p.slot) * row;
+}
+
 // ------------------------------------------------------------ paged rows
 
 // Where row (token t, kv head h) of one sequence lives.  Strides are in
@@ -143,11 +225,13 @@ struct RowMap {
     int bt_log2;   // log2(block_tokens)
     int num_blocks;
     int table_len;  // entries in this sequence's table
+    ZoneMap zone;   // zone.page_base set: zone geometry instead of the table
 };
 
 // Offset of the row, or -1 when the token is past the table or its block id
-// is out of [0, num_blocks).
+// is out of [0, num_blocks) (zone geometry: zone_row_offset's rules).
 __device__ __forceinline__ long long row_offset(const RowMap& m, int t, int h) {
+    if (m.zone.page_base) return zone_row_offset(m.zone, t, h, m.token_stride);
     int blk = 0;
     if (m.table) {
         if ((t >> m.bt_log2) >= m.table_len) return -1;

@@ -112,6 +112,10 @@ struct DecodeArgs {
     unsigned* status;  // the device's range-status word (binary16 q overflow)
     int direct;        // > 0: direct partition, pieces per segment (else stream-K)
     int seg_tiles;     // direct: host bound on the tiles of one segment
+    // zone geometry (gather path): sequence b's page offsets at
+    // page_bases + b * zone.n_pages; zone.page_base unused
+    const int64_t* page_bases;
+    ZoneMap zone;
 };
 
 // Sequences per launch: the per-sequence tile prefix sums live in LDS.
@@ -951,6 +955,8 @@ void decode_kernel(DecodeArgs a) {
         m.bt_log2 = a.bt_log2;
         m.num_blocks = a.num_blocks;
         m.table_len = a.table_stride;
+        m.zone = a.zone;
+        m.zone.page_base = a.page_bases ? a.page_bases + (long long)b * a.zone.n_pages : nullptr;
 
         if (ALIGNED) {
             const int mt = e.main_tiles;
@@ -1298,6 +1304,7 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
         a.q += qo;
         a.out += qo;
         if (a.tables) a.tables += (long long)b0 * a.table_stride;
+        if (a.page_bases) a.page_bases += (long long)b0 * a.zone.n_pages;
         if (a.ctx_lens) a.ctx_lens += b0;
         if (a.q_pos) a.q_pos += b0;
         if (a.positions) a.positions += (long long)b0 * a.pos_stride;
@@ -1686,6 +1693,53 @@ int nyion_paged_decode_attention_positions(
     a.bt_log2 = ilog2(block_tokens);
     a.num_blocks = num_blocks;
     a.mode = MODE_LIST;
+    return launch_plan(pl, (hipStream_t)stream);
+}
+
+int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,
+                                int64_t pool_units, const int64_t* page_bases, int max_pages_per_seq,
+                                int n_layers, int layer, const int32_t* ctx_lens,
+                                const int32_t* q_pos, int batch, int n_heads, int n_kv_heads,
+                                int head_dim, int kv_dtype, int window, int global_stride,
+                                int max_ctx, float scale, float* d_out, void* d_workspace,
+                                size_t workspace_bytes, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!d_q || !d_out || !page_bases || !ctx_lens)
+        return set_error(NYION_ERR_INVALID, "zone decode: null q/out/page_bases/ctx_lens");
+    if (!aligned(d_q, 16) || !aligned(d_out, 16))
+        return set_error(NYION_ERR_INVALID, "zone decode: q/out must be 16-byte aligned");
+    if (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B && kv_dtype != NYION_KV_F16)
+        return set_error(NYION_ERR_INVALID, "zone decode: kv_dtype %d", kv_dtype);
+    if ((rc = check_pool_ptrs(k_pool, v_pool, kv_dtype)) != NYION_OK) return rc;
+    ZoneMap zone;
+    if ((rc = make_zone_map(zone, pool_units, max_pages_per_seq, n_layers, layer, n_kv_heads,
+                            kv_dtype, "zone decode")) != NYION_OK)
+        return rc;
+    if (max_ctx <= 0 || zone_pos(max_ctx - 1).page >= max_pages_per_seq)
+        return set_error(NYION_ERR_INVALID,
+                         "zone decode: max_ctx %d needs %d pages per sequence, the table has %d",
+                         max_ctx, max_ctx > 0 ? zone_pos(max_ctx - 1).page + 1 : 0, max_pages_per_seq);
+    DecodePlan pl;
+    if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype,
+                          window_main_len(max_ctx, window), window > 0 && global_stride > 0,
+                          false, scale)) != NYION_OK)
+        return rc;
+    if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
+    DecodeArgs& a = pl.a;
+    a.q = d_q;
+    a.k = k_pool;
+    a.v = v_pool;
+    a.ctx_lens = ctx_lens;
+    a.q_pos = q_pos;
+    a.out = d_out;
+    a.token_stride = (int)row_elems(head_dim, kv_dtype);
+    a.page_bases = page_bases;
+    a.zone = zone;
+    a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
+    a.window = window;
+    a.global_stride = global_stride;
     return launch_plan(pl, (hipStream_t)stream);
 }
 

@@ -73,6 +73,10 @@ struct WriteArgs {
     long long head_stride;
     int token_stride;
     unsigned* status;  // bf16 source: the device's range-status word (V beyond binary16)
+    // zone geometry: sequence s's page offsets at page_bases + s * zone.n_pages
+    // (tables unused); nullptr: block tables
+    const int64_t* page_bases;
+    ZoneMap zone;
 };
 
 __device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r, int h) {
@@ -87,6 +91,8 @@ __device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r,
     m.bt_log2 = a.bt_log2;
     m.num_blocks = a.num_blocks;
     m.table_len = a.table_stride;
+    m.zone = a.zone;
+    m.zone.page_base = a.page_bases ? a.page_bases + (long long)seq * a.zone.n_pages : nullptr;
     return row_offset(m, pos, h);
 }
 
@@ -291,6 +297,7 @@ struct GatherArgs {
     int head_dim;
     int n_tokens;
     int kvt;
+    ZoneMap zone;  // zone geometry when zone.page_base is set (table unused)
 };
 
 // f32 -> bf16 bits, round to nearest even; NaN -> the quiet NaN 0x7fc0 with
@@ -315,6 +322,7 @@ __global__ void kv_gather_kernel(GatherArgs a) {
     m.bt_log2 = a.bt_log2;
     m.num_blocks = a.num_blocks;
     m.table_len = (a.n_tokens + (1 << a.bt_log2) - 1) >> a.bt_log2;
+    m.zone = a.zone;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
          i += (long long)gridDim.x * blockDim.x) {
         const int x = (int)(i % vec);
@@ -400,14 +408,11 @@ static int grid_for(long long n, int block) {
     return (int)g;
 }
 
-static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_tokens,
-                           int num_blocks, int n_kv_heads, int head_dim, int kv_dtype) {
+// Pools, row format and heads (either geometry).
+static int fill_write_rows(WriteArgs& a, void* k_pool, void* v_pool, int n_kv_heads, int head_dim,
+                           int kv_dtype) {
     if (!k_pool || !v_pool) return set_error(NYION_ERR_INVALID, "kv write: null pool");
-    if (!is_pow2(block_tokens) || block_tokens > (1 << 20))
-        return set_error(NYION_ERR_INVALID, "kv write: block_tokens %d not a power of two",
-                         block_tokens);
-    if (num_blocks <= 0 || n_kv_heads <= 0)
-        return set_error(NYION_ERR_INVALID, "kv write: num_blocks/n_kv_heads");
+    if (n_kv_heads <= 0) return set_error(NYION_ERR_INVALID, "kv write: n_kv_heads");
     if (kv_dtype == NYION_KV_F32) {
         if (head_dim <= 0 || head_dim % 4)
             return set_error(NYION_ERR_UNSUPPORTED, "kv write f32: head_dim %d not a multiple of 4",
@@ -432,11 +437,24 @@ static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_t
     a.v_pool = v_pool;
     a.n_kv_heads = n_kv_heads;
     a.head_dim = head_dim;
+    a.token_stride = (int)row;
+    return NYION_OK;
+}
+
+// The above plus the block-table geometry.
+static int fill_write_args(WriteArgs& a, void* k_pool, void* v_pool, int block_tokens,
+                           int num_blocks, int n_kv_heads, int head_dim, int kv_dtype) {
+    int rc;
+    if ((rc = fill_write_rows(a, k_pool, v_pool, n_kv_heads, head_dim, kv_dtype)) != NYION_OK)
+        return rc;
+    if (!is_pow2(block_tokens) || block_tokens > (1 << 20))
+        return set_error(NYION_ERR_INVALID, "kv write: block_tokens %d not a power of two",
+                         block_tokens);
+    if (num_blocks <= 0) return set_error(NYION_ERR_INVALID, "kv write: num_blocks");
     a.bt_log2 = ilog2(block_tokens);
     a.num_blocks = num_blocks;
-    a.token_stride = (int)row;
-    a.head_stride = (long long)block_tokens * row;
-    a.block_stride = (long long)n_kv_heads * block_tokens * row;
+    a.head_stride = (long long)block_tokens * a.token_stride;
+    a.block_stride = (long long)n_kv_heads * block_tokens * a.token_stride;
     return NYION_OK;
 }
 
@@ -608,6 +626,80 @@ int nyion_kv_gather_bf16(const void* pool, const int32_t* block_table, int block
                          uint16_t* out, nyion_stream_t stream) {
     return kv_gather_impl(pool, block_table, block_tokens, num_blocks, n_kv_heads, head_dim,
                           kv_dtype, n_tokens, nullptr, out, stream);
+}
+
+int64_t nyion_zone_page_id(int64_t pos) {
+    if (pos < 0) return -1;
+    if (pos <= INT32_MAX) return zone_pos((int)pos).page;
+    return 1120 + ((pos - kZoneStart2) >> 10);
+}
+
+int nyion_zone_page_tokens(int64_t pos) {
+    if (pos < 0) return -1;
+    return pos <= INT32_MAX ? 1 << zone_pos((int)pos).page_log2 : 1024;
+}
+
+int nyion_zone_kv_write(void* k_pool, void* v_pool, int64_t pool_units, const int64_t* page_base,
+                        int n_pages, int n_layers, int layer, int n_kv_heads, int head_dim,
+                        int kv_dtype, int start_pos, int n_tokens, const float* k, const float* v,
+                        nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    WriteArgs a{};
+    if ((rc = fill_write_rows(a, k_pool, v_pool, n_kv_heads, head_dim, kv_dtype)) != NYION_OK)
+        return rc;
+    if ((rc = make_zone_map(a.zone, pool_units, n_pages, n_layers, layer, n_kv_heads, kv_dtype,
+                            "zone kv write")) != NYION_OK)
+        return rc;
+    if (!page_base || !k || !v) return set_error(NYION_ERR_INVALID, "zone kv write: null argument");
+    if (start_pos < 0 || n_tokens <= 0 || (long long)start_pos + n_tokens > (1LL << 31) - 1)
+        return set_error(NYION_ERR_INVALID, "zone kv write: start_pos %d, n_tokens %d", start_pos,
+                         n_tokens);
+    if (kv_dtype != NYION_KV_Q4_20B && (!aligned(k, 16) || !aligned(v, 16)))
+        return set_error(NYION_ERR_INVALID, "zone kv write: k/v must be 16-byte aligned");
+    a.page_bases = page_base;
+    a.k = k;
+    a.v = v;
+    a.start_pos = start_pos;
+    a.rows = n_tokens;
+    a.per_seq = 0;
+    return launch_write(a, kv_dtype, (hipStream_t)stream);
+}
+
+int nyion_zone_kv_gather(const void* pool, int64_t pool_units, const int64_t* page_base,
+                         int n_pages, int n_layers, int layer, int n_kv_heads, int head_dim,
+                         int kv_dtype, int n_tokens, float* out, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!pool || !page_base || !out || n_tokens <= 0)
+        return set_error(NYION_ERR_INVALID, "zone kv gather: null argument or non-positive size");
+    if (head_dim <= 0 || head_dim % 8)
+        return set_error(NYION_ERR_UNSUPPORTED, "zone kv gather: head_dim %d not a multiple of 8",
+                         head_dim);
+    if (kv_dtype != NYION_KV_F32 && kv_dtype != NYION_KV_Q4_20B && kv_dtype != NYION_KV_F16)
+        return set_error(NYION_ERR_INVALID, "zone kv gather: kv_dtype");
+    if ((kv_dtype == NYION_KV_F32 || kv_dtype == NYION_KV_F16) && !aligned(pool, 16))
+        return set_error(NYION_ERR_INVALID, "zone kv gather: f32/f16 pool must be 16-byte aligned");
+    if (kv_dtype == NYION_KV_Q4_20B && !aligned(pool, 4))
+        return set_error(NYION_ERR_INVALID, "zone kv gather: Q4-20B pool must be 4-byte aligned");
+    GatherArgs a{};
+    if ((rc = make_zone_map(a.zone, pool_units, n_pages, n_layers, layer, n_kv_heads, kv_dtype,
+                            "zone kv gather")) != NYION_OK)
+        return rc;
+    a.zone.page_base = page_base;
+    a.pool = pool;
+    a.out = out;
+    a.token_stride = (int)(kv_dtype == NYION_KV_Q4_20B ? q4_row_bytes(head_dim) : head_dim);
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.n_tokens = n_tokens;
+    a.kvt = kv_dtype;
+    const long long n = (long long)n_kv_heads * n_tokens * (head_dim / 8);
+    hipLaunchKernelGGL(kv_gather_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+    return check_launch("zone kv gather");
 }
 
 int nyion_q4_dequant(const uint8_t* in, int64_t n_rows, int head_dim, float* out,

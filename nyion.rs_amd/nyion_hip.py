@@ -108,6 +108,13 @@ SIGNATURES = {
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_kv_gather_bf16": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_zone_page_id": (i64, [i64]),
+    "nyion_zone_page_tokens": (i32, [i64]),
+    "nyion_zone_kv_write": (i32, [vp, vp, i64, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp,
+                                  vp, vp]),
+    "nyion_zone_kv_gather": (i32, [vp, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "nyion_zone_decode_attention": (i32, [vp, vp, vp, i64, vp, i32, i32, i32, vp, vp, i32, i32,
+                                          i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
     "nyion_page_policy_create": (vp, [i32, i32, i32]),
     "nyion_page_policy_destroy": (None, [vp]),
     "nyion_page_policy_ensure": (i32, [vp, i32, i32, vp, i32, C.POINTER(C.c_int)]),
@@ -490,6 +497,55 @@ def kv_gather(pool, block_table, block_tokens, n_kv_heads, head_dim, kv_dtype, n
                                 n_kv_heads, head_dim, kv_dtype, n_tokens, ptr(out),
                                 stream_handle(stream))
     check(rc, "nyion_kv_gather")
+
+
+# Reference-shaped zone pools (PagedKVCache geometry): pools are 1-D device
+# tensors of pool units (f32 / float16 elements, uint8 bytes for Q4-20B);
+# page_base [n_pages] (or [B][n_pages] for decode) int64 offsets in units.
+
+def zone_page_id(pos: int) -> int:
+    return int(load().nyion_zone_page_id(pos))
+
+
+def zone_page_tokens(pos: int) -> int:
+    return int(load().nyion_zone_page_tokens(pos))
+
+
+def zone_kv_write(k_pool, v_pool, page_base, n_layers, layer, n_kv_heads, head_dim, kv_dtype,
+                  start_pos, k, v, stream=None):
+    rc = load().nyion_zone_kv_write(ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_base),
+                                    page_base.shape[-1], n_layers, layer, n_kv_heads, head_dim,
+                                    kv_dtype, start_pos, k.shape[0], ptr(k), ptr(v),
+                                    stream_handle(stream))
+    check(rc, "nyion_zone_kv_write")
+
+
+def zone_kv_gather(pool, page_base, n_layers, layer, n_kv_heads, head_dim, kv_dtype, n_tokens,
+                   out, stream=None):
+    rc = load().nyion_zone_kv_gather(ptr(pool), pool.numel(), ptr(page_base), page_base.shape[-1],
+                                     n_layers, layer, n_kv_heads, head_dim, kv_dtype, n_tokens,
+                                     ptr(out), stream_handle(stream))
+    check(rc, "nyion_zone_kv_gather")
+
+
+def zone_decode(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens, out, n_heads,
+                n_kv_heads, head_dim, kv_dtype=KV_F32, window=0, global_stride=0, max_ctx=None,
+                q_pos=None, scale=0.0, workspace=None, stream=None):
+    """q [B][Hq][D] f32, page_bases [B][max_pages] int64, ctx_lens [B] int32."""
+    B = q.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = load().nyion_zone_decode_attention(
+        ptr(q), ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_bases), page_bases.shape[1],
+        n_layers, layer, ptr(ctx_lens), ptr(q_pos), B, n_heads, n_kv_heads, head_dim, kv_dtype,
+        window, global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes,
+        stream_handle(stream))
+    check(rc, "nyion_zone_decode_attention")
+    return workspace
 
 
 def q4_dequant(inp, n_rows, head_dim, out, stream=None):

@@ -87,6 +87,99 @@ def paged_batch(ctx_lens, n_heads=32, n_kv_heads=4, head_dim=64, block_tokens=16
                       seed)
 
 
+# ---------------------------------------------------------------- zone pools
+
+@dataclasses.dataclass
+class ZonePool:
+    """K and V pools laid out as PagedKVCache's zone pages (1-D, in pool units:
+    f32, binary16 bits as uint16, or Q4-20B bytes), page_base[p] the offset of
+    flat page p in both pools (-1 absent)."""
+    k_pool: np.ndarray
+    v_pool: np.ndarray
+    page_base: np.ndarray  # [n_pages] int64
+    n_layers: int
+    n_kv_heads: int
+    head_dim: int
+    kv_dtype: int
+
+    @property
+    def row(self) -> int:
+        return oracle.q4_row_bytes(self.head_dim) if self.kv_dtype == oracle.KV_Q4 else self.head_dim
+
+
+def zone_page_first_position(p: int) -> int:
+    """First position of flat page p (the inverse of page_id, checked against
+    the oracle's golden-pinned orc_zone_page_id by the caller)."""
+    if p < 128:
+        return 32 * p
+    if p < 1120:
+        return 4096 + 128 * (p - 128)
+    return 131072 + 1024 * (p - 1120)
+
+
+def zone_pool(n_tokens, n_layers=2, n_kv_heads=2, head_dim=64, kv_dtype=oracle.KV_F32, seed=0,
+              present=None, gaps=True) -> ZonePool:
+    """Pages covering [0, n_tokens) (only the flat ids in `present` when given),
+    placed in shuffled order, with gaps of 0-3 alignment units between them,
+    filled with N(0,1) rows (quantised for Q4-20B, rounded for binary16)."""
+    L = oracle.lib()
+    big = 1 << 40  # max_seq_len argument: beyond every position used
+    n_pages = int(L.orc_zone_page_id(n_tokens - 1, big)) + 1
+    pages = list(range(n_pages)) if present is None else sorted(set(int(p) for p in present))
+    row = oracle.q4_row_bytes(head_dim) if kv_dtype == oracle.KV_Q4 else head_dim
+    align = 8 if kv_dtype == oracle.KV_F16 else 4
+    rng = np.random.default_rng(seed)
+    base = np.full(n_pages, -1, np.int64)
+    sizes = {}
+    off = 0
+    for p in rng.permutation(pages):
+        first = zone_page_first_position(int(p))
+        assert L.orc_zone_page_id(first, big) == p
+        bs = int(L.orc_zone_block_size(first))
+        off += align * int(rng.integers(0, 4)) if gaps else 0
+        base[p] = off
+        sizes[int(p)] = n_layers * n_kv_heads * bs * row
+        off += sizes[int(p)]
+    dt = {oracle.KV_F32: np.float32, oracle.KV_F16: np.uint16}.get(kv_dtype, np.uint8)
+    pools = []
+    for _ in range(2):
+        pool = np.zeros(off + 64, dt)
+        for p, units in sizes.items():
+            x = _normal(rng, (units // row, head_dim))
+            if kv_dtype == oracle.KV_Q4:
+                x = oracle.q4_quantize_rows(x)
+            elif kv_dtype == oracle.KV_F16:
+                x = x.astype(np.float16).view(np.uint16)
+            pool[base[p]:base[p] + units] = x.reshape(-1)
+        pools.append(pool)
+    return ZonePool(pools[0], pools[1], base, n_layers, n_kv_heads, head_dim, kv_dtype)
+
+
+def zone_row_offsets(zp: ZonePool, layer: int, n_tokens: int) -> np.ndarray:
+    """[Hkv][n_tokens] offsets (pool units) of each row through the oracle's
+    zone arithmetic (orc_zone_page_id + orc_zone_f32_offset / _q4_offset),
+    -1 where the page is absent."""
+    L = oracle.lib()
+    big = 1 << 40
+    off = np.full((zp.n_kv_heads, n_tokens), -1, np.int64)
+    rel = L.orc_zone_q4_offset if zp.kv_dtype == oracle.KV_Q4 else L.orc_zone_f32_offset
+    for t in range(n_tokens):
+        b = zp.page_base[L.orc_zone_page_id(t, big)]
+        if b < 0:
+            continue
+        for h in range(zp.n_kv_heads):
+            off[h, t] = b + rel(layer, h, t, zp.n_kv_heads, zp.head_dim)
+    return off
+
+
+def zone_rows(pool: np.ndarray, offsets: np.ndarray, row: int) -> np.ndarray:
+    """[Hkv][n][row] raw rows at `offsets` (zeros where -1)."""
+    out = np.zeros(offsets.shape + (row,), pool.dtype)
+    ok = offsets >= 0
+    out[ok] = pool[offsets[ok][:, None] + np.arange(row)]
+    return out
+
+
 def c1_contiguous(seed=0):
     """Contiguous node: B=1, 32/4 heads, D=64, contiguous f32 KV of 128 positions."""
     rng = np.random.default_rng(seed)
