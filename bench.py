@@ -16,7 +16,9 @@ and reported under "configs", keyed by their --only selector: c1
 4096; c2t the same through the tracked form), c3h (the headline batch on
 binary16 KV), c4 (4-bit KV, 131072 context, window 4096, cold), c5 (causal
 prefill of 8192 tokens with its paged KV write, TFLOP/s against the bf16
-MFMA peak), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV pool
+MFMA peak), abi (gpu_attention_device without scratch against the node with
+its scores buffer), zone (decode over zone-geometry pages against 16-token
+block tables), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV pool
 with host spill).
 
 Timing: `ms_per_step` is the wall clock over exactly K calls bracketed by
@@ -49,7 +51,7 @@ for sub in ("nyion.rs_amd", "oracle", "tests"):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = ("decode-attn µs/layer + achieved HBM GB/s (% peak); prefill TFLOP/s (% MFMA)")
-ALL = ("c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "gemv", "gemv6", "pool")
+ALL = ("c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "abi", "zone", "gemv", "gemv6", "pool")
 
 
 def log(msg):
@@ -608,6 +610,108 @@ def bench_c1(nh, torch, steps, warmup):
             "bytes_per_layer": 278528}
 
 
+def bench_abi(nh, torch, steps, warmup):
+    """The project-ABI entry without scratch (gpu_attention_device,
+    fused_attention.cu:194-213: the reference allocates an n_heads*seq_len
+    scores buffer per call; this library allocates nothing and, given no
+    buffer, runs one workgroup per (kv head, head group)) against
+    nyion_attention_node given that scores buffer (ScratchBuffers::d_scores,
+    swamp-gpu/src/lib.rs:290-331).  Contiguous f32 KV [Hkv][4096][64], 32/4
+    heads, 40 rotated caches (336 MB, beyond the 256 MB Infinity Cache)."""
+    Hq, Hkv, D, ctx, R = 32, 4, 64, 4096, 40
+    g = torch.Generator(device="cuda").manual_seed(0)
+    sets = [(torch.randn((Hkv, ctx, D), generator=g, device="cuda"),
+             torch.randn((Hkv, ctx, D), generator=g, device="cuda")) for _ in range(R)]
+    q = torch.randn((Hq, D), generator=g, device="cuda")
+    out = torch.empty_like(q)
+    scores = torch.empty(Hq * ctx, device="cuda")
+    L = nh.load()
+    # arguments resolved once: a call then costs only the C-ABI crossing
+    dev_args = [(nh.ptr(q), nh.ptr(k), nh.ptr(v), nh.ptr(out), Hq, Hkv, ctx, D, ctx)
+                for k, v in sets]
+    node_args = [(nh.ptr(q), nh.ptr(k), nh.ptr(v), nh.ptr(scores), nh.ptr(out), Hq, Hkv, ctx, D,
+                  ctx, nh.KV_F32, nh.stream_handle(None)) for k, v in sets]
+
+    def device_call(i):
+        if L.gpu_attention_device(*dev_args[i % R]) != 0:
+            raise RuntimeError("gpu_attention_device failed")
+
+    def node_call(i):
+        if L.nyion_attention_node(*node_args[i % R]) != 0:
+            nh.check(-1, "nyion_attention_node")
+
+    bytes_call = 2 * Hkv * ctx * D * 4 + 2 * Hq * D * 4
+    res = {"workload": "contiguous f32 KV, ctx 4096, 32/4 heads, D 64, cold",
+           "bytes_per_call": bytes_call}
+    for name, fn in (("gpu_attention_device", device_call), ("node_with_scores", node_call)):
+        timed(fn, steps, warmup, torch)
+        us = event_mean(fn, max(steps, 20) * 2, torch) * 1e3
+        res[name] = {"call_us_event_mean": us, "call_us_p10_p50_p90": _us3(event_pcts(fn, max(steps, 20), torch)),
+                     "gbs": bytes_call / (us * 1e-6) / 1e9}
+    res["device_over_node"] = res["gpu_attention_device"]["call_us_event_mean"] / res["node_with_scores"]["call_us_event_mean"]
+    return res
+
+
+def bench_zone(nh, torch, steps, warmup):
+    """Decode over a reference-shaped zone cache (32-token pages holding all
+    22 layers, shuffled page order; the gather path) against the same rows
+    through 16-token block tables (the aligned path): one layer, ctx 4096,
+    32/4 heads, D 64, f32, 2 rotated copies (371 MB)."""
+    Hq, Hkv, D, ctx, NL, R = 32, 4, 64, 4096, 22, 2
+    n_pages = ctx // 32
+    page_units = NL * Hkv * 32 * D
+    g = torch.Generator(device="cuda").manual_seed(0)
+    rng = np.random.default_rng(0)
+    zone, paged = [], []
+    for r in range(R):
+        kz = torch.randn((n_pages * page_units,), generator=g, device="cuda")
+        vz = torch.randn((n_pages * page_units,), generator=g, device="cuda")
+        perm = rng.permutation(n_pages)
+        bases = torch.from_numpy((perm * page_units).astype(np.int64)[None, :]).cuda()
+        zone.append((kz, vz, bases))
+        # layer 0 of the same rows as 16-token blocks: page p slot s -> block 2p + s // 16
+        kp = kz.view(n_pages, NL, Hkv, 2, 16, D)[:, 0].permute(0, 2, 1, 3, 4).reshape(-1, Hkv, 16, D)
+        vp = vz.view(n_pages, NL, Hkv, 2, 16, D)[:, 0].permute(0, 2, 1, 3, 4).reshape(-1, Hkv, 16, D)
+        tab = torch.from_numpy(paged_tables(rng, 1, ctx // 16, ctx // 16)).cuda()
+        kp2, vp2 = torch.empty_like(kp), torch.empty_like(vp)
+        kp2[tab[0].long()] = kp.contiguous()
+        vp2[tab[0].long()] = vp.contiguous()
+        paged.append((kp2, vp2, tab))
+    q = torch.randn((1, Hq, D), generator=g, device="cuda")
+    ctx_t = torch.full((1,), ctx, dtype=torch.int32, device="cuda")
+    out_z, out_p = torch.empty_like(q), torch.empty_like(q)
+    ws = nh.alloc_workspace(nh.decode_workspace_size(1, Hq, Hkv, D, ctx))
+
+    L = nh.load()
+    zargs = [(nh.ptr(q), nh.ptr(kz), nh.ptr(vz), kz.numel(), nh.ptr(bases), n_pages, NL, 0,
+              nh.ptr(ctx_t), None, 1, Hq, Hkv, D, nh.KV_F32, 0, 0, ctx, 0.0, nh.ptr(out_z),
+              nh.ptr(ws), ws.numel(), nh.stream_handle(None)) for kz, vz, bases in zone]
+    pcalls = [nh.prepare_paged_decode(q, kp, vp, tab, ctx_t, out_p, Hq, Hkv, D, 16, ctx, workspace=ws)
+              for kp, vp, tab in paged]
+
+    def zone_call(i):
+        rc = L.nyion_zone_decode_attention(*zargs[i % R])
+        if rc != 0:
+            nh.check(rc, "nyion_zone_decode_attention")
+
+    def paged_call(i):
+        pcalls[i % R]()
+
+    zone_call(0)
+    paged_call(0)
+    torch.cuda.synchronize()
+    diff = float((out_z - out_p).abs().max())
+    bytes_call = 2 * Hkv * ctx * D * 4 + 2 * Hq * D * 4
+    res = {"workload": "f32 KV, ctx 4096, 32/4 heads, D 64, 22-layer zone pages", "bytes_per_call": bytes_call,
+           "max_abs_zone_vs_paged": diff}
+    for name, fn in (("zone", zone_call), ("paged16", paged_call)):
+        timed(fn, steps, warmup, torch)
+        us = event_mean(fn, max(steps, 20) * 2, torch) * 1e3
+        res[name] = {"call_us_event_mean": us, "gbs": bytes_call / (us * 1e-6) / 1e9}
+    res["zone_over_paged"] = res["zone"]["call_us_event_mean"] / res["paged16"]["call_us_event_mean"]
+    return res
+
+
 def _q4k_random(torch, rows, cols, seed):
     """Random Q4_K matrix on the device: uniform nibbles/scales, finite f16
     d = dmin in [5e-5, 5e-4]."""
@@ -871,6 +975,14 @@ def main():
     if "c1" in only:
         log("contiguous 128-position node")
         res["c1"] = bench_c1(nh, torch, steps, warmup)
+    if "abi" in only:
+        log("project ABI: gpu_attention_device vs the node with its scores buffer")
+        res["abi_cliff"] = bench_abi(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
+    if "zone" in only:
+        log("zone-geometry cache vs 16-token block tables")
+        res["zone"] = bench_zone(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
     if "c4" in only:
         log("Q4 KV, ctx 131072, window 4096 (cold: rotated tables)")
         res["c4"] = bench_c4(nh, torch, steps, warmup)
