@@ -1084,27 +1084,32 @@ void decode_kernel(DecodeArgs a) {
 // Tracked decode, second pass: importance[b][t] += sum over q heads of the
 // normalised probability of position t (ops::attention_tracked,
 // ops.rs:303-368: p in f32, accumulated in f64), for every attended t.
+// A workgroup takes 64 positions of one sequence; wavefront w sums heads
+// w, w+4, w+8, ... for its lane's position (so a thread evaluates n_heads/4
+// exponentials and divides), and the four partial sums are added in a fixed
+// order through LDS.
+constexpr int kImpPositions = 64;
+
 __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
-    // (m, l) of up to 256 heads at a time, staged in LDS by vector loads (as
-    // wave-uniform scalar loads behind the per-head guard the compiler
-    // issued them one head, and one round trip, at a time).  A barrier waits
-    // for every load in flight, so the sequence's length, the chunk's (m, l)
-    // and the first 32 heads' scores are all requested before the first one.
-    constexpr int HB = 32;  // score loads issued together
+    constexpr int HB = 16;  // score loads issued together per thread
     __shared__ float2 sml[256];
-    const int t = blockIdx.x * 256 + threadIdx.x;
+    __shared__ double part[4][kImpPositions];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int t = blockIdx.x * kImpPositions + lane;
     const int tt = min(t, a.scores_stride - 3);  // in-row address for any thread
     for (int b = blockIdx.y; b < a.batch; b += gridDim.y) {
         const float* rows = a.scores + (long long)b * a.n_heads * a.scores_stride;
         const Extent e = lane_extent<true>(a, b);
-        // the accumulated value, read with the other loads (written back below
-        // only by the threads of attended positions)
         double* dst = imp + (long long)b * imp_stride + min(t, imp_stride - 1);
-        const double prev = *dst;
+        const double prev = w == 0 ? *dst : 0.0;  // requested with the other loads
         double acc = 0.0;
-        bool active = false;
+        const bool in_window = t >= e.lo && t <= e.hi;
+        const bool global = e.n_glob > 0 && t < e.n_glob * a.global_stride && t % a.global_stride == 0;
+        const bool active = in_window || global;
         for (int h0 = 0; h0 < a.n_heads; h0 += 256) {
             const int hn = min(256, a.n_heads - h0);
+            // (m, l) of this chunk's heads staged in LDS by vector loads
             float2 ml = float2{0.f, 1.f};
             if ((int)threadIdx.x < hn) {
                 const float* row = rows + (long long)(h0 + threadIdx.x) * a.scores_stride;
@@ -1113,31 +1118,30 @@ __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* i
             float sv[HB];
 #pragma unroll
             for (int k = 0; k < HB; k++)
-                sv[k] = rows[(long long)(h0 + min(k, hn - 1)) * a.scores_stride + tt];
+                sv[k] = rows[(long long)(h0 + min(w + 4 * k, hn - 1)) * a.scores_stride + tt];
             __syncthreads();  // the previous chunk's readers are done
             if ((int)threadIdx.x < hn) sml[threadIdx.x] = ml;
             __syncthreads();
-            const bool in_window = t >= e.lo && t <= e.hi;
-            const bool global =
-                e.n_glob > 0 && t % a.global_stride == 0 && t / a.global_stride < e.n_glob;
-            active = in_window || global;
-            if (!active) continue;
-            // heads in ascending order
-            for (int k0 = 0; k0 < hn; k0 += HB) {
+            for (int k0 = 0; 4 * k0 < hn; k0 += HB) {
                 if (k0 > 0) {
 #pragma unroll
                     for (int k = 0; k < HB; k++)
-                        sv[k] = rows[(long long)(h0 + min(k0 + k, hn - 1)) * a.scores_stride + t];
+                        sv[k] = rows[(long long)(h0 + min(w + 4 * (k0 + k), hn - 1)) * a.scores_stride + tt];
                 }
 #pragma unroll
-                for (int k = 0; k < HB; k++)
-                    if (k0 + k < hn) {
-                        const float2 m = sml[k0 + k];
+                for (int k = 0; k < HB; k++) {
+                    const int hh = w + 4 * (k0 + k);
+                    if (active && hh < hn) {
+                        const float2 m = sml[hh];
                         acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) / m.y);
                     }
+                }
             }
         }
-        if (active) *dst = prev + acc;
+        part[w][lane] = acc;
+        __syncthreads();
+        if (w == 0 && active) *dst = prev + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+        __syncthreads();  // part[] is reused by the next sequence
     }
 }
 
@@ -1566,7 +1570,8 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
     DecodeArgs ia = a;
     ia.batch = batch;
     const unsigned gy = batch < 65535 ? (unsigned)batch : 65535u;
-    hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((max_ctx + 255) / 256), gy), dim3(256), 0,
+    hipLaunchKernelGGL(importance_kernel,
+                       dim3((unsigned)((max_ctx + kImpPositions - 1) / kImpPositions), gy), dim3(256), 0,
                        stream, ia, d_importance, importance_stride);
     return check_launch("decode importance");
 }
