@@ -667,6 +667,26 @@ int nyion_softmax_padic_dev(const float* d_logits, float* d_probs, int n, float 
 int nyion_stokes_count(const void* cache);
 int nyion_stokes_read(const void* cache, float* keys, float* values, float* scores);
 
+/* ------------------------------------------------------ Mojo kernel FFI */
+
+/* The symbol the reference loads from libswamp_mojo.so
+ * (swamp-gpu/src/mojo.rs:5,38: extern "C" fn(u64 x 5, i32 x 5)), with the
+ * semantics of swamp-gpu/kernels/attention.mojo:38-152.  Host pointers passed
+ * as integers: q [n_heads][head_dim] f32, k_q4 and v_q4 one K and one V
+ * shared by all heads, row t at t * ceil(head_dim/32) * 20 f32 words (per
+ * 32-element block: d, dmin, then the 16 nibble bytes as float values, low
+ * nibble first), positions [n_sparse] int32 (>= 0), out [n_heads][head_dim]
+ * f32.  Per head: scores dot(k, q) / sqrt(head_dim); tiles of 64 listed
+ * positions; each tile's weights are exp(s - m) / d with the running (m, d)
+ * after that tile (the output of earlier tiles is not rescaled), weights
+ * below 1e-8 skipped.  window and global_stride are accepted and unused, as
+ * in the reference.  The call copies its operands to device buffers it
+ * allocates and frees (not a hot path: the reference has no caller), and
+ * returns when out is written.  On an error out is left unchanged and
+ * nyion_last_error() says why. */
+void  sparse_attention_q4(uint64_t q, uint64_t k_q4, uint64_t v_q4, uint64_t positions, uint64_t out,
+                          int n_heads, int head_dim, int n_sparse, int window, int global_stride);
+
 #ifdef __cplusplus
 }
 #endif

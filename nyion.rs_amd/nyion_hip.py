@@ -108,6 +108,7 @@ SIGNATURES = {
                                     vp]),
     "nyion_kv_gather": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_kv_gather_bf16": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "sparse_attention_q4": (None, [C.c_uint64] * 5 + [i32] * 5),
     "nyion_zone_page_id": (i64, [i64]),
     "nyion_zone_page_tokens": (i32, [i64]),
     "nyion_zone_kv_write": (i32, [vp, vp, i64, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp,
@@ -546,6 +547,22 @@ def zone_decode(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens, out, n
         stream_handle(stream))
     check(rc, "nyion_zone_decode_attention")
     return workspace
+
+
+def sparse_attention_q4(q, k_q4, v_q4, positions, n_heads, head_dim, window=0, global_stride=0):
+    """The Mojo FFI symbol on host numpy arrays (f32 q, f32-word K/V rows,
+    int32 positions); returns out [n_heads][head_dim] f32."""
+    import numpy as np
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k_q4 = np.ascontiguousarray(k_q4, dtype=np.float32)
+    v_q4 = np.ascontiguousarray(v_q4, dtype=np.float32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    out = np.full((n_heads, head_dim), np.nan, np.float32)
+    load().sparse_attention_q4(q.ctypes.data, k_q4.ctypes.data, v_q4.ctypes.data, pos.ctypes.data,
+                               out.ctypes.data, n_heads, head_dim, len(pos), window, global_stride)
+    if out.size and np.isnan(out).all() and last_error():  # the symbol returns nothing
+        raise NyionError(ERR_INVALID, f"sparse_attention_q4: {last_error()}")
+    return out
 
 
 def q4_dequant(inp, n_rows, head_dim, out, stream=None):

@@ -833,3 +833,67 @@ int orc_gemv_q6k(const uint8_t* w, const float* x, float* out, int n_rows, int n
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------
+ * sparse_attention_q4 (swamp-gpu/kernels/attention.mojo):
+ *   rows: position t's K (and V) row is blocks*20 f32 words at t*blocks*20
+ *         (blocks = ceil(head_dim/32), 53-54); block b: word 0 d, word 1
+ *         dmin, word 2 + i/2 holds the byte of elements i, i+1 as a float
+ *         value, read as an integer (truncation), low nibble for even i
+ *         (74-83, 104-113);
+ *   k = d*nib + dmin, dot accumulated in element order (76-84),
+ *   s = dot * (1/sqrt(head_dim)) (85, 141);
+ *   per tile of 64 listed positions (60-63): tile max from -1e10 (66, 87),
+ *   tile sum of exp(s - tile max) in order (90-92), then the running
+ *   (m, d) from (-1e10, 0): new_m = max(m, tile max), d = d*exp(m - new_m)
+ *   + tile_sum*exp(tile max - new_m), m = new_m (94-96);
+ *   each position of the tile adds v*w to the output, w = exp(s - m)/d with
+ *   the running (m, d) after this tile, skipping w < 1e-8 (99-115); the
+ *   output of earlier tiles is not rescaled.
+ * The library is built with -ffp-contract=off: each written multiply-add
+ * keeps two roundings.
+ * --------------------------------------------------------------------- */
+static float mojo_q4_elem(const float* row, int i) {
+    const float* blk = row + (i / 32) * 20;
+    const int e = i % 32;
+    const int64_t byte = (int64_t)blk[2 + e / 2];
+    const int nib = (int)((byte >> ((e % 2) * 4)) & 0x0F);
+    return blk[0] * (float)nib + blk[1];
+}
+
+void orc_mojo_sparse_attention_q4(const float* q, const float* k_q4, const float* v_q4,
+                                  const int32_t* positions, float* out, int n_heads,
+                                  int head_dim, int n_sparse) {
+    const int blocks = (head_dim + 31) / 32;
+    const int64_t row = (int64_t)blocks * 20;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float scores[64];
+    for (int h = 0; h < n_heads; h++) {
+        const float* qh = q + (int64_t)h * head_dim;
+        float* oh = out + (int64_t)h * head_dim;
+        float m = -1e10f, d = 0.0f;
+        for (int i = 0; i < head_dim; i++) oh[i] = 0.0f;
+        for (int t0 = 0; t0 < n_sparse; t0 += 64) {
+            const int nt = n_sparse - t0 < 64 ? n_sparse - t0 : 64;
+            float tmax = -1e10f;
+            for (int p = 0; p < nt; p++) {
+                const float* kr = k_q4 + positions[t0 + p] * row;
+                float dot = 0.0f;
+                for (int i = 0; i < head_dim; i++) dot += mojo_q4_elem(kr, i) * qh[i];
+                scores[p] = dot * scale;
+                if (scores[p] > tmax) tmax = scores[p];
+            }
+            float tsum = 0.0f;
+            for (int p = 0; p < nt; p++) tsum += expf(scores[p] - tmax);
+            const float nm = m > tmax ? m : tmax;
+            d = d * expf(m - nm) + tsum * expf(tmax - nm);
+            m = nm;
+            for (int p = 0; p < nt; p++) {
+                const float w = expf(scores[p] - m) / d;
+                if (w < 1e-8f) continue;
+                const float* vr = v_q4 + positions[t0 + p] * row;
+                for (int i = 0; i < head_dim; i++) oh[i] += mojo_q4_elem(vr, i) * w;
+            }
+        }
+    }
+}

@@ -46,6 +46,13 @@
  *                                              blocks (fused_gemv_q6k.rs:329-
  *                                              356), a numpy restatement and
  *                                              float64 dequantise-then-dot
+ *   orc_mojo_sparse_attention_q4             : one tile (<= 64 positions) equals
+ *                                              orc_attention_positions on the
+ *                                              dequantised rows; equal scores
+ *                                              over two tiles give the closed
+ *                                              form sum(v1)/64 + sum(v2)/128 of
+ *                                              the per-tile normalisation; a
+ *                                              weight below 1e-8 adds nothing
  * Bit-parity of attention outputs with the Rust binary (glibc expf order,
  * rayon scheduling of the importance sum) is unpinned and not required:
  * attention parity is at tolerance.
@@ -158,6 +165,15 @@ int  orc_gemv_q4k(const uint8_t* w, const float* x, float* out, int n_rows, int 
 float orc_q6k_scale_to_f32(uint16_t v);
 void  orc_q6k_dequant_block(const uint8_t* blk, float* out);
 int   orc_gemv_q6k(const uint8_t* w, const float* x, float* out, int n_rows, int n_cols);
+
+/* sparse_attention_q4 of the Mojo kernel library (swamp-gpu/kernels/
+ * attention.mojo:38-152, loaded through swamp-gpu/src/mojo.rs:5,38): every
+ * head against one K/V of f32-word Q4 rows, tiles of 64 listed positions,
+ * each tile's weights normalised by the running denominator of the tiles so
+ * far. */
+void  orc_mojo_sparse_attention_q4(const float* q, const float* k_q4, const float* v_q4,
+                                   const int32_t* positions, float* out, int n_heads,
+                                   int head_dim, int n_sparse);
 
 int orc_max_threads(void);
 

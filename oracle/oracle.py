@@ -65,6 +65,8 @@ def lib():
         L.orc_q6k_dequant_block.argtypes = [C.c_void_p, C.c_void_p]
         L.orc_gemv_q6k.restype = C.c_int
         L.orc_gemv_q6k.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.orc_mojo_sparse_attention_q4.restype = None
+        L.orc_mojo_sparse_attention_q4.argtypes = [C.c_void_p] * 5 + [C.c_int] * 3
         L.orc_gemv_q4k.restype = C.c_int
         L.orc_gemv_q4k.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         L.orc_dot_avx512_order.restype = C.c_float
@@ -361,3 +363,34 @@ def gemv_q6k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np.ndarr
     if lib().orc_gemv_q6k(w.ctypes.data, x.ctypes.data, out.ctypes.data, n_rows, n_cols) != 0:
         raise ValueError("orc_gemv_q6k: n_cols must be a positive multiple of 256")
     return out
+
+
+def mojo_q4_rows(x: np.ndarray) -> np.ndarray:
+    """f32 rows [n][head_dim] -> the Mojo kernel's row format [n][blocks*20]
+    f32 words (attention.mojo:8-33): per 32-element block word 0 d, word 1
+    dmin, words 2.. the 16 nibble bytes as float values, quantised with the
+    Q4-20B rules (cache.rs:637-663; d and dmin as the f16 values stored)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, hd = x.shape
+    b = q4_quantize_rows(x)
+    blocks = (hd + 31) // 32
+    g = b.reshape(n, blocks, 20)
+    d = g[:, :, 0:2].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    dmin = g[:, :, 2:4].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    out = np.zeros((n, blocks, 20), np.float32)
+    out[:, :, 0] = d
+    out[:, :, 1] = dmin
+    out[:, :, 2:18] = g[:, :, 4:20].astype(np.float32)
+    return out.reshape(n, blocks * 20)
+
+
+def mojo_sparse_attention_q4(q: np.ndarray, k_q4: np.ndarray, v_q4: np.ndarray,
+                             positions: np.ndarray, n_heads: int, head_dim: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k_q4 = np.ascontiguousarray(k_q4, dtype=np.float32)
+    v_q4 = np.ascontiguousarray(v_q4, dtype=np.float32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    lib().orc_mojo_sparse_attention_q4(q.ctypes.data, k_q4.ctypes.data, v_q4.ctypes.data,
+                                       pos.ctypes.data, out.ctypes.data, n_heads, head_dim, len(pos))
+    return out.reshape(n_heads, head_dim)

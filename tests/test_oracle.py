@@ -487,3 +487,68 @@ def test_apply_rope_rotation():
     qa, _ = oracle.apply_rope(q, k, 10 * M, M, lut)
     qb, _ = oracle.apply_rope(q, k, M - 1, M, lut)
     assert np.array_equal(qa, qb)
+
+
+# ---------------------------------------------------------------- Mojo FFI
+
+def _mojo_dequant(rows, head_dim):
+    """f32 values of Mojo-format rows through the Q4-20B dequantiser (an
+    independent path: the words carry the f16 d, dmin and nibble bytes)."""
+    n = rows.shape[0]
+    blocks = (head_dim + 31) // 32
+    w = rows.reshape(n, blocks, 20)
+    b = np.zeros((n, blocks, 20), np.uint8)
+    b[:, :, 0:2] = w[:, :, 0].astype(np.float16).view(np.uint8).reshape(n, blocks, 2)
+    b[:, :, 2:4] = w[:, :, 1].astype(np.float16).view(np.uint8).reshape(n, blocks, 2)
+    b[:, :, 4:20] = w[:, :, 2:18].astype(np.uint8)
+    return oracle.q4_dequant_rows(b.reshape(n, blocks * 20), head_dim)
+
+
+def test_mojo_one_tile_is_softmax_attention():
+    """<= 64 positions: one tile, so the result is softmax attention over the
+    listed positions (every head against the one K/V)."""
+    rng = np.random.default_rng(7)
+    for hd, n_pos in ((64, 40), (128, 64), (96, 17)):
+        x_k = rng.standard_normal((300, hd)).astype(np.float32)
+        x_v = rng.standard_normal((300, hd)).astype(np.float32)
+        kq, vq = oracle.mojo_q4_rows(x_k), oracle.mojo_q4_rows(x_v)
+        q = rng.standard_normal((3, hd)).astype(np.float32)
+        pos = rng.choice(300, n_pos, replace=False).astype(np.int32)
+        got = oracle.mojo_sparse_attention_q4(q, kq, vq, pos, 3, hd)
+        k = _mojo_dequant(kq, hd)[None]
+        v = _mojo_dequant(vq, hd)[None]
+        lay = oracle.contiguous_layout(np.ascontiguousarray(k), np.ascontiguousarray(v), 300, hd)
+        ref = oracle.attention_positions(q, lay, pos, 3, 1, hd).reshape(3, hd)
+        assert np.allclose(got, ref, rtol=1e-5, atol=1e-6), (hd, np.abs(got - ref).max())
+
+
+def test_mojo_tiles_normalise_by_the_running_denominator():
+    """Equal scores over 150 positions (tiles of 64, 64, 22): tile k's weights
+    are 1 / (positions seen so far), so out = sum(v1)/64 + sum(v2)/128 +
+    sum(v3)/150, not the mean."""
+    rng = np.random.default_rng(8)
+    hd = 64
+    kq = np.repeat(oracle.mojo_q4_rows(rng.standard_normal((1, hd)).astype(np.float32)), 150, axis=0)
+    vq = oracle.mojo_q4_rows(rng.standard_normal((150, hd)).astype(np.float32))
+    q = rng.standard_normal((2, hd)).astype(np.float32)
+    pos = np.arange(150, dtype=np.int32)
+    got = oracle.mojo_sparse_attention_q4(q, kq, vq, pos, 2, hd)
+    v = _mojo_dequant(vq, hd).astype(np.float64)
+    want = v[:64].sum(0) / 64 + v[64:128].sum(0) / 128 + v[128:].sum(0) / 150
+    assert np.allclose(got, np.broadcast_to(want, got.shape), rtol=1e-5, atol=1e-6)
+    assert not np.allclose(got[0], v.mean(0), rtol=1e-3)
+
+
+def test_mojo_skips_weights_below_1e_8():
+    """Position 1's weight exp(-21.2) ~ 6e-10 is skipped: its V row (9e5 per
+    element) would otherwise add ~5.5e-4 to an output of 1.0."""
+    hd = 32
+    k = np.zeros((2, 20), np.float32)
+    k[0, 0], k[0, 2:18] = 0.25, 255.0     # k0 = 3.75 per element: s0 = 3.75*32/sqrt(32)
+    v = np.zeros((2, 20), np.float32)
+    v[0, 0], v[0, 2:18] = 1.0 / 15.0, 255.0  # v0 = 15 * (1/15) per element
+    v[1, 0], v[1, 2:18] = 60000.0, 255.0     # v1 = 900000 per element
+    q = np.ones((1, hd), np.float32)
+    got = oracle.mojo_sparse_attention_q4(q, k, v, np.array([0, 1], np.int32), 1, hd)
+    v0 = np.float32(np.float32(1.0 / 15.0) * np.float32(15.0))
+    assert np.all(got == v0), got[0, :4]
