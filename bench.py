@@ -14,7 +14,8 @@ microseconds beside it.  The other workloads are measured in the same run
 and reported under "configs", keyed by their --only selector: c1
 (contiguous 128-position node), c2 (22-layer TinyLlama decode step, ctx
 4096; c2t the same through the tracked form), c3h (the headline batch on
-binary16 KV), c4 (4-bit KV, 131072 context, window 4096, cold), c5 (causal
+binary16 KV), c3q (the headline batch on Q4-20B KV), c4 (4-bit KV, 131072
+context, window 4096, cold), c5 (causal
 prefill of 8192 tokens with its paged KV write, TFLOP/s against the bf16
 MFMA peak), abi (gpu_attention_device without scratch against the node with
 its scores buffer), zone (decode over zone-geometry pages against 16-token
@@ -51,7 +52,7 @@ for sub in ("nyion.rs_amd", "oracle", "tests"):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = ("decode-attn µs/layer + achieved HBM GB/s (% peak); prefill TFLOP/s (% MFMA)")
-ALL = ("c1", "c2", "c2t", "c3", "c3h", "c4", "c5", "abi", "zone", "gemv", "gemv6", "pool")
+ALL = ("c1", "c2", "c2t", "c3", "c3h", "c3q", "c4", "c5", "abi", "zone", "gemv", "gemv6", "pool")
 
 
 def log(msg):
@@ -190,9 +191,10 @@ def _cpu_model():
 C3_HQ, C3_HKV, C3_D, C3_BT = 32, 4, 64, 16
 
 
-def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
+def bench_c3(nh, torch, steps, warmup, seed=0, f16=False, q4=False):
     """64-sequence continuous batch; f16=True stores the same K/V draw as
-    binary16 rows (half the bytes)."""
+    binary16 rows (half the bytes), q4=True as Q4-20B rows (40 bytes per
+    64-element row, quantised on the device)."""
     import workloads as W
 
     Hq, Hkv, D, bt = C3_HQ, C3_HKV, C3_D, C3_BT
@@ -211,13 +213,21 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
     vp = torch.randn((total, Hkv, bt, D), generator=g, device="cuda")
     if f16:
         kp, vp = kp.half(), vp.half()
+    if q4:
+        rb = 40
+        kq = torch.empty((total, Hkv, bt, rb), dtype=torch.uint8, device="cuda")
+        vq = torch.empty_like(kq)
+        rows = total * Hkv * bt
+        nh.q4_quantize(kp, rows, D, kq)
+        nh.q4_quantize(vp, rows, D, vq)
+        kp, vp = kq, vq
     q = torch.randn((64, Hq, D), generator=g, device="cuda")
     tab = torch.from_numpy(tables).cuda()
     ctx = torch.from_numpy(lens).cuda()
     out = torch.empty_like(q)
     maxc = int(lens.max())
     ws = nh.alloc_workspace(nh.decode_workspace_size(64, Hq, Hkv, D, maxc))
-    kvt = nh.KV_F16 if f16 else nh.KV_F32
+    kvt = nh.KV_F16 if f16 else nh.KV_Q4_20B if q4 else nh.KV_F32
     call1 = nh.prepare_paged_decode(q, kp, vp, tab, ctx, out, Hq, Hkv, D, bt, maxc, kv_dtype=kvt,
                                     workspace=ws)
 
@@ -225,7 +235,8 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
         call1()
 
     toks = int(lens.sum())
-    nbytes = 2 * toks * Hkv * D * (2 if f16 else 4) + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
+    row_bytes = 40 if q4 else D * (2 if f16 else 4)
+    nbytes = 2 * toks * Hkv * row_bytes + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
     ms = timed(call, steps, warmup, torch)
     reps = max(steps, 20)
     us = event_mean(call, reps, torch) * 1e3
@@ -234,7 +245,7 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False):
             "reps": reps, "bytes": nbytes, "tokens": toks,
             "gbs_wall": nbytes / (ms * 1e-3) / 1e9, "gbs": nbytes / (us * 1e-6) / 1e9,
             "gbs_median": nbytes / (pct[1] * 1e-3) / 1e9,
-            "roofline": hbm_roofline(nbytes, us, pmc_traffic("c3h" if f16 else "c3")),
+            "roofline": hbm_roofline(nbytes, us, pmc_traffic("c3h" if f16 else "c3q" if q4 else "c3")),
             "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
 
 
@@ -963,6 +974,10 @@ def main():
     if "c3h" in only:
         log("64-sequence continuous batch, binary16 KV")
         res["c3h"] = bench_c3(nh, torch, steps, warmup, f16=True)
+        torch.cuda.empty_cache()
+    if "c3q" in only:
+        log("64-sequence continuous batch, Q4-20B KV")
+        res["c3q"] = bench_c3(nh, torch, steps, warmup, q4=True)
         torch.cuda.empty_cache()
     if "c2" in only:
         log("22-layer decode step, ctx 4096")

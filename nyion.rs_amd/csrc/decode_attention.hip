@@ -193,17 +193,16 @@ __device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e,
 //   f16: value c = 8x+4e+y (binary16 MFMA 2x+e, element y) holds dim
 //        32x + 8kq + 4e + y  (per x, the 4 quads of a row read 64 contiguous
 //        bytes)
-//   Q4 : call c holds dim kq*D/4 + c            (contiguous nibbles)
+//   Q4 : as f32, in binary16 steps of 16 dims: step x = c/4 holds dims
+//        16x + 4kq .. +3, the lane's 4 nibbles of K row j
 // The Q operand uses the same map (qk_dim).  V operand of lane (col j, quad
 // kq), row 4kq+r: DPL = D/16 consecutive dims from DPL*j.
 template <int D, int KVT>
 __device__ __forceinline__ int qk_dim(int c, int kq) {
     if constexpr (KVT == NYION_KV_F16)
         return 32 * (c >> 3) + 8 * kq + 4 * ((c >> 2) & 1) + (c & 3);
-    else if constexpr (KVT == NYION_KV_F32)
-        return 16 * (c >> 2) + 4 * kq + (c & 3);
     else
-        return kq * (D / 4) + c;
+        return 16 * (c >> 2) + 4 * kq + (c & 3);  // f32 and Q4-20B
 }
 
 // Raw (undecoded) registers of one tile for one lane.
@@ -224,8 +223,8 @@ struct Tile<D, NYION_KV_F16> {
 
 template <int D>
 struct Tile<D, NYION_KV_Q4_20B> {
-    uint32_t khdr;            // f16 d | f16 dmin << 16 of the lane's K group
-    uint32_t k[D / 32];       // D/4 nibbles of K row j
+    uint32_t kn[D / 16];      // K row j, step x: the nibbles of dims 16x + 4kq .. +3 (low 16 bits)
+    uint32_t khdr;            // K row j, group kq % (D/32): f16 d | f16 dmin << 16
     uint32_t vhdr[4];
     uint32_t v[4];            // D/16 nibbles of V row 4kq+r (low 16 bits when D = 64)
 };
@@ -267,12 +266,15 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
                 t.v[r][x] = __builtin_nontemporal_load((const floatx4*)(vr + 4 * x));
         }
     } else {
-        const int ke0 = kq * (D / 4);
-        const uint8_t* kr = (const uint8_t*)kb + koff + kQ4GroupBytes * (ke0 >> 5);
-        t.khdr = __builtin_nontemporal_load((const uint32_t*)kr);
-        const uint32_t* kn = (const uint32_t*)(kr + 4 + ((ke0 & 31) >> 1));
+        // K row j: step x is group x/2, nibble bytes 8(x&1) + 2kq, +1; and
+        // the header of group kq % (D/32) (lane 16g + i then holds row i's
+        // header of group g)
+        const uint8_t* kr = (const uint8_t*)kb + koff;
 #pragma unroll
-        for (int w = 0; w < D / 32; w++) t.k[w] = __builtin_nontemporal_load(kn + w);
+        for (int x = 0; x < D / 16; x++)
+            t.kn[x] = __builtin_nontemporal_load(
+                (const uint16_t*)(kr + kQ4GroupBytes * (x >> 1) + 4 + 8 * (x & 1) + 2 * kq));
+        t.khdr = __builtin_nontemporal_load((const uint32_t*)(kr + kQ4GroupBytes * (kq % (D / 32))));
         const int ve0 = (D / 16) * j;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -289,37 +291,23 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
 
 template <int D, int KVT>
 __device__ __forceinline__ void decode_k(const Tile<D, KVT>& t, float* kv) {
-    if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
-        for (int x = 0; x < D / 16; x++) {
-            kv[4 * x + 0] = t.k[x].x;
-            kv[4 * x + 1] = t.k[x].y;
-            kv[4 * x + 2] = t.k[x].z;
-            kv[4 * x + 3] = t.k[x].w;
-        }
-    } else {
-        const float d = f16_bits_to_f32(t.khdr), dmin = f16_bits_to_f32(t.khdr >> 16);
-#pragma unroll
-        for (int w = 0; w < D / 32; w++) q4_dequant8(t.k[w], d, dmin, kv + 8 * w);
+    for (int x = 0; x < D / 16; x++) {
+        kv[4 * x + 0] = t.k[x].x;
+        kv[4 * x + 1] = t.k[x].y;
+        kv[4 * x + 2] = t.k[x].z;
+        kv[4 * x + 3] = t.k[x].w;
     }
 }
 
 template <int D, int KVT>
 __device__ __forceinline__ void decode_v(const Tile<D, KVT>& t, int r, float* vv) {
-    if constexpr (KVT == NYION_KV_F32) {
 #pragma unroll
-        for (int x = 0; x < D / 64; x++) {
-            vv[4 * x + 0] = t.v[r][x].x;
-            vv[4 * x + 1] = t.v[r][x].y;
-            vv[4 * x + 2] = t.v[r][x].z;
-            vv[4 * x + 3] = t.v[r][x].w;
-        }
-    } else {
-        const float d = f16_bits_to_f32(t.vhdr[r]), dmin = f16_bits_to_f32(t.vhdr[r] >> 16);
-        if constexpr (D == 64)
-            q4_dequant4(t.v[r], d, dmin, vv);
-        else
-            q4_dequant8(t.v[r], d, dmin, vv);
+    for (int x = 0; x < D / 64; x++) {
+        vv[4 * x + 0] = t.v[r][x].x;
+        vv[4 * x + 1] = t.v[r][x].y;
+        vv[4 * x + 2] = t.v[r][x].z;
+        vv[4 * x + 3] = t.v[r][x].w;
     }
 }
 
@@ -363,6 +351,42 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
             s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, s, 0, 0, 0);
+        }
+    } else if constexpr (KVT == NYION_KV_Q4_20B) {
+        // k = d*nib + dmin per 32-element group g, so q.k = sum_g d*(nib.q)_g
+        // + dmin*sum(q_g): the nibbles are exact binary16 operands against q
+        // split into binary16 high and low parts (qv words as for binary16
+        // KV; qv[NC + g] = sum of head j's q over group g), one accumulator
+        // per group, then each row's d and dmin (headers of rows 4kq+r, from
+        // the lanes that loaded them).
+        floatx4 sg[D / 32];
+#pragma unroll
+        for (int g = 0; g < D / 32; g++) sg[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+        for (int x = 0; x < D / 16; x++) {
+            // nibbles e0..e3 of dims 16x + 4kq .. +3 as binary16 1024 + e, less 1024
+            const uint32_t w = t.kn[x];
+            const uint32_t p01 = (w & 0xfu) | ((w & 0xf0u) << 12);
+            const uint32_t p23 = ((w >> 8) & 0xfu) | ((w & 0xf000u) << 4);
+            const halfx2 h01 = __builtin_bit_cast(halfx2, p01 | 0x64006400u) - k1024;
+            const halfx2 h23 = __builtin_bit_cast(halfx2, p23 | 0x64006400u) - k1024;
+            const halfx4 kx = {h01[0], h01[1], h23[0], h23[1]};
+            const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
+            const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
+            sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, sg[x >> 1], 0, 0, 0);
+            sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, sg[x >> 1], 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int g = 0; g < D / 32; g++) {
+                const uint32_t h = __shfl(t.khdr, 16 * g + 4 * kq + r);
+                const float d = f16_bits_to_f32(h), dmin = f16_bits_to_f32(h >> 16);
+                acc = __builtin_fmaf(d, sg[g][r], __builtin_fmaf(dmin, qv[NC + g], acc));
+            }
+            s[r] = acc;
         }
     } else {
         float kv[NC];
@@ -424,6 +448,35 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
                                          : (vw[2][w] & 0xffffu) | (vw[3][w] << 16);
             st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(
                 pa, __builtin_bit_cast(halfx4, u32x2{b01, b23}), st.acc[z], 0, 0, 0);
+        }
+    } else if constexpr (KVT == NYION_KV_Q4_20B) {
+        // O += P.V on binary16 MFMAs: A = 32p rounded to binary16 (as for
+        // binary16 KV; 32p <= 2^13), B = V/32 split into binary16 high and low
+        // parts (V dequantised exactly as dequant_block, then scaled by 2^-5,
+        // which is exact and keeps d*15 + dmin <= 2^20 inside binary16 range)
+        const halfx4 pa = {(_Float16)(32.f * pr[0]), (_Float16)(32.f * pr[1]), (_Float16)(32.f * pr[2]),
+                           (_Float16)(32.f * pr[3])};
+        float dv[4], mv[4];
+        bool ok[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            dv[r] = f16_bits_to_f32(t.vhdr[r]) * 0.03125f;
+            mv[r] = f16_bits_to_f32(t.vhdr[r] >> 16) * 0.03125f;
+            ok[r] = !MASKED || ((mask >> (4 * kq + r)) & 1u);
+        }
+#pragma unroll
+        for (int z = 0; z < DPL; z++) {  // element z: nibble z of the lane's word
+            halfx4 vh, vl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // masked rows may hold uninitialised slots: keep NaN out
+                const float v = ok[r] ? q4_dequant(dv[r], mv[r], (t.v[r] >> (4 * z)) & 0xfu) : 0.f;
+                vh[r] = (_Float16)v;
+                vl[r] = (_Float16)(v - (float)vh[r]);
+            }
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vh, st.acc[z], 0, 0, 0);
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vl, st.acc[z], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     } else {
 #pragma unroll
@@ -750,12 +803,14 @@ __device__ __forceinline__ int sload(const int* p) { return __builtin_amdgcn_rea
 // Occupancy target, which bounds the registers the compiler may use: two
 // workgroups (8 wavefronts) per CU, except f32 KV at head_dim 128, whose two
 // register-resident 16-token tiles alone take 128 VGPRs per lane (one), and
-// the smaller binary16 and 4-bit tiles at head_dim 64 (three).  Two tiles of
-// loads in flight per wavefront at this occupancy keep ~32 MB of f32 reads
-// outstanding, more than HBM latency x bandwidth.
+// the smaller binary16 tiles at head_dim 64 (three).  Two tiles of loads in
+// flight per wavefront at this occupancy keep ~32 MB of f32 reads
+// outstanding, more than HBM latency x bandwidth.  The 4-bit kernels keep
+// two: at three their binary16 products spill, and the 131072-token window
+// runs 10 % faster at two.
 template <int D, int KVT>
 constexpr int decode_waves_per_eu() {
-    return (D == 128 && KVT == NYION_KV_F32) ? 1 : (D == 64 && KVT != NYION_KV_F32) ? 3 : 2;
+    return (D == 128 && KVT == NYION_KV_F32) ? 1 : (D == 64 && KVT == NYION_KV_F16) ? 3 : 2;
 }
 
 template <int D, int KVT, bool ALIGNED, bool TRACK>
@@ -899,7 +954,8 @@ void decode_kernel(DecodeArgs a) {
         const int head0 = kvh * a.group + hg * 16;
 
         // Q operand (B of the QK product): head j, dims by qk_dim.
-        float qv[NC];
+        // Q4-20B: NC + D/32 values, the group sums of head j's q after the NC
+        float qv[KVT == NYION_KV_Q4_20B ? NC + D / 32 : NC];
         {
             const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
             const bool ok = j < g_local;
@@ -913,7 +969,20 @@ void decode_kernel(DecodeArgs a) {
                 qv[4 * i + 2] = r4.z;
                 qv[4 * i + 3] = r4.w;
             }
-            if constexpr (KVT == NYION_KV_F16) {
+            if constexpr (KVT == NYION_KV_Q4_20B) {
+                // sum of head j's q over each 32-element group (steps 2g, 2g+1
+                // of every quad kq)
+#pragma unroll
+                for (int g = 0; g < D / 32; g++) {
+                    float sum = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sum += qv[8 * g + i];
+                    sum += __shfl_xor(sum, 16);
+                    sum += __shfl_xor(sum, 32);
+                    qv[NC + g] = sum;
+                }
+            }
+            if constexpr (KVT == NYION_KV_F16 || KVT == NYION_KV_Q4_20B) {
                 // words 4x, 4x+1: the four values as binary16; 4x+2, 4x+3: the
                 // binary16 residuals.  |q| >= 65520 rounds the high part to
                 // infinity: reported through the status word.
