@@ -73,8 +73,8 @@ const char* nyion_version(void);
 /* Range report of the current device.  Kernels that carry an input in a
  * narrower format than the reference's f32 record, in a per-device sticky
  * word, when an input does not fit it: prefill's V (binary16 in the P.V
- * product: |v| >= 65520 or infinite) and binary16-KV decode's q (binary16
- * high part: |q| >= 65520).  This call orders itself after the work on
+ * product: |v| >= 65520 or infinite) and the q of decode over binary16 or
+ * Q4-20B pools (binary16 high part: |q| >= 65520).  This call orders itself after the work on
  * `stream`, waits for it, takes (reads and clears) the word and returns
  * NYION_OK, or NYION_ERR_RANGE with nyion_last_error() naming what
  * overflowed since the last take.  The word is per device, not per stream:
@@ -166,10 +166,15 @@ void* gpu_graph_create_attention_half(const float* d_q, const uint16_t* d_k_cach
  *                           (none when global_stride <= 0), then the window
  *                           [window_start, valid_end], window_start =
  *                           valid_end-window+1 if valid_end > window else 0.
- *   kv_dtype Q4_20B       : K/V dequantised in registers exactly as
- *                           dequant_block (cache.rs:375-394).
- *   kv_dtype F16          : K/V binary16 rows widened exactly to f32 (the
- *                           same results as f32 pools holding those values).
+ *   kv_dtype Q4_20B       : the values of dequant_block (cache.rs:375-394):
+ *                           V dequantised exactly so, K's products taken
+ *                           per 32-element group as d*(nib.q) + dmin*sum(q);
+ *                           multiplied on binary16 matrix cores with q and V
+ *                           split into high and low parts and the weights
+ *                           rounded to binary16 (|q| < 65504).
+ *   kv_dtype F16          : K/V binary16 rows multiplied as stored, q split
+ *                           into binary16 high and low parts, the weights
+ *                           rounded to binary16 (|q| < 65504).
  * d_q, d_out: [batch][n_heads][head_dim] f32.  ctx_lens[batch] (>= 1);
  * q_pos[batch] or NULL (= ctx_len-1).  max_ctx: host upper bound of ctx_lens,
  * sizes the grid.  scale <= 0 means 1/sqrt(head_dim).

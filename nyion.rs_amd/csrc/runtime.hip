@@ -203,7 +203,7 @@ int nyion_take_status(nyion_stream_t stream) {
         msg += "prefill: a V value of magnitude >= 65520 (or infinite) does not fit the binary16 "
                "operand of the P.V product; rows attending to it are not valid. ";
     if (got & kRangeDecodeQ)
-        msg += "binary16-KV decode: a q value of magnitude >= 65520 overflows the binary16 high "
+        msg += "binary16 / Q4-20B KV decode: a q value of magnitude >= 65520 overflows the binary16 high "
                "part of q; the heads holding it are not valid. ";
     return set_error(NYION_ERR_RANGE, "%s", msg.c_str());
 }
