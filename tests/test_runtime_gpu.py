@@ -87,17 +87,19 @@ def test_prefill_reports_v_outside_binary16(gpu):
     assert nh.take_status() == (nh.OK, "")
 
 
-def test_binary16_decode_reports_q_outside_binary16(gpu):
-    pb = W.paged_batch([300, 77], kv_dtype=oracle.KV_F16, seed=9)
+@pytest.mark.parametrize("kvt", [oracle.KV_F16, oracle.KV_Q4])
+def test_binary16_decode_reports_q_outside_binary16(gpu, kvt):
+    """Decode over binary16 and Q4-20B pools splits q into binary16 parts."""
+    pb = W.paged_batch([300, 77], kv_dtype=kvt, seed=9)
     q = to_dev(pb.q)
     kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
     tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
     out = torch.empty_like(q)
     nh.take_status()
-    gpu.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 64, 16, kv_dtype=nh.KV_F16)
+    gpu.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 64, 16, kv_dtype=kvt)
     assert nh.take_status() == (nh.OK, "")
     q[1, 5, 3] = -1e5
-    gpu.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 64, 16, kv_dtype=nh.KV_F16)
+    gpu.paged_decode(q, kp, vp, tab, ctx, out, 32, 4, 64, 16, kv_dtype=kvt)
     rc, msg = nh.take_status()
     assert rc == nh.ERR_RANGE and "decode" in msg
     # f32 pools carry q as f32: nothing to report
