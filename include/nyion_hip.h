@@ -657,7 +657,10 @@ void  nyion_hma_destroy(void* hma);
 /* Same symbols and signatures as swamp-kernels/src/lib.rs:36-85,181-223.
  * Host pointers; null arguments or n <= 0 return silently, as there.
  * mojo_softmax_padic runs the Q16.16 pipeline of the reference's AVX-512
- * branch on the GPU (staged through device memory). */
+ * branch on the GPU and returns when probs is written; up to 2^20 logits are
+ * staged through a device array the library holds (8 MiB per device, calls
+ * on one device take turns), longer arrays through device memory allocated
+ * and freed by the call. */
 void  mojo_softmax_padic(const float* logits, float* probs, int n, float temperature);
 void* mojo_stokes_init(int head_dim);
 void  mojo_stokes_append(void* cache, int token_id, const float* key, const float* value,

@@ -23,11 +23,40 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
 
+// Staging for mojo_softmax_padic's host arrays: logits and probabilities of
+// up to kSoftmaxStage elements, one copy per device (the name is a host-side
+// stand-in: softmax_stage_ptr() looks its device address up once per device).
+constexpr int kSoftmaxStage = 1 << 20;
+static __device__ __align__(256) float softmax_stage[2 * kSoftmaxStage];
+
 namespace nyion {
+
+// Device address of this device's staging array and the lock that
+// serialises its users (the host-pointer call is synchronous).
+static float* softmax_stage_ptr(std::mutex** lock) {
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    static std::mutex locks[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    *lock = &locks[dev];
+    uintptr_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v) return (float*)v;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(softmax_stage));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        set_error(NYION_ERR_LAUNCH, "mojo_softmax_padic: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(e));
+        return nullptr;
+    }
+    cache[dev].store((uintptr_t)ptr, std::memory_order_relaxed);
+    return (float*)ptr;
+}
 
 __device__ __forceinline__ int32_t sat_i32(float x) {
     if (x != x) return 0;
@@ -134,23 +163,29 @@ void mojo_softmax_padic(const float* logits, float* probs, int n, float temperat
     if (!logits || !probs || n <= 0) return;
     clear_error();
     if (require_device() != NYION_OK) return;
-    float* d = nullptr;
-    if (hipMalloc(&d, 2 * (size_t)n * sizeof(float)) != hipSuccess) {
+    // up to kSoftmaxStage logits go through the device's staging array;
+    // longer arrays through device memory allocated for the call
+    std::mutex* lock = nullptr;
+    float* stage = n <= kSoftmaxStage ? softmax_stage_ptr(&lock) : nullptr;
+    if (n <= kSoftmaxStage && !stage) return;
+    std::unique_lock<std::mutex> held;
+    if (lock) held = std::unique_lock<std::mutex>(*lock);
+    float* d = stage;
+    if (!d && hipMalloc(&d, 2 * (size_t)n * sizeof(float)) != hipSuccess) {
         (void)hipGetLastError();
         set_error(NYION_ERR_OOM, "mojo_softmax_padic: hipMalloc failed");
         return;
     }
     float* dl = d;
-    float* dp = d + n;
-    if (hipMemcpy(dl, logits, (size_t)n * sizeof(float), hipMemcpyDefault) == hipSuccess &&
-        nyion_softmax_padic_dev(dl, dp, n, temperature, nullptr) == NYION_OK &&
-        hipMemcpy(probs, dp, (size_t)n * sizeof(float), hipMemcpyDefault) == hipSuccess) {
-        (void)hipFree(d);
-        return;
+    float* dp = d + (stage ? kSoftmaxStage : n);
+    const bool ok = hipMemcpy(dl, logits, (size_t)n * sizeof(float), hipMemcpyDefault) == hipSuccess &&
+                    nyion_softmax_padic_dev(dl, dp, n, temperature, nullptr) == NYION_OK &&
+                    hipMemcpy(probs, dp, (size_t)n * sizeof(float), hipMemcpyDefault) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        if (nyion_last_error()[0] == 0) set_error(NYION_ERR_LAUNCH, "mojo_softmax_padic: HIP copy failed");
     }
-    (void)hipGetLastError();
-    if (nyion_last_error()[0] == 0) set_error(NYION_ERR_LAUNCH, "mojo_softmax_padic: HIP copy failed");
-    (void)hipFree(d);
+    if (!stage) (void)hipFree(d);
 }
 
 void* mojo_stokes_init(int head_dim) {

@@ -43,6 +43,35 @@ def test_softmax_padic_vocab(gpu):
         assert np.count_nonzero(diff) <= max(2, n // 500), (n, np.count_nonzero(diff))
 
 
+def test_softmax_padic_staging_sizes_and_threads(gpu):
+    """Arrays up to 2^20 go through the library's staging array (back-to-back
+    calls of different sizes reuse it; two host threads take turns), longer
+    ones through memory allocated for the call."""
+    import threading
+    rng = np.random.default_rng(1)
+    cases = [((rng.standard_normal(n) * 3).astype(np.float32), t)
+             for n, t in [(1 << 20, 1.0), (300, 0.5), ((1 << 20) + 5000, 1.3), (70000, 1.0)]]
+    for x, t in cases:
+        got = gpu_softmax(gpu, x, t)
+        diff = np.abs(got - oracle.softmax_padic(x, t)) * 65536
+        assert diff.max() <= 2 and np.count_nonzero(diff) <= max(2, len(x) // 500), (len(x), diff.max())
+    results = {}
+
+    def worker(k):
+        x, t = cases[k % 2 * 3]  # the 2^20 case and the 70000 case, from two threads
+        results[k] = [gpu_softmax(gpu, x, t) for _ in range(3)]
+
+    ths = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    for k in range(2):
+        x, t = cases[k % 2 * 3]
+        ref = gpu_softmax(gpu, x, t)
+        assert all(np.array_equal(r, ref) for r in results[k])
+
+
 def test_softmax_padic_device_entry(gpu):
     x = torch.randn(1000, device="cuda") * 2
     p = torch.empty_like(x)
