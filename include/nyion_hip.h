@@ -298,7 +298,8 @@ int nyion_zone_kv_gather(const void* pool, int64_t pool_units, const int64_t* pa
  * / ops::attention_sparse semantics as documented there, reading K/V
  * through k_page_ptr / v_page_ptr's addressing (ops.rs:210, 221).
  * page_bases: [batch][max_pages_per_seq] int64; max_ctx must be covered by
- * the table (nyion_zone_page_id(max_ctx - 1) < max_pages_per_seq).  The
+ * the table (nyion_zone_page_id(max_ctx - 1) < max_pages_per_seq); each
+ * pool holds at least 32 rows (pool_units >= 32 * row).  The
  * workspace is sized by nyion_paged_decode_workspace_size with the same
  * arguments. */
 int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void* v_pool,

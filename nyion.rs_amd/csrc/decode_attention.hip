@@ -506,35 +506,56 @@ __device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, con
 }
 
 // Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
-// one block; valid rows [vlo, vhi].
+// one block; valid rows [vlo, vhi].  ZONE: the blocks are 32-token units of
+// zone pages (every zone page is a whole number of them, and a unit's rows
+// of one (layer, kv head) are consecutive); lane l holds the offset of row
+// (layer, kv head 0) of unit bi_first + l, low word in tblv, high in tblh
+// (-1: page absent).
 struct AlignedWalk {
     int base;        // lo & ~15
     int lo, hi;
     int bi_first;    // first block index of this wavefront's tiles
     int tblv;        // lane l: block id of block index bi_first + l (or -1)
+    int tblh;        // ZONE: high word of the lane's row offset
+    int kvh;         // ZONE: the kv head
     long long head_off;
 };
 
-template <int D, int KVT>
+constexpr int kZoneUnitLog2 = 5;  // zone walks: 32-token units
+
+template <int D, int KVT, bool ZONE = false>
 __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const AlignedWalk& w,
                                                     int tile, int j, int kq, long long& koff,
                                                     long long* voff, int* pos) {
     const int t0 = w.base + 16 * tile;
 #pragma unroll
     for (int r = 0; r < 4; r++) pos[r] = t0 + 4 * kq + r;
-    int blk = 0;
-    if (a.tables) blk = __builtin_amdgcn_readlane(w.tblv, (t0 >> a.bt_log2) - w.bi_first);
     const int vlo = max(w.lo - t0, 0);
     const int vhi = min(w.hi - t0, 15);
     uint32_t mask = (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
-    if (blk < 0) {  // block index past the table or block id out of range
-        blk = 0;
-        mask = 0;
-    }
     // rows of a paged pool are contiguous: the token stride is the row size
     constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
-    const long long base = (long long)blk * a.block_stride + w.head_off +
-                           (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
+    long long base;
+    if constexpr (ZONE) {
+        const int idx = (t0 >> kZoneUnitLog2) - w.bi_first;
+        const long long row = ((long long)__builtin_amdgcn_readlane(w.tblh, idx) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane(w.tblv, idx);
+        const int lg = zone_pos(t0).page_log2;  // uniform: a tile lies in one page
+        base = row + (long long)w.kvh * ((long long)TS << lg) + (long long)(t0 & 31) * TS;
+        if (row < 0) {  // page absent, misaligned or outside the pool: the
+            base = 0;   // loads read the pool's first rows (the host keeps at
+            mask = 0;   // least 32), and the tile is masked
+        }
+    } else {
+        int blk = 0;
+        if (a.tables) blk = __builtin_amdgcn_readlane(w.tblv, (t0 >> a.bt_log2) - w.bi_first);
+        if (blk < 0) {  // block index past the table or block id out of range
+            blk = 0;
+            mask = 0;
+        }
+        base = (long long)blk * a.block_stride + w.head_off +
+               (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
+    }
     koff = base + j * TS;
     const long long vbase = base + 4 * kq * TS;
 #pragma unroll
@@ -772,11 +793,12 @@ __device__ __forceinline__ int run_table_entry(const DecodeArgs& a, const int32_
     return blk;
 }
 
-template <int D, int KVT, bool TRACK>
+template <int D, int KVT, bool TRACK, bool ZONE = false>
 __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, const float* qv,
                                           const Extent& e, const int32_t* table, long long head_off,
                                           int first, int n, int lane, int j, int kq, float* srow,
-                                          bool have_pref = false, int tbl_pref = -1) {
+                                          bool have_pref = false, int tbl_pref = -1,
+                                          const ZoneMap* zone = nullptr, int kvh = 0) {
     for (int c0 = 0; c0 < n; c0 += 64) {
         const int f = first + c0;
         const int nc = min(64, n - c0);
@@ -790,10 +812,22 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         // the first run's entries may have been loaded ahead (a superset of
         // the run from the same first block index: entries past the run are
         // never read)
-        if (table) w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
+        w.tblh = 0;
+        w.kvh = kvh;
+        if constexpr (ZONE) {
+            // this run's 32-token units, one per lane
+            constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
+            const int u = w.bi_first + lane;
+            const int u_last = (w.base + 16 * (f + nc) - 1) >> kZoneUnitLog2;
+            const long long row = u <= u_last ? zone_row_offset(*zone, u << kZoneUnitLog2, 0, TS) : -1;
+            w.tblv = (int)(uint32_t)row;
+            w.tblh = (int)(row >> 32);
+        } else if (table) {
+            w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
+        }
         walk_tiles<D, KVT, TRACK>(st, a, qv, nc, j, kq, srow,
                                   [&](int i, long long& ko, long long* vo, int* pos) {
-                                      return aligned_offsets<D, KVT>(a, w, f + i, j, kq, ko, vo, pos);
+                                      return aligned_offsets<D, KVT, ZONE>(a, w, f + i, j, kq, ko, vo, pos);
                                   });
     }
 }
@@ -813,7 +847,7 @@ constexpr int decode_waves_per_eu() {
     return (D == 128 && KVT == NYION_KV_F32) ? 1 : (D == 64 && KVT == NYION_KV_F16) ? 3 : 2;
 }
 
-template <int D, int KVT, bool ALIGNED, bool TRACK>
+template <int D, int KVT, bool ALIGNED, bool TRACK, bool ZONE = false>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, KVT>())))
 void decode_kernel(DecodeArgs a) {
@@ -1031,11 +1065,18 @@ void decode_kernel(DecodeArgs a) {
             const int mt = e.main_tiles;
             const int me = min(wb, mt);
             if (wa < me)
-                walk_main<D, KVT, TRACK>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa,
-                                         me - wa, lane, j, kq, srow, pref, tbl_pref);
+                walk_main<D, KVT, TRACK, ZONE>(st, a, qv, e, m.table, (long long)kvh * a.head_stride, wa,
+                                               me - wa, lane, j, kq, srow, pref, tbl_pref, &m.zone, kvh);
             const int ga = max(wa, mt) - mt;
             const int gb = wb - mt;
-            if (ga < gb) {
+            if (ZONE && ga < gb) {
+                // zone pages: each global row through the zone arithmetic
+                walk_tiles<D, KVT, TRACK>(st, a, qv, gb - ga, j, kq, srow,
+                                          [&](int i, long long& ko, long long* vo, int* pos) {
+                                              return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (ga + i),
+                                                                            e.n_glob, true, j, kq, ko, vo, pos);
+                                          });
+            } else if (ga < gb) {
                 // the block ids of all this wavefront's globals in one batch
                 const GlobalBlocks gbk = load_global_blocks(a, e, m, 16 * ga, lane);
                 walk_tiles<D, KVT, TRACK>(st, a, qv, gb - ga, j, kq, srow,
@@ -1248,6 +1289,7 @@ struct DecodePlan {
     int kvt;
     bool aligned;
     bool track;
+    bool zone;         // zone pages on the aligned walk
 };
 
 static size_t ws_layout(int slots, int segments, int head_dim, size_t* ml_off, size_t* ctr_off) {
@@ -1307,6 +1349,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     pl.kvt = kvt;
     pl.aligned = aligned_path;
     pl.track = false;
+    pl.zone = false;
     pl.grid_bound = grid_for(chunk * per_seq, kMinWgTiles, kMaxGrid);
     // one sequence over at most one workgroup per segment: no partials
     if (batch == 1 && pl.grid_bound <= units) {
@@ -1336,14 +1379,14 @@ static int attach_workspace(DecodePlan& pl, void* ws, size_t ws_bytes) {
 
 // Workgroups of one kernel instance resident on the whole device (per
 // device, computed on first use there).
-template <int D, int KVT, bool AL, bool TR>
+template <int D, int KVT, bool AL, bool TR, bool ZN = false>
 static int resident_capacity() {
     static std::atomic<int> cache[kMaxDevices];
     return per_device_value(
         cache,
         [] {
             int per_cu = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL, TR>,
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<D, KVT, AL, TR, ZN>,
                                                              256, 0) != hipSuccess) {
                 (void)hipGetLastError();
                 return 0;
@@ -1365,10 +1408,10 @@ static int wg_tiles_for(long long total_tiles) {
 // dependent round trip and two barriers that the direct form skips.
 constexpr int kDirectMaxSegments = 64;
 
-template <int D, int KVT, bool AL, bool TR>
+template <int D, int KVT, bool AL, bool TR, bool ZN = false>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
     const int units = pl.a.n_kv_heads * pl.a.n_hg;
-    const int cap = resident_capacity<D, KVT, AL, TR>();
+    const int cap = resident_capacity<D, KVT, AL, TR, ZN>();
     for (int b0 = 0; b0 < pl.batch; b0 += pl.chunk) {
         const int nb = pl.batch - b0 < pl.chunk ? pl.batch - b0 : pl.chunk;
         DecodeArgs a = pl.a;
@@ -1402,13 +1445,15 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
                 grid = (int)(P * segs);
             }
         }
-        hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR>), dim3(grid), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR, ZN>), dim3(grid), dim3(256), 0, stream, a);
     }
 }
 
 template <int D, int KVT>
 static void launch_dkt(const DecodePlan& pl, hipStream_t stream) {
-    if (pl.track) {
+    if (pl.zone) {  // zone pages on the aligned walk (no tracked form)
+        launch_dk<D, KVT, true, false, true>(pl, stream);
+    } else if (pl.track) {
         if (pl.aligned)
             launch_dk<D, KVT, true, true>(pl, stream);
         else
@@ -1791,6 +1836,9 @@ int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void
     if ((rc = make_zone_map(zone, pool_units, max_pages_per_seq, n_layers, layer, n_kv_heads,
                             kv_dtype, "zone decode")) != NYION_OK)
         return rc;
+    if (pool_units < 32 * row_elems(head_dim, kv_dtype))
+        return set_error(NYION_ERR_INVALID, "zone decode: pools of %lld units hold less than 32 rows",
+                         (long long)pool_units);
     if (max_ctx <= 0 || zone_pos(max_ctx - 1).page >= max_pages_per_seq)
         return set_error(NYION_ERR_INVALID,
                          "zone decode: max_ctx %d needs %d pages per sequence, the table has %d",
@@ -1798,8 +1846,9 @@ int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void
     DecodePlan pl;
     if ((rc = plan_common(pl, batch, n_heads, n_kv_heads, head_dim, kv_dtype,
                           window_main_len(max_ctx, window), window > 0 && global_stride > 0,
-                          false, scale)) != NYION_OK)
+                          true, scale)) != NYION_OK)
         return rc;
+    pl.zone = true;  // the aligned walk over 32-token units of zone pages
     if ((rc = attach_workspace(pl, d_workspace, workspace_bytes)) != NYION_OK) return rc;
     DecodeArgs& a = pl.a;
     a.q = d_q;
@@ -1811,6 +1860,7 @@ int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void
     a.token_stride = (int)row_elems(head_dim, kv_dtype);
     a.page_bases = page_bases;
     a.zone = zone;
+    a.bt_log2 = kZoneUnitLog2;
     a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
     a.window = window;
     a.global_stride = global_stride;

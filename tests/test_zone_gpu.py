@@ -168,7 +168,8 @@ def expected_decode(q, zp, layer, n, q_pos, positions=None):
 
 
 @pytest.mark.parametrize("kv_dtype,hd", [(oracle.KV_F32, 64), (oracle.KV_Q4, 64),
-                                         (oracle.KV_F16, 64), (oracle.KV_F32, 128)])
+                                         (oracle.KV_F16, 64), (oracle.KV_F32, 128),
+                                         (oracle.KV_Q4, 128), (oracle.KV_F16, 128)])
 def test_zone_decode_full(gpu, kv_dtype, hd):
     ctx = [4100, 4500, 700]
     hq, hkv, n_layers, layer = 16, 2, 3, 1
@@ -221,6 +222,17 @@ def test_zone_decode_skips_absent_pages(gpu):
     keep = np.array([t for t in range(n) if not 160 <= t < 192], np.int32)
     assert_close(got[0], expected_decode(q[0], pools[0], 0, n, n - 1, positions=keep),
                  "absent page")
+
+
+def test_zone_decode_all_pages_absent_is_zero(gpu):
+    """Every page absent: every tile is masked (its loads read the pool's
+    first rows) and the output is zero, as for a sequence with nothing to
+    attend."""
+    pools, k, v, bases = zone_batch([700], 1, 2, 64, oracle.KV_F32, seed=60)
+    bases[:] = -1
+    q = np.random.default_rng(61).standard_normal((1, 8, 64)).astype(np.float32)
+    got = run_zone_decode(gpu, q, k, v, bases, 1, 0, [700], 2, oracle.KV_F32)
+    assert np.all(got == 0.0)
 
 
 def test_zone_decode_rejects_short_table(gpu):
