@@ -22,7 +22,7 @@
 //   S^T[64 keys][32 rows] = K . Q^T      v_mfma_f32_32x32x16_bf16, Q^T from
 //                                        registers (loaded once)
 //   online softmax per row (rows are lanes; 32 keys per lane per half), the
-//   running max moved only when a tile exceeds it by 2^8
+//   running max moved only when a half's weights against it grow too large
 //   O[32 rows][D] += P . V               v_mfma_f32_32x32x16_f16, A = P in
 //                                        fp16 converted in registers from the
 //                                        S^T accumulators, B = V^T from LDS
@@ -30,7 +30,7 @@
 // loads were issued a whole tile earlier) while the current one is consumed,
 // with one barrier per tile.
 //
-// fp16 for P and V keeps 11 significant bits (p <= 2^8 after the lazy max),
+// fp16 for P and V keeps 11 significant bits (p <= 2^14 after the lazy max),
 // so the P.V product stays within the f32 reference's tolerance; V must lie
 // within the fp16 range (|v| <= 65504).
 #include <math.h>
@@ -81,7 +81,11 @@ template <int D>
 constexpr int prefill_threads() {
     return D == 128 ? 512 : 256;
 }
-constexpr float kPrefillRescaleLog2 = 8.0f;
+// Largest sum of one lane's 16 softmax weights of a half that is used as
+// computed; above it the half's row max is taken and the weights redone.
+// Every weight enters the P.V product as binary16, so the limit stays well
+// below 65504.
+constexpr float kPrefillSumLimit = 16384.0f;
 
 // LDS tiles, padded by 16 bytes per row so that every lane's reads are one
 // base address plus compile-time offsets (no per-read address registers):
@@ -339,10 +343,9 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     };
 
     // Online softmax of half kb of the tile at key kt and O += P.V over its
-    // two 16-key k-steps (V^T from slot `vs`).  Lane holds row row0+j, keys
-    // kt + 32kb + 8(r/4) + 4h + r%4 in st[r].  The O rescale of a moved max
-    // comes after the exps, so that the softmax up to there has no branch
-    // and can interleave with the MFMAs issued before it.
+    // two 16-key k-steps (consume_half).  Lane holds row row0+j, keys
+    // kt + 32kb + 8(r/4) + 4h + r%4 in st[r].  The exps come before any
+    // branch, so they interleave with the MFMAs issued before them.
     // Causal / range mask of half kb of the tile at key kt: the key of
     // st[r] is kt + 32kb + 4h + c(r), c(r) = 8(r/4) + r%4, compared as the
     // constant c(r) against this lane's bounds.
@@ -355,18 +358,18 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
             st[r] = c <= hi && c >= lo ? st[r] : -INFINITY;
         }
     };
-    auto consume_half = [&](floatx16 st, const unsigned char* vs, int kb) {
-        float mt = -INFINITY;
+    // B operands of the PV product of half kb: V^T row 32dt + j, the 8 keys
+    // of k-step t = 2kb + t2.  They are read before the softmax that
+    // produces P, so the PV MFMAs do not wait on LDS.
+    auto load_vhalf = [&](const unsigned char* vs, int kb, halfx8 (&vb)[2][DT]) {
+        const unsigned char* vp = vs + j * L::VROW + 16 * h + 64 * kb;
 #pragma unroll
-        for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
-        mt = max_xor32(mt) * a.scale_log2;  // scale > 0: max commutes
-        // the running max (log2 units, scaled) moves only when some row's max
-        // exceeds it by more than 2^8, so most halves skip the O rescale
-        const bool moved = __any(mt > mrun + kPrefillRescaleLog2);
-        const float mnew = moved ? fmaxf(mrun, mt) : mrun;
-        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-        mrun = mnew;
-        lrun *= alpha;
+        for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                vb[t2][dt] = __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
+    };
+    auto consume_half = [&](floatx16 st, const halfx8 (&vb)[2][DT]) {
         // p = exp2(s*scale - m), one FMA + one exp per score, converted to
         // fp16 pairs; the row sum adds the same fp16 values the PV product
         // uses (v_dot2 against (1, 1)).  A operands of the PV product: k-step
@@ -374,27 +377,39 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
         halfx8 pa[2];
         const halfx2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
         float psum = 0.f;
+        auto exps = [&]() {
+            psum = 0.f;
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
+            for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e], a.scale_log2, -mrun));
-                const float p1 =
-                    __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e + 1], a.scale_log2, -mrun));
-                const halfx2 pp = {(_Float16)p0, (_Float16)p1};
-                psum = __builtin_amdgcn_fdot2(pp, one2, psum, false);
-                pa[t2][e] = pp[0];
-                pa[t2][e + 1] = pp[1];
-            }
-        lrun += psum;
-        // P and the row sum are needed only after the rescale branch, and
-        // the compiler would otherwise place the exps behind it, where no S
-        // MFMA is left to hide them; this empty use keeps them ahead of it
-        asm volatile("" : : "v"(pa[0]), "v"(pa[1]), "v"(lrun));
-        // B operands of the PV product: V^T row 32dt + j, the 8 keys of
-        // k-step t = 2kb + t2
-        const unsigned char* vp = vs + j * L::VROW + 16 * h + 64 * kb;
-        if (moved) {
+                for (int e = 0; e < 8; e += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e], a.scale_log2, -mrun));
+                    const float p1 =
+                        __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e + 1], a.scale_log2, -mrun));
+                    const halfx2 pp = {(_Float16)p0, (_Float16)p1};
+                    psum = __builtin_amdgcn_fdot2(pp, one2, psum, false);
+                    pa[t2][e] = pp[0];
+                    pa[t2][e + 1] = pp[1];
+                }
+        };
+        // The running max m (log2 units, scaled) is not recomputed per half:
+        // the exps run against the current m, and only when some lane's sum
+        // of p exceeds kPrefillSumLimit (so some p may be past it, up to an
+        // fp16 overflow) is the half's row max taken, m raised to it, O and
+        // the row sum rescaled and the exps redone.  Every kept p is then at
+        // most kPrefillSumLimit.  The first half of every row takes this
+        // path (m starts at -1e30, so its p are inf); a NaN sum (NaN inputs)
+        // does not, and propagates as in the f32 reference.
+        exps();
+        if (__any(psum > kPrefillSumLimit)) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
+            mt = max_xor32(mt) * a.scale_log2;  // scale > 0: max commutes
+            const float mnew = fmaxf(mrun, mt);
+            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 // O reg r of this lane is row 8(r/4) + 4h + r%4
@@ -402,17 +417,14 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
 #pragma unroll
                 for (int t = 0; t < DT; t++) o[t][r] *= ar;
             }
+            exps();
         }
+        lrun += psum;
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++) {
-            halfx8 vb[DT];
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
-                vb[dt] = __builtin_bit_cast(halfx8, *(const uint4*)(vp + 32 * dt * L::VROW + 32 * t2));
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[dt], o[dt], 0, 0, 0);
-        }
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t2], vb[t2][dt], o[dt], 0, 0, 0);
     };
     auto tile_masked = [&](int kt) {
         return (kt + BN > a.n) || (a.causal && kt + BN - 1 > row0) || kt < key_lo;
@@ -443,12 +455,15 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     auto step = [&](int it, bool masked) {
         const int kt = kt0 + it * BN;
         const unsigned char* vs = vslot0 + (it & 1) * L::VBYTES;
+        halfx8 vb[2][DT];
+        load_vhalf(vs, 0, vb);
         if (masked) mask_half(s0, kt, 0);
         floatx16 s1 = scores_half(kslot(it), 1);
-        consume_half(s0, vs, 0);
+        consume_half(s0, vb);
         s0 = scores_half(kslot(it + 1), 0);
+        load_vhalf(vs, 1, vb);
         if (masked) mask_half(s1, kt, 1);
-        consume_half(s1, vs, 1);
+        consume_half(s1, vb);
         // a slot past the last tile is written and never read
         stage_store_k<D>(kst, kslot(it + 2), tid);
         stage_store_v<D>(vst, vslot0 + ((it + 1) & 1) * L::VBYTES, tid);
@@ -469,8 +484,11 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
             mask_half(s0, kt, 0);
             mask_half(s1, kt, 1);
         }
-        consume_half(s0, vs, 0);
-        consume_half(s1, vs, 1);
+        halfx8 vb[2][DT];
+        load_vhalf(vs, 0, vb);
+        consume_half(s0, vb);
+        load_vhalf(vs, 1, vb);
+        consume_half(s1, vb);
     }
 
     // epilogue: divide by the row sums and store
