@@ -284,6 +284,47 @@ def test_tracked_split_and_window(gpu):
         assert np.all(imp[b][~mask] == 0.0)
 
 
+def _check_tracked(pb, out, imp, init=None):
+    assert_close(out, W.reference_decode(pb), "tracked out")
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, L - 1, pb.n_heads,
+                                      pb.n_kv_heads, pb.head_dim, importance=True)
+        got = imp[b] - (0.0 if init is None else init[b])
+        assert np.max(np.abs(got[:L] - ref_imp)) <= 1e-4 * pb.n_heads, f"importance b={b}"
+        assert np.all(got[L:] == 0.0), f"importance past the context b={b}"
+
+
+def test_tracked_calls_in_a_row_share_a_workspace(gpu):
+    """Three tracked calls in a row on one workspace (batch 1, then 3, then 1
+    at other lengths, so the split-K counters the previous call left at zero
+    are reused under another layout) each match the oracle, onto nonzero
+    importance arrays, with a clean status word."""
+    ws = gpu.alloc_workspace(gpu.decode_workspace_size(3, 32, 4, 64, 6000))
+    for lens, seed in (([4096], 11), ([5000, 64, 1777], 12), ([6000], 13)):
+        pb = W.paged_batch(lens, seed=seed)
+        q = to_dev(pb.q)
+        kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+        tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+        out = torch.full_like(q, float("nan"))
+        init = np.random.default_rng(seed).random((pb.batch, 6000 + 2))
+        imp = torch.from_numpy(init.copy()).cuda()
+        gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out, imp, pb.n_heads, pb.n_kv_heads,
+                                 pb.head_dim, pb.block_tokens, max_ctx=max(lens), workspace=ws)
+        assert gpu.take_status()[0] == 0
+        torch.cuda.synchronize()
+        _check_tracked(pb, out.cpu().numpy(), imp.cpu().numpy(), init)
+
+
+def test_tracked_large_batch(gpu):
+    """A batch with more segments than the direct partition takes (20 x 4
+    kv heads: the stream-K partition) through the tracked form."""
+    pb = W.paged_batch([97 * (i + 1) for i in range(20)], seed=14)
+    out, imp = run_tracked(gpu, pb)
+    assert gpu.take_status()[0] == 0
+    _check_tracked(pb, out, imp)
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd", [(8, 8, 64), (16, 8, 64), (32, 8, 128), (64, 4, 64),
                                              (32, 1, 128), (40, 2, 64)])
 def test_paged_head_shapes(gpu, n_heads, n_kv, hd):
