@@ -689,9 +689,11 @@ int nyion_stokes_read(const void* cache, float* keys, float* values, float* scor
  * positions; each tile's weights are exp(s - m) / d with the running (m, d)
  * after that tile (the output of earlier tiles is not rescaled), weights
  * below 1e-8 skipped.  window and global_stride are accepted and unused, as
- * in the reference.  The call copies its operands to device buffers it
- * allocates and frees (not a hot path: the reference has no caller), and
- * returns when out is written.  On an error out is left unchanged and
+ * in the reference.  The call copies its operands through a per-device
+ * 16 MiB staging array (calls on one device take turns); a call whose q,
+ * out, K/V rows up to the largest position and positions need more copies
+ * through device memory it allocates and frees for the call.  It returns
+ * when out is written.  On an error out is left unchanged and
  * nyion_last_error() says why. */
 void  sparse_attention_q4(uint64_t q, uint64_t k_q4, uint64_t v_q4, uint64_t positions, uint64_t out,
                           int n_heads, int head_dim, int n_sparse, int window, int global_stride);

@@ -9,18 +9,50 @@
 // denominator of the tiles seen so far (earlier tiles are not rescaled), with
 // weights below 1e-8 skipped.  Here the same arithmetic runs on the device:
 // the call copies q, the positions and the K/V rows up to the largest listed
-// position to device buffers it allocates, runs one wavefront per head
+// position to device buffers (a per-device staging array of kMojoStage
+// words, under a lock; a call that needs more allocates its buffers for the
+// call), runs one wavefront per head
 // (lane p scores tile position p; lane i accumulates output elements i,
 // i + 64, ... over the tile's positions in list order, as the reference's
 // loop does), and copies the output back.  It is not a hot path: the
 // reference has no caller of it.
 #include <math.h>
 
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
 
+// Staging for sparse_attention_q4's host arrays (q, out, K and V rows,
+// positions): 16 MiB of 4-byte words, one copy per device (the name is a
+// host-side stand-in: mojo_stage_ptr() looks its device address up once per
+// device).
+constexpr size_t kMojoStage = (size_t)1 << 22;
+static __device__ __align__(256) float mojo_stage[kMojoStage];
+
 namespace nyion {
+
+// Device address of this device's staging array and the lock that
+// serialises its users (the call is synchronous).
+static float* mojo_stage_ptr(std::mutex** lock) {
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    static std::mutex locks[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    *lock = &locks[dev];
+    uintptr_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v) return (float*)v;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(mojo_stage));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        set_error(NYION_ERR_LAUNCH, "sparse_attention_q4: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(e));
+        return nullptr;
+    }
+    cache[dev].store((uintptr_t)ptr, std::memory_order_relaxed);
+    return (float*)ptr;
+}
 
 // Element i of a row of f32 words (attention.mojo:74-83): the word holding
 // its byte is read as an integer, low nibble for even i.
@@ -125,19 +157,36 @@ static int mojo_sparse_impl(const float* q, const float* k_q4, const float* v_q4
     }
     const size_t row_bytes = (size_t)((head_dim + 31) / 32) * 20 * sizeof(float);
     const size_t q_bytes = (size_t)n_heads * head_dim * sizeof(float);
+    const size_t kv_bytes = n_sparse > 0 ? (size_t)(max_pos + 1) * row_bytes : 0;
+    const size_t pos_bytes = (size_t)n_sparse * sizeof(int32_t);
+    // the five arrays in 256-byte aligned pieces of the staging array when
+    // they fit it, else in buffers allocated for the call
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t stage_need = 2 * up(q_bytes) + 2 * up(kv_bytes) + up(pos_bytes);
+    std::mutex* lock = nullptr;
+    char* stage = stage_need <= kMojoStage * sizeof(float) ? (char*)mojo_stage_ptr(&lock) : nullptr;
+    if (stage_need <= kMojoStage * sizeof(float) && !stage) return NYION_ERR_LAUNCH;
+    std::unique_lock<std::mutex> held;
+    if (lock) held = std::unique_lock<std::mutex>(*lock);
     CallBuffers buf;
     void *dq = nullptr, *dout = nullptr, *dk = nullptr, *dv = nullptr, *dpos = nullptr;
-    if ((rc = buf.alloc(&dq, q_bytes)) != NYION_OK || (rc = buf.alloc(&dout, q_bytes)) != NYION_OK)
+    if (stage) {
+        dq = stage;
+        dout = stage + up(q_bytes);
+        dk = stage + 2 * up(q_bytes);
+        dv = stage + 2 * up(q_bytes) + up(kv_bytes);
+        dpos = stage + 2 * up(q_bytes) + 2 * up(kv_bytes);
+    } else if ((rc = buf.alloc(&dq, q_bytes)) != NYION_OK || (rc = buf.alloc(&dout, q_bytes)) != NYION_OK ||
+               (n_sparse > 0 && ((rc = buf.alloc(&dk, kv_bytes)) != NYION_OK ||
+                                 (rc = buf.alloc(&dv, kv_bytes)) != NYION_OK ||
+                                 (rc = buf.alloc(&dpos, pos_bytes)) != NYION_OK))) {
         return rc;
+    }
     NYION_CHECK_HIP(hipMemcpy(dq, q, q_bytes, hipMemcpyHostToDevice));
     if (n_sparse > 0) {
-        const size_t kv_bytes = (size_t)(max_pos + 1) * row_bytes;
-        if ((rc = buf.alloc(&dk, kv_bytes)) != NYION_OK || (rc = buf.alloc(&dv, kv_bytes)) != NYION_OK ||
-            (rc = buf.alloc(&dpos, (size_t)n_sparse * sizeof(int32_t))) != NYION_OK)
-            return rc;
         NYION_CHECK_HIP(hipMemcpy(dk, k_q4, kv_bytes, hipMemcpyHostToDevice));
         NYION_CHECK_HIP(hipMemcpy(dv, v_q4, kv_bytes, hipMemcpyHostToDevice));
-        NYION_CHECK_HIP(hipMemcpy(dpos, positions, (size_t)n_sparse * sizeof(int32_t), hipMemcpyHostToDevice));
+        NYION_CHECK_HIP(hipMemcpy(dpos, positions, pos_bytes, hipMemcpyHostToDevice));
     }
     const float scale = 1.0f / sqrtf((float)head_dim);
     hipLaunchKernelGGL(mojo_sparse_kernel, dim3((unsigned)n_heads), dim3(64), 0, nullptr, (const float*)dq,

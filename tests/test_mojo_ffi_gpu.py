@@ -49,3 +49,41 @@ def test_sparse_attention_q4_rejects_negative_position(gpu):
     q = np.ones((1, hd), np.float32)
     with pytest.raises(gpu.NyionError):
         gpu.sparse_attention_q4(q, k, k, np.array([0, -1], np.int32), 1, hd)
+
+
+def test_sparse_attention_q4_staging_sizes_and_threads(gpu):
+    """Calls whose arrays fit the library's 16 MiB staging array reuse it
+    (back to back, and from two host threads taking turns); a call whose K/V
+    rows up to the largest position do not fit (60000 rows of head_dim 64:
+    19.2 MB) runs on memory allocated for the call."""
+    import threading
+    hd = 64
+
+    def case(n_rows, n_sparse, n_heads, seed):
+        rng = np.random.default_rng(seed)
+        kq = oracle.mojo_q4_rows(rng.standard_normal((n_rows, hd)).astype(np.float32))
+        vq = oracle.mojo_q4_rows(rng.standard_normal((n_rows, hd)).astype(np.float32))
+        q = rng.standard_normal((n_heads, hd)).astype(np.float32)
+        pos = rng.integers(0, n_rows, n_sparse).astype(np.int32)
+        pos[-1] = n_rows - 1  # the copy reaches the last row
+        return q, kq, vq, pos, n_heads
+
+    cases = [case(60000, 100, 2, 1), case(20000, 300, 4, 2), case(64, 10, 1, 3)]
+    for q, kq, vq, pos, nh in cases:
+        got = gpu.sparse_attention_q4(q, kq, vq, pos, nh, hd)
+        check(got, oracle.mojo_sparse_attention_q4(q, kq, vq, pos, nh, hd))
+    results = {}
+
+    def worker(k):
+        q, kq, vq, pos, nh = cases[1 + k]
+        results[k] = [gpu.sparse_attention_q4(q, kq, vq, pos, nh, hd) for _ in range(3)]
+
+    ths = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    for k in range(2):
+        q, kq, vq, pos, nh = cases[1 + k]
+        ref = gpu.sparse_attention_q4(q, kq, vq, pos, nh, hd)
+        assert all(np.array_equal(r, ref) for r in results[k])
