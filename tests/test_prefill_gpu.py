@@ -62,6 +62,35 @@ def test_prefill_small_all_rows(gpu, n, hq, hkv, d):
     check(got, oracle_rows(q, k, v, rows), rows, f"prefill {n},{hq}/{hkv},{d}")
 
 
+@pytest.mark.parametrize("shape", ["rising", "falling", "wide"])
+def test_prefill_running_max_moves(gpu, shape):
+    """Scores that rise along the keys (every tile passes the running max by
+    far more than the weight-sum limit, so each half recomputes its
+    weights against a new max), fall (the first tile holds the max, later
+    weights underflow), or spread wide (random, scaled by 6): all rows
+    against the oracle."""
+    n, hq, hkv, d = 700, 4, 1, 64
+    rng = np.random.default_rng(17)
+    u = rng.standard_normal(d).astype(np.float32)
+    u /= np.linalg.norm(u)
+    t = np.arange(n, dtype=np.float32)
+    if shape == "wide":
+        q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=18)
+        q *= 6.0
+        k *= 6.0
+    else:
+        # score of key t for every query (scale 1/8 at head_dim 64):
+        # +-t / (2 ln 2) = +-0.72 t, i.e. 1.04 t in exp2 units, 33 per 32-key half
+        sign = 1.0 if shape == "rising" else -1.0
+        q = np.tile(u * 8.0, (n, hq, 1)).astype(np.float32)
+        k = (sign * 0.5 / np.log(2.0) * t[:, None, None] * u[None, None, :]).astype(np.float32)
+        k = np.repeat(k, hkv, axis=1)
+        v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    got = run_prefill(gpu, q, k, v)
+    rows = np.arange(n)
+    check(got, oracle_rows(q, k, v, rows), rows, f"running max {shape}")
+
+
 def test_prefill_non_causal(gpu):
     q, k, v = W.prefill_inputs(257, 8, 2, 128, seed=1)
     got = run_prefill(gpu, q, k, v, causal=False)
