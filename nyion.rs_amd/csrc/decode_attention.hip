@@ -402,9 +402,16 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         if (MASKED) sv[r] = ((mask >> (4 * kq + r)) & 1u) ? sv[r] : -1e30f;
     }
     if (TRACK && srow) {
+        const uint32_t mq = (mask >> (4 * kq)) & 0xfu;
+        if (mq == 0xfu && pos[3] == pos[0] + 3) {
+            // four consecutive positions: one store (dword alignment suffices)
+            typedef float floatx4u __attribute__((ext_vector_type(4), aligned(4)));
+            *(floatx4u*)(srow + pos[0]) = floatx4u{sv[0], sv[1], sv[2], sv[3]};
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            if ((mask >> (4 * kq + r)) & 1u) srow[pos[r]] = sv[r];
+            for (int r = 0; r < 4; r++)
+                if ((mq >> r) & 1u) srow[pos[r]] = sv[r];
+        }
     }
     float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mt = fmaxf(mt, __shfl_xor(mt, 16));
