@@ -1203,12 +1203,12 @@ void decode_kernel(DecodeArgs a) {
 // ops.rs:303-368: p in f32, accumulated in f64), for every attended t.
 // A workgroup takes 64 positions of one sequence; wavefront w sums heads
 // w, w+4, w+8, ... for its lane's position (so a thread evaluates n_heads/4
-// exponentials and divides), and the four partial sums are added in a fixed
-// order through LDS.
+// exponentials, each times the head's 1/l, staged once per workgroup), and
+// the four partial sums are added in a fixed order through LDS.
 constexpr int kImpPositions = 64;
 
 __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
-    constexpr int HB = 16;  // score loads issued together per thread
+    constexpr int HB = 8;  // score loads issued together per thread
     __shared__ float2 sml[256];
     __shared__ double part[4][kImpPositions];
     const int lane = threadIdx.x & 63;
@@ -1230,7 +1230,7 @@ __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* i
             float2 ml = float2{0.f, 1.f};
             if ((int)threadIdx.x < hn) {
                 const float* row = rows + (long long)(h0 + threadIdx.x) * a.scores_stride;
-                ml = float2{row[a.scores_stride - 2], row[a.scores_stride - 1]};
+                ml = float2{row[a.scores_stride - 2], 1.0f / row[a.scores_stride - 1]};
             }
             float sv[HB];
 #pragma unroll
@@ -1250,7 +1250,7 @@ __global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* i
                     const int hh = w + 4 * (k0 + k);
                     if (active && hh < hn) {
                         const float2 m = sml[hh];
-                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) / m.y);
+                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) * m.y);
                     }
                 }
             }
