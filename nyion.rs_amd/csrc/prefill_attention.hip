@@ -371,14 +371,14 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     };
     auto consume_half = [&](floatx16 st, const halfx8 (&vb)[2][DT]) {
         // p = exp2(s*scale - m), one FMA + one exp per score, converted to
-        // fp16 pairs; the row sum adds the same fp16 values the PV product
-        // uses (v_dot2 against (1, 1)).  A operands of the PV product: k-step
+        // fp16 pairs; the row sum adds the f32 values in two chains of plain
+        // adds (a v_dot2 sum of the fp16 pairs competes with the MFMAs for
+        // issue and measured 1-2 % slower).  A operands of the PV product: k-step
         // t2 of this half holds keys 16t2 + 8(e/4) + 4h + e%4 (e = 0..7).
         halfx8 pa[2];
-        const halfx2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
         float psum = 0.f;
         auto exps = [&]() {
-            psum = 0.f;
+            float sa = 0.f, sb = 0.f;
 #pragma unroll
             for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
@@ -386,11 +386,12 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
                     const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e], a.scale_log2, -mrun));
                     const float p1 =
                         __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * t2 + e + 1], a.scale_log2, -mrun));
-                    const halfx2 pp = {(_Float16)p0, (_Float16)p1};
-                    psum = __builtin_amdgcn_fdot2(pp, one2, psum, false);
-                    pa[t2][e] = pp[0];
-                    pa[t2][e + 1] = pp[1];
+                    sa += p0;
+                    sb += p1;
+                    pa[t2][e] = (_Float16)p0;
+                    pa[t2][e + 1] = (_Float16)p1;
                 }
+            psum = sa + sb;
         };
         // The running max m (log2 units, scaled) is not recomputed per half:
         // the exps run against the current m, and only when some lane's sum
