@@ -440,18 +440,22 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
     // tile it+1.  The iteration writes the staged K into the slot of tile
     // it-1 and the staged V into the other V slot (both last read one
     // iteration ago), issues the next global loads and synchronises once.
-    load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0, tid);
-    load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0, tid);
-    stage_store_k<D>(kst, kslot0, tid);
-    stage_store_v<D>(vst, vslot0, tid);
-    if (n_tiles > 1) {
-        load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + BN, tid);
-        stage_store_k<D>(kst, kslot0 + L::KBYTES, tid);
+    // Prologue: K and V of tile 0 and K of tile 1 in one round of loads,
+    // then K of tile 2 and V of tile 1 requested as soon as the staging
+    // registers are in LDS.
+    {
+        KStage<D> kst1;
+        load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0, tid);
+        load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0, tid);
+        if (n_tiles > 1) load_k_tile<D>(kst1, a, kbase, khbase, tok_stride, kt0 + BN, tid);
+        stage_store_k<D>(kst, kslot0, tid);
+        stage_store_v<D>(vst, vslot0, tid);
+        if (n_tiles > 1) stage_store_k<D>(kst1, kslot0 + L::KBYTES, tid);
     }
-    __syncthreads();
-    floatx16 s0 = scores_half(kslot0, 0);
     if (n_tiles > 2) load_k_tile<D>(kst, a, kbase, khbase, tok_stride, kt0 + 2 * BN, tid);
     if (n_tiles > 1) load_v_tile<D>(vst, a, vbase, vhbase, tok_stride, kt0 + BN, tid);
+    __syncthreads();
+    floatx16 s0 = scores_half(kslot0, 0);
 
     auto step = [&](int it, bool masked) {
         const int kt = kt0 + it * BN;
