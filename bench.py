@@ -23,9 +23,10 @@ block tables), gemv / gemv6 (Q4_K and Q6_K weight GEMV) and pool (paged KV pool
 with host spill).
 
 Timing: `ms_per_step` is the wall clock over exactly K calls bracketed by
-device synchronisation, after the W warm-up calls; before those, the headline
+device synchronisation, after the W warm-up calls; before those, each GPU
 workload's set-up runs its call back to back for ~60 ms, untimed, so the
-clock has left idle (`settle_calls` reports how many); per-call statistics (median, p10, p90) come from
+clock has left idle (`settle_calls` reports how many for the headline);
+per-call statistics (median, p10, p90) come from
 an event pair recorded around each of >= 20 further calls on the launching
 stream; `roofline.achieved` divides the algorithmic bytes (or FLOPs) of one
 launch by the mean launch duration over back-to-back calls timed with HIP
@@ -333,6 +334,7 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
             c()
 
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
+    settle(step, torch)
     ms = timed(step, steps, warmup, torch)
     pct_step = event_pcts(step, max(steps, 20), torch)
     reps = max(steps, 20) * L
@@ -391,6 +393,7 @@ def bench_c2_tracked(nh, torch, steps, seed=0):
         return step
 
     reps = max(steps // R, 5)
+    settle(lambda i: step_of(i % R, True)(), torch)
     us = [_graph_us(torch, step_of(r, True), reps) for r in range(R)]
     us_plain = [_graph_us(torch, step_of(r, False), reps) for r in range(R)]
     step_us, plain_us = float(np.mean(us)), float(np.mean(us_plain))
@@ -500,6 +503,7 @@ def bench_c4(nh, torch, steps, warmup, seed=0):
 
         n_pos = w + (128 if stride else 0)
         nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4 + B * (n_pos // bt + 8) * 4
+        settle(call, torch)
         ms = timed(call, max(steps, C4_R), warmup, torch)
         reps = max(steps, 2 * C4_R)
         us = event_mean(call, reps, torch) * 1e3
@@ -573,6 +577,7 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
                         block_tokens=bt)
 
     reps = max(20, steps)
+    settle(attn_kv, torch)
     ms_kv = timed(attn_kv, reps, max(2, warmup // 5), torch)
     us = event_mean(attn, reps, torch) * 1e3
     pct = event_pcts(attn, reps, torch)
@@ -632,6 +637,7 @@ def bench_c1(nh, torch, steps, warmup):
     def call(i):
         nh.attention_node(q, k, v, out, 32, 4, 128, 64, 128, scores=scores)
 
+    settle(call, torch)
     ms = timed(call, steps * 10, warmup, torch)
     us = event_mean(call, steps * 4, torch) * 1e3
     pct = event_pcts(call, max(steps, 20), torch)
