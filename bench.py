@@ -43,7 +43,9 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
+import threading
 import time
 
 import numpy as np
@@ -73,6 +75,9 @@ def parse():
                     help="GEMV section: issue the launches directly instead of replaying graphs")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 512 MiB device copy (PMC traffic calibration)")
+    ap.add_argument("--sustain", type=float, default=0.0,
+                    help="c5: also run the prefill back to back for this many seconds on the "
+                         "workload's inputs and on all-zero inputs, sampling power and clock")
     return ap.parse_args()
 
 
@@ -598,6 +603,78 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
                          "traffic": None, "mfma_busy_frac_counters": busy}}
 
 
+def _smi_sample():
+    """Socket power (W) and the mean graphics clock over the XCDs (MHz), from
+    a read-only `amd-smi metric -p -c --json`; None where unavailable."""
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True,
+                           text=True, timeout=30)
+        d = json.loads(r.stdout)
+        g = (d["gpu_data"] if isinstance(d, dict) else d)[0]
+        pw = g.get("power", {}).get("socket_power", {}).get("value")
+        clks = [v["clk"]["value"] for k, v in g.get("clock", {}).items()
+                if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)
+                and isinstance(v["clk"].get("value"), (int, float))]
+        return (float(pw) if isinstance(pw, (int, float)) else None,
+                float(np.mean(clks)) if clks else None)
+    except Exception:  # no tool or an unexpected format: the sample is missing
+        return None, None
+
+
+def bench_c5_sustained(nh, torch, seconds, seed=0):
+    """C5's prefill call back to back for `seconds` on the workload's N(0,1)
+    inputs, then on all-zero inputs of the same shape (the same instructions
+    with almost no data toggling), sampling socket power and graphics clock
+    over the second half of each run: under this load the package power cap,
+    not the instruction schedule, sets the clock."""
+    n, Hq, Hkv, D = 8192, 32, 8, 128
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((n, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((n, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((n, Hq, D), device="cuda")
+    flops = 4 * Hq * D * n * (n + 1) / 2
+    res = {}
+    for kind in ("randn", "zeros"):
+        if kind == "zeros":
+            q.zero_()
+            k.zero_()
+            v.zero_()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        samples, calls = [], 0
+        stop = threading.Event()
+        t0 = time.perf_counter()
+
+        def sampler():  # off the issuing thread, so the GPU's queue never drains
+            while not stop.wait(0.25):
+                if time.perf_counter() - t0 > seconds / 2:
+                    samples.append(_smi_sample())
+
+        th = threading.Thread(target=sampler, daemon=True)
+        th.start()
+        e0.record(st)
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(20):
+                nh.prefill_bf16(q, k, v, out, Hq, Hkv, D)
+            calls += 20
+            torch.cuda.synchronize()
+        e1.record(st)
+        torch.cuda.synchronize()
+        stop.set()
+        th.join()
+        us = e0.elapsed_time(e1) * 1e3 / calls
+        pw = [x[0] for x in samples if x[0] is not None]
+        mhz = [x[1] for x in samples if x[1] is not None]
+        res[kind] = {"us_per_call": round(us, 1), "calls": calls,
+                     "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                     "mfma_frac": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "socket_power_w": round(float(np.mean(pw)), 1) if pw else None,
+                     "gfx_clock_mhz": round(float(np.mean(mhz)), 1) if mhz else None,
+                     "samples": len(samples)}
+    return res
+
+
 def cpu_baseline_c5(seed=0, n_rows=256):
     """The reference's prefill: one decode call per row (executor.rs:132-137),
     timed on n_rows rows spread over the 8192 and scaled by attended keys."""
@@ -1029,6 +1106,9 @@ def main():
     if "c5" in only:
         log("causal prefill N=8192 with paged KV write")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
+        if args.sustain > 0:
+            log(f"causal prefill N=8192 sustained {args.sustain:.0f} s on N(0,1) and on zero inputs")
+            res["c5"]["sustained"] = bench_c5_sustained(nh, torch, args.sustain)
         torch.cuda.empty_cache()
     if "pool" in only:
         log("paged KV pool: cold-page round trips over the host link")
