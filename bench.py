@@ -365,7 +365,10 @@ def bench_c2_tracked(nh, torch, steps, seed=0):
     the executor's Full decode call, executor.rs:742-755): per layer the
     decode launch also stores the scores, and a second launch adds
     importance[t] = sum_h p_h[t] in f64.  Replayed from a HIP graph (no host
-    overhead), 3 rotated caches as for C2."""
+    overhead), 3 rotated caches as for C2.  Also timed pipelined: layer l's
+    launch also runs layer l-1's importance sum on workgroups past its
+    decode's (two scores buffers in turn), and one importance launch after
+    the last layer -- L + 1 launches instead of 2L, the same results."""
     L, ctx, Hq, Hkv, D, bt = 22, 4096, 32, 4, 64, 16
     R = 3
     nblk = ctx // bt
@@ -397,16 +400,33 @@ def bench_c2_tracked(nh, torch, steps, seed=0):
                                     workspace=ws)
         return step
 
+    scores2 = [torch.empty((1, Hq, ctx + 2), dtype=torch.float32, device="cuda") for _ in range(2)]
+
+    def step_pipelined(r):
+        def step():
+            for layer in range(L):
+                q, kp, vp, tab = sets[r * L + layer]
+                first = layer == 0
+                nh.paged_decode_tracked_pipelined(
+                    q, kp, vp, tab, ctx_t, out, scores2[layer % 2],
+                    None if first else scores2[(layer - 1) % 2], None if first else imp[layer - 1],
+                    Hq, Hkv, D, bt, max_ctx=ctx, workspace=ws)
+            nh.paged_decode_importance(ctx_t, scores2[(L - 1) % 2], imp[L - 1], Hq, max_ctx=ctx)
+        return step
+
     reps = max(steps // R, 5)
     settle(lambda i: step_of(i % R, True)(), torch)
     us = [_graph_us(torch, step_of(r, True), reps) for r in range(R)]
     us_plain = [_graph_us(torch, step_of(r, False), reps) for r in range(R)]
-    step_us, plain_us = float(np.mean(us)), float(np.mean(us_plain))
+    us_pipe = [_graph_us(torch, step_pipelined(r), reps) for r in range(R)]
+    step_us, plain_us, pipe_us = float(np.mean(us)), float(np.mean(us_plain)), float(np.mean(us_pipe))
     bytes_layer = 2 * ctx * Hkv * D * 4 + nblk * 4 + 2 * Hq * D * 4
     return {"timing": "graph replay" if USE_GRAPHS else "direct launches",
             "ms_per_step": step_us * 1e-3, "us_per_layer": step_us / L,
             "untracked_us_per_layer_same_timing": plain_us / L,
             "tracked_over_untracked": step_us / plain_us,
+            "pipelined_us_per_layer": pipe_us / L,
+            "pipelined_over_untracked": pipe_us / plain_us,
             "gbs": L * bytes_layer / (step_us * 1e-6) / 1e9, "bytes_per_layer": bytes_layer,
             "score_and_importance_bytes_per_layer": Hq * (ctx + 2) * 4 * 2 + (ctx + 2) * 8 * 2}
 

@@ -237,6 +237,53 @@ int nyion_paged_decode_attention_tracked(
     size_t workspace_bytes, float* d_scores, int scores_stride, double* d_importance,
     int importance_stride, nyion_stream_t stream);
 
+/* The two launches of nyion_paged_decode_attention_tracked as separate calls
+ * (no counterpart in the reference, whose attention_tracked is one CPU
+ * routine, ops.rs:283-401): for GPU executors that run the importance sum
+ * on a second stream, beside whatever follows the decode on the first (the
+ * next layer's decode leaves most CUs idle at small batch).
+ *   _scores: the tracked decode's first launch -- the same arguments and
+ *     results as the tracked call, less the importance.
+ *   _importance: the second -- importance[b][t] += sum over q heads of the
+ *     normalised probability of t, from d_scores as _scores left it, for
+ *     the positions the decode with the same ctx_lens, q_pos, window,
+ *     global_stride and max_ctx attended.
+ * Issued on one stream, _scores then _importance give the tracked call's
+ * results bit for bit.  On two streams the caller orders _importance after
+ * _scores (an event), and keeps d_scores unchanged until _importance has
+ * run (one scores buffer per call in flight). */
+int nyion_paged_decode_attention_scores(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, nyion_stream_t stream);
+int nyion_paged_decode_importance(const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                  int n_heads, int window, int global_stride, int max_ctx,
+                                  const float* d_scores, int scores_stride, double* d_importance,
+                                  int importance_stride, nyion_stream_t stream);
+
+/* Pipelined tracked decode (no counterpart in the reference): one launch
+ * that runs this call's decode with its scores, as
+ * nyion_paged_decode_attention_scores, and on workgroups past the decode's
+ * the importance sum of the previous call's scores d_prev_scores into
+ * d_prev_importance [batch][importance_stride >= max_ctx] -- the previous
+ * call being one with the same ctx_lens, q_pos, batch, n_heads, window,
+ * global_stride and max_ctx, such as the previous layer of the same decode
+ * step, and d_prev_scores a different buffer from d_scores with the same
+ * scores_stride.  d_prev_scores
+ * NULL: no importance sum (the first layer); after the last layer,
+ * nyion_paged_decode_importance sums its scores.  A step of L layers is then
+ * L + 1 launches instead of 2L, with results equal to the tracked call's,
+ * layer by layer, bit for bit. */
+int nyion_paged_decode_attention_tracked_pipelined(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, const float* d_prev_scores,
+    double* d_prev_importance, int importance_stride, nyion_stream_t stream);
+
 /* Decode over explicit position lists (ops::attention_fugu, ops.rs:445-541,
  * whose list is the sparse set plus DSPark positions; also the Mojo
  * sparse_attention_q4 FFI, swamp-gpu/src/mojo.rs:5).  Softmax over exactly

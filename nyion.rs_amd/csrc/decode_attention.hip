@@ -116,6 +116,14 @@ struct DecodeArgs {
     // page_bases + b * zone.n_pages; zone.page_base unused
     const int64_t* page_bases;
     ZoneMap zone;
+    int decode_grid;   // workgroups of the decode itself (the launch may add more)
+    // tracked decode, pipelined: the workgroups past decode_grid sum the
+    // importance of the previous call's scores (same sequences and lengths),
+    // imp_nx position blocks x imp_ny sequence strides over imp_batch sequences
+    const float* imp_scores;
+    double* imp_out;
+    int imp_stride;
+    int imp_nx, imp_ny, imp_batch;
 };
 
 // Sequences per launch: the per-sequence tile prefix sums live in LDS.
@@ -854,6 +862,81 @@ constexpr int decode_waves_per_eu() {
     return (D == 128 && KVT == NYION_KV_F32) ? 1 : (D == 64 && KVT == NYION_KV_F16) ? 3 : 2;
 }
 
+// Tracked decode, second pass: importance[b][t] += sum over q heads of the
+// normalised probability of position t (ops::attention_tracked,
+// ops.rs:303-368: p in f32, accumulated in f64), for every attended t.
+// A workgroup takes 64 positions of one sequence; wavefront w sums heads
+// w, w+4, w+8, ... for its lane's position (so a thread evaluates n_heads/4
+// exponentials, each times the head's 1/l, staged once per workgroup), and
+// the four partial sums are added in a fixed order through LDS.
+constexpr int kImpPositions = 64;
+// Sequence stride of the importance workgroups a pipelined decode launch
+// adds (each takes every kImpMaxSeqStride-th sequence).
+constexpr int kImpMaxSeqStride = 64;
+
+// One workgroup's share: positions bx*64 .. +63 of sequences by0, by0 + by_step,
+// ...; sml and part are LDS of 256 float2 and 4 x 64 double.
+__device__ __forceinline__ void importance_body(const DecodeArgs& a, double* imp, int imp_stride,
+                                                int bx, int by0, int by_step, float2* sml,
+                                                double (*part)[kImpPositions]) {
+    constexpr int HB = 8;  // score loads issued together per thread
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int t = bx * kImpPositions + lane;
+    const int tt = min(t, a.scores_stride - 3);  // in-row address for any thread
+    for (int b = by0; b < a.batch; b += by_step) {
+        const float* rows = a.scores + (long long)b * a.n_heads * a.scores_stride;
+        const Extent e = lane_extent<true>(a, b);
+        double* dst = imp + (long long)b * imp_stride + min(t, imp_stride - 1);
+        const double prev = w == 0 ? *dst : 0.0;  // requested with the other loads
+        double acc = 0.0;
+        const bool in_window = t >= e.lo && t <= e.hi;
+        const bool global = e.n_glob > 0 && t < e.n_glob * a.global_stride && t % a.global_stride == 0;
+        const bool active = in_window || global;
+        for (int h0 = 0; h0 < a.n_heads; h0 += 256) {
+            const int hn = min(256, a.n_heads - h0);
+            // (m, l) of this chunk's heads staged in LDS by vector loads
+            float2 ml = float2{0.f, 1.f};
+            if ((int)threadIdx.x < hn) {
+                const float* row = rows + (long long)(h0 + threadIdx.x) * a.scores_stride;
+                ml = float2{row[a.scores_stride - 2], 1.0f / row[a.scores_stride - 1]};
+            }
+            float sv[HB];
+#pragma unroll
+            for (int k = 0; k < HB; k++)
+                sv[k] = rows[(long long)(h0 + min(w + 4 * k, hn - 1)) * a.scores_stride + tt];
+            __syncthreads();  // the previous chunk's readers are done
+            if ((int)threadIdx.x < hn) sml[threadIdx.x] = ml;
+            __syncthreads();
+            for (int k0 = 0; 4 * k0 < hn; k0 += HB) {
+                if (k0 > 0) {
+#pragma unroll
+                    for (int k = 0; k < HB; k++)
+                        sv[k] = rows[(long long)(h0 + min(w + 4 * (k0 + k), hn - 1)) * a.scores_stride + tt];
+                }
+#pragma unroll
+                for (int k = 0; k < HB; k++) {
+                    const int hh = w + 4 * (k0 + k);
+                    if (active && hh < hn) {
+                        const float2 m = sml[hh];
+                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) * m.y);
+                    }
+                }
+            }
+        }
+        part[w][lane] = acc;
+        __syncthreads();
+        if (w == 0 && active) *dst = prev + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+        __syncthreads();  // part[] is reused by the next sequence
+    }
+}
+
+__global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
+    __shared__ float2 sml[256];
+    __shared__ double part[4][kImpPositions];
+    importance_body(a, imp, imp_stride, blockIdx.x, blockIdx.y, gridDim.y, sml, part);
+}
+
 template <int D, int KVT, bool ALIGNED, bool TRACK, bool ZONE = false>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, KVT>())))
@@ -868,6 +951,21 @@ void decode_kernel(DecodeArgs a) {
     __shared__ int sm_wsum[4];
     __shared__ int sm_last;
 
+    if constexpr (TRACK) {
+        if ((int)blockIdx.x >= a.decode_grid) {
+            // pipelined tracked decode: the previous call's importance sum
+            // (its scores are final, launches on one stream run in order)
+            // on workgroups past the decode's, in the merge buffer's LDS
+            const int k = (int)blockIdx.x - a.decode_grid;
+            DecodeArgs ia = a;
+            ia.scores = const_cast<float*>(a.imp_scores);
+            ia.batch = a.imp_batch;
+            float2* sml = reinterpret_cast<float2*>(&sm_acc[0][0][0]);
+            importance_body(ia, a.imp_out, a.imp_stride, k % a.imp_nx, k / a.imp_nx, a.imp_ny, sml,
+                            reinterpret_cast<double(*)[kImpPositions]>(sml + 256));
+            return;
+        }
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15;
@@ -918,12 +1016,12 @@ void decode_kernel(DecodeArgs a) {
         }
         // the host keeps batch * U * (tiles of the longest segment) below 2^31
         const int T = __builtin_amdgcn_readfirstlane(carry) * U;
-        c = (T + (int)gridDim.x - 1) / (int)gridDim.x;  // tiles per workgroup
+        c = (T + a.decode_grid - 1) / a.decode_grid;  // tiles per workgroup
         const int g0 = min((int)blockIdx.x * c, T);
         g1 = min(g0 + c, T);
 
         // sequences with nothing to attend to (ctx_len <= 0, q_pos < 0, empty list)
-        for (int bb = blockIdx.x; bb < a.batch; bb += gridDim.x) {
+        for (int bb = blockIdx.x; bb < a.batch; bb += a.decode_grid) {
             if (sload(&sm_pref[bb + 1]) != sload(&sm_pref[bb])) continue;
             float* o = a.out + (long long)bb * a.n_heads * D;
             for (int i = threadIdx.x; i < a.n_heads * D; i += 256) o[i] = 0.f;
@@ -1198,70 +1296,6 @@ void decode_kernel(DecodeArgs a) {
     }
 }
 
-// Tracked decode, second pass: importance[b][t] += sum over q heads of the
-// normalised probability of position t (ops::attention_tracked,
-// ops.rs:303-368: p in f32, accumulated in f64), for every attended t.
-// A workgroup takes 64 positions of one sequence; wavefront w sums heads
-// w, w+4, w+8, ... for its lane's position (so a thread evaluates n_heads/4
-// exponentials, each times the head's 1/l, staged once per workgroup), and
-// the four partial sums are added in a fixed order through LDS.
-constexpr int kImpPositions = 64;
-
-__global__ __launch_bounds__(256) void importance_kernel(DecodeArgs a, double* imp, int imp_stride) {
-    constexpr int HB = 8;  // score loads issued together per thread
-    __shared__ float2 sml[256];
-    __shared__ double part[4][kImpPositions];
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int t = blockIdx.x * kImpPositions + lane;
-    const int tt = min(t, a.scores_stride - 3);  // in-row address for any thread
-    for (int b = blockIdx.y; b < a.batch; b += gridDim.y) {
-        const float* rows = a.scores + (long long)b * a.n_heads * a.scores_stride;
-        const Extent e = lane_extent<true>(a, b);
-        double* dst = imp + (long long)b * imp_stride + min(t, imp_stride - 1);
-        const double prev = w == 0 ? *dst : 0.0;  // requested with the other loads
-        double acc = 0.0;
-        const bool in_window = t >= e.lo && t <= e.hi;
-        const bool global = e.n_glob > 0 && t < e.n_glob * a.global_stride && t % a.global_stride == 0;
-        const bool active = in_window || global;
-        for (int h0 = 0; h0 < a.n_heads; h0 += 256) {
-            const int hn = min(256, a.n_heads - h0);
-            // (m, l) of this chunk's heads staged in LDS by vector loads
-            float2 ml = float2{0.f, 1.f};
-            if ((int)threadIdx.x < hn) {
-                const float* row = rows + (long long)(h0 + threadIdx.x) * a.scores_stride;
-                ml = float2{row[a.scores_stride - 2], 1.0f / row[a.scores_stride - 1]};
-            }
-            float sv[HB];
-#pragma unroll
-            for (int k = 0; k < HB; k++)
-                sv[k] = rows[(long long)(h0 + min(w + 4 * k, hn - 1)) * a.scores_stride + tt];
-            __syncthreads();  // the previous chunk's readers are done
-            if ((int)threadIdx.x < hn) sml[threadIdx.x] = ml;
-            __syncthreads();
-            for (int k0 = 0; 4 * k0 < hn; k0 += HB) {
-                if (k0 > 0) {
-#pragma unroll
-                    for (int k = 0; k < HB; k++)
-                        sv[k] = rows[(long long)(h0 + min(w + 4 * (k0 + k), hn - 1)) * a.scores_stride + tt];
-                }
-#pragma unroll
-                for (int k = 0; k < HB; k++) {
-                    const int hh = w + 4 * (k0 + k);
-                    if (active && hh < hn) {
-                        const float2 m = sml[hh];
-                        acc += (double)(__builtin_amdgcn_exp2f(sv[k] - m.x) * m.y);
-                    }
-                }
-            }
-        }
-        part[w][lane] = acc;
-        __syncthreads();
-        if (w == 0 && active) *dst = prev + ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
-        __syncthreads();  // part[] is reused by the next sequence
-    }
-}
-
 __global__ void fill_zero_kernel(int* p, long long n) {
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
          i += (long long)gridDim.x * blockDim.x)
@@ -1297,6 +1331,8 @@ struct DecodePlan {
     bool aligned;
     bool track;
     bool zone;         // zone pages on the aligned walk
+    int imp_max_ctx;   // > 0: the first launch also sums the importance of
+                       // a.imp_scores (pipelined tracked decode)
 };
 
 static size_t ws_layout(int slots, int segments, int head_dim, size_t* ml_off, size_t* ctr_off) {
@@ -1357,6 +1393,7 @@ static int plan_common(DecodePlan& pl, int batch, int n_heads, int n_kv_heads, i
     pl.aligned = aligned_path;
     pl.track = false;
     pl.zone = false;
+    pl.imp_max_ctx = 0;
     pl.grid_bound = grid_for(chunk * per_seq, kMinWgTiles, kMaxGrid);
     // one sequence over at most one workgroup per segment: no partials
     if (batch == 1 && pl.grid_bound <= units) {
@@ -1452,7 +1489,18 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
                 grid = (int)(P * segs);
             }
         }
-        hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR, ZN>), dim3(grid), dim3(256), 0, stream, a);
+        a.decode_grid = grid;
+        long long launch = grid;
+        if (TR && b0 == 0 && pl.imp_max_ctx > 0) {
+            // the previous call's importance: all its sequences, from this
+            // first launch (its ctx_lens / q_pos are not offset)
+            a.imp_nx = (pl.imp_max_ctx + kImpPositions - 1) / kImpPositions;
+            a.imp_ny = pl.batch < kImpMaxSeqStride ? pl.batch : kImpMaxSeqStride;
+            a.imp_batch = pl.batch;
+            launch += (long long)a.imp_nx * a.imp_ny;
+        }
+        hipLaunchKernelGGL((decode_kernel<D, KVT, AL, TR, ZN>), dim3((unsigned)launch), dim3(256), 0,
+                           stream, a);
     }
 }
 
@@ -1599,6 +1647,20 @@ void* decode_scratch_ptr() {
 
 }  // namespace nyion
 
+// The tracked form's second launch over the scores (and per-row max and
+// denominator) the decode stored: `a` carries the attended sets (mode,
+// window, globals, lengths) and the scores buffer.
+static int launch_importance(const DecodeArgs& a, int batch, int max_ctx, double* d_importance,
+                             int importance_stride, hipStream_t stream) {
+    DecodeArgs ia = a;
+    ia.batch = batch;
+    const unsigned gy = batch < 65535 ? (unsigned)batch : 65535u;
+    hipLaunchKernelGGL(importance_kernel,
+                       dim3((unsigned)((max_ctx + kImpPositions - 1) / kImpPositions), gy), dim3(256), 0,
+                       stream, ia, d_importance, importance_stride);
+    return check_launch("decode importance");
+}
+
 // Shared body of the paged decode entry points; scores/imp non-null selects
 // the tracked form; use_scratch takes the split-K workspace from the
 // library's scratch array (d_workspace is ignored) and clears its counters.
@@ -1610,7 +1672,8 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
                                int max_ctx, float scale, float* d_out, void* d_workspace,
                                size_t workspace_bytes, float* d_scores, int scores_stride,
                                double* d_importance, int importance_stride, hipStream_t stream,
-                               bool use_scratch = false) {
+                               bool use_scratch = false, bool with_importance = true,
+                               const float* d_prev_scores = nullptr) {
     clear_error();
     int rc;
     if ((rc = require_device()) != NYION_OK) return rc;
@@ -1630,15 +1693,29 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
                          max_ctx);
     const bool track = d_scores != nullptr;
     if (track) {
-        if (!d_importance)
+        if (with_importance && !d_importance)
             return set_error(NYION_ERR_INVALID, "tracked decode: null importance");
-        if ((long long)scores_stride < (long long)max_ctx + 2 || importance_stride < max_ctx)
+        if ((long long)scores_stride < (long long)max_ctx + 2 ||
+            (with_importance && importance_stride < max_ctx))
             return set_error(NYION_ERR_INVALID,
                              "tracked decode: scores_stride %d must be >= max_ctx + 2 and "
                              "importance_stride %d >= max_ctx (%d)",
                              scores_stride, importance_stride, max_ctx);
-        if (!aligned(d_scores, 4) || !aligned(d_importance, 8))
+        if (!aligned(d_scores, 4) || (with_importance && !aligned(d_importance, 8)))
             return set_error(NYION_ERR_INVALID, "tracked decode: buffer alignment");
+        if (d_prev_scores) {
+            if (!d_importance || importance_stride < max_ctx)
+                return set_error(NYION_ERR_INVALID,
+                                 "pipelined tracked decode: the previous call's importance needs "
+                                 "d_prev_importance with importance_stride %d >= max_ctx (%d)",
+                                 importance_stride, max_ctx);
+            if (!aligned(d_prev_scores, 4) || !aligned(d_importance, 8))
+                return set_error(NYION_ERR_INVALID, "pipelined tracked decode: buffer alignment");
+            if (d_prev_scores == d_scores)
+                return set_error(NYION_ERR_INVALID,
+                                 "pipelined tracked decode: the previous scores buffer is this "
+                                 "call's scores buffer");
+        }
     }
     const bool aligned_path = block_tokens >= 16;
     DecodePlan pl;
@@ -1687,14 +1764,14 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
     a.global_stride = global_stride;
     a.scores = d_scores;
     a.scores_stride = scores_stride;
-    if ((rc = launch_plan(pl, stream)) != NYION_OK || !track) return rc;
-    DecodeArgs ia = a;
-    ia.batch = batch;
-    const unsigned gy = batch < 65535 ? (unsigned)batch : 65535u;
-    hipLaunchKernelGGL(importance_kernel,
-                       dim3((unsigned)((max_ctx + kImpPositions - 1) / kImpPositions), gy), dim3(256), 0,
-                       stream, ia, d_importance, importance_stride);
-    return check_launch("decode importance");
+    if (track && d_prev_scores) {
+        pl.imp_max_ctx = max_ctx;
+        a.imp_scores = d_prev_scores;
+        a.imp_out = d_importance;
+        a.imp_stride = importance_stride;
+    }
+    if ((rc = launch_plan(pl, stream)) != NYION_OK || !track || !with_importance) return rc;
+    return launch_importance(a, batch, max_ctx, d_importance, importance_stride, stream);
 }
 
 // Plan of the attention node over scratch_bytes of its scores buffer.  The
@@ -1767,6 +1844,74 @@ int nyion_paged_decode_attention_tracked(
                                num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
                                d_workspace, workspace_bytes, d_scores, scores_stride, d_importance,
                                importance_stride, (hipStream_t)stream);
+}
+
+int nyion_paged_decode_attention_scores(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, nyion_stream_t stream) {
+    if (!d_scores) {
+        clear_error();
+        return set_error(NYION_ERR_INVALID, "tracked decode: null scores buffer");
+    }
+    return paged_decode_common(d_q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                               q_pos, batch, n_heads, n_kv_heads, head_dim, block_tokens,
+                               num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
+                               d_workspace, workspace_bytes, d_scores, scores_stride, nullptr, 0,
+                               (hipStream_t)stream, false, false);
+}
+
+int nyion_paged_decode_attention_tracked_pipelined(
+    const float* d_q, const void* k_pool, const void* v_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* ctx_lens, const int32_t* q_pos, int batch, int n_heads,
+    int n_kv_heads, int head_dim, int block_tokens, int num_blocks, int kv_dtype, int window,
+    int global_stride, int max_ctx, float scale, float* d_out, void* d_workspace,
+    size_t workspace_bytes, float* d_scores, int scores_stride, const float* d_prev_scores,
+    double* d_prev_importance, int importance_stride, nyion_stream_t stream) {
+    if (!d_scores) {
+        clear_error();
+        return set_error(NYION_ERR_INVALID, "tracked decode: null scores buffer");
+    }
+    return paged_decode_common(d_q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                               q_pos, batch, n_heads, n_kv_heads, head_dim, block_tokens,
+                               num_blocks, kv_dtype, window, global_stride, max_ctx, scale, d_out,
+                               d_workspace, workspace_bytes, d_scores, scores_stride,
+                               d_prev_importance, importance_stride, (hipStream_t)stream, false,
+                               false, d_prev_scores);
+}
+
+int nyion_paged_decode_importance(const int32_t* ctx_lens, const int32_t* q_pos, int batch,
+                                  int n_heads, int window, int global_stride, int max_ctx,
+                                  const float* d_scores, int scores_stride, double* d_importance,
+                                  int importance_stride, nyion_stream_t stream) {
+    clear_error();
+    int rc;
+    if ((rc = require_device()) != NYION_OK) return rc;
+    if (!ctx_lens || !d_scores || !d_importance)
+        return set_error(NYION_ERR_INVALID, "decode importance: null ctx_lens/scores/importance");
+    if (batch <= 0 || n_heads <= 0 || max_ctx <= 0)
+        return set_error(NYION_ERR_INVALID, "decode importance: batch/heads/max_ctx must be positive");
+    if ((long long)scores_stride < (long long)max_ctx + 2 || importance_stride < max_ctx)
+        return set_error(NYION_ERR_INVALID,
+                         "decode importance: scores_stride %d must be >= max_ctx + 2 and "
+                         "importance_stride %d >= max_ctx (%d)",
+                         scores_stride, importance_stride, max_ctx);
+    if (!aligned(d_scores, 4) || !aligned(d_importance, 8))
+        return set_error(NYION_ERR_INVALID, "decode importance: buffer alignment");
+    // the attended sets exactly as the decode call with these arguments saw them
+    DecodeArgs a{};
+    a.n_heads = n_heads;
+    a.max_len = window_main_len(max_ctx, window);
+    a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
+    a.window = window;
+    a.global_stride = global_stride;
+    a.ctx_lens = ctx_lens;
+    a.q_pos = q_pos;
+    a.scores = const_cast<float*>(d_scores);
+    a.scores_stride = scores_stride;
+    return launch_importance(a, batch, max_ctx, d_importance, importance_stride, (hipStream_t)stream);
 }
 
 size_t nyion_paged_decode_positions_workspace_size(int batch, int n_heads, int n_kv_heads,

@@ -83,6 +83,14 @@ SIGNATURES = {
     "nyion_paged_decode_attention_tracked": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32,
                                                    i32, i32, i32, i32, i32, i32, f32, vp, vp, sz,
                                                    vp, i32, vp, i32, vp]),
+    "nyion_paged_decode_attention_scores": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32,
+                                                  i32, i32, i32, i32, i32, i32, f32, vp, vp, sz,
+                                                  vp, i32, vp]),
+    "nyion_paged_decode_importance": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, i32, vp, i32, vp]),
+    "nyion_paged_decode_attention_tracked_pipelined": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32,
+                                                             i32, i32, i32, i32, i32, i32, i32, i32,
+                                                             f32, vp, vp, sz, vp, i32, vp, vp, i32,
+                                                             vp]),
     "nyion_paged_decode_positions_workspace_size": (sz, [i32, i32, i32, i32, i32]),
     "nyion_paged_decode_attention_positions": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
                                                      i32, i32, i32, i32, i32, f32, vp, vp, sz,
@@ -330,6 +338,69 @@ def paged_decode_tracked(q, k_pool, v_pool, block_tables, ctx_lens, out, importa
         scores.shape[-1], ptr(importance), importance.shape[-1], stream_handle(stream))
     check(rc, "nyion_paged_decode_attention_tracked")
     return workspace
+
+
+def paged_decode_scores(q, k_pool, v_pool, block_tables, ctx_lens, out, scores, n_heads,
+                        n_kv_heads, head_dim, block_tokens, kv_dtype=KV_F32, window=0,
+                        global_stride=0, max_ctx=None, q_pos=None, scale=0.0, workspace=None,
+                        stream=None):
+    """The tracked decode's first launch: paged_decode plus the scores (and each
+    row's max and denominator) in scores [B][Hq][>= max_ctx + 2] f32."""
+    B = q.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = load().nyion_paged_decode_attention_scores(
+        ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1], ptr(ctx_lens),
+        ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens, k_pool.shape[0], kv_dtype,
+        window, global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes, ptr(scores),
+        scores.shape[-1], stream_handle(stream))
+    check(rc, "nyion_paged_decode_attention_scores")
+    return workspace
+
+
+def paged_decode_tracked_pipelined(q, k_pool, v_pool, block_tables, ctx_lens, out, scores,
+                                   prev_scores, prev_importance, n_heads, n_kv_heads, head_dim,
+                                   block_tokens, kv_dtype=KV_F32, window=0, global_stride=0,
+                                   max_ctx=None, q_pos=None, scale=0.0, workspace=None,
+                                   stream=None):
+    """One launch: this call's decode with its scores (as paged_decode_scores)
+    and the importance sum of prev_scores (the previous call's, same
+    sequences and lengths) into prev_importance; prev_scores None for the
+    first call of a chain."""
+    B = q.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = decode_workspace_size(B, n_heads, n_kv_heads, head_dim, max_ctx, window, global_stride)
+    if workspace is None and need:
+        workspace = alloc_workspace(need, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    imp_stride = 0 if prev_importance is None else prev_importance.shape[-1]
+    rc = load().nyion_paged_decode_attention_tracked_pipelined(
+        ptr(q), ptr(k_pool), ptr(v_pool), ptr(block_tables), block_tables.shape[1], ptr(ctx_lens),
+        ptr(q_pos), B, n_heads, n_kv_heads, head_dim, block_tokens, k_pool.shape[0], kv_dtype,
+        window, global_stride, max_ctx, scale, ptr(out), ptr(workspace), ws_bytes, ptr(scores),
+        scores.shape[-1], ptr(prev_scores), ptr(prev_importance), imp_stride,
+        stream_handle(stream))
+    check(rc, "nyion_paged_decode_attention_tracked_pipelined")
+    return workspace
+
+
+def paged_decode_importance(ctx_lens, scores, importance, n_heads, window=0, global_stride=0,
+                            max_ctx=None, q_pos=None, stream=None):
+    """The tracked decode's second launch: importance [B][>= max_ctx] f64 +=
+    the normalised probabilities summed over heads, from scores as
+    paged_decode_scores left them."""
+    B = scores.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    rc = load().nyion_paged_decode_importance(
+        ptr(ctx_lens), ptr(q_pos), B, n_heads, window, global_stride, max_ctx, ptr(scores),
+        scores.shape[-1], ptr(importance), importance.shape[-1], stream_handle(stream))
+    check(rc, "nyion_paged_decode_importance")
 
 
 def paged_decode_positions(q, k_pool, v_pool, block_tables, positions, n_positions, out, n_heads,

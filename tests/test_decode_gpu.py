@@ -284,6 +284,129 @@ def test_tracked_split_and_window(gpu):
         assert np.all(imp[b][~mask] == 0.0)
 
 
+@pytest.mark.parametrize("window,global_stride", [(0, 0), (512, 64)])
+def test_tracked_scores_then_importance(gpu, window, global_stride):
+    """The tracked call's two launches as separate entry points give its
+    results bit for bit: on one stream, and with the importance on a second
+    stream ordered after the decode by an event while the first stream runs
+    another decode into a second scores buffer."""
+    pb = W.paged_batch([4096, 700, 1, 2500], seed=21)
+    q_pos = [4095, 650, 0, 2499]
+    q = to_dev(pb.q)
+    kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    qp = to_dev(np.asarray(q_pos, np.int32))
+    max_ctx = int(pb.ctx_lens.max())
+    init = np.random.default_rng(22).random((pb.batch, max_ctx + 4))
+    kw = dict(window=window, global_stride=global_stride, q_pos=qp)
+
+    def fresh():
+        return (torch.full_like(q, float("nan")), torch.from_numpy(init.copy()).cuda(),
+                torch.full((pb.batch, pb.n_heads, max_ctx + 2), float("nan"), device="cuda"))
+
+    out_t, imp_t, sc_t = fresh()
+    gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out_t, imp_t, pb.n_heads, pb.n_kv_heads,
+                             pb.head_dim, pb.block_tokens, scores=sc_t, **kw)
+    # one stream
+    out_1, imp_1, sc_1 = fresh()
+    gpu.paged_decode_scores(q, kp, vp, tab, ctx, out_1, sc_1, pb.n_heads, pb.n_kv_heads,
+                            pb.head_dim, pb.block_tokens, **kw)
+    gpu.paged_decode_importance(ctx, sc_1, imp_1, pb.n_heads, window=window,
+                                global_stride=global_stride, q_pos=qp)
+    # two streams: the importance of the first decode runs beside a second decode
+    main, side = torch.cuda.Stream(), torch.cuda.Stream()
+    out_2, imp_2, sc_2 = fresh()
+    out_3, _, sc_3 = fresh()
+    torch.cuda.synchronize()
+    gpu.paged_decode_scores(q, kp, vp, tab, ctx, out_2, sc_2, pb.n_heads, pb.n_kv_heads,
+                            pb.head_dim, pb.block_tokens, stream=main, **kw)
+    ev = torch.cuda.Event()
+    ev.record(main)
+    side.wait_event(ev)
+    gpu.paged_decode_importance(ctx, sc_2, imp_2, pb.n_heads, window=window,
+                                global_stride=global_stride, q_pos=qp, stream=side)
+    gpu.paged_decode_scores(q, kp, vp, tab, ctx, out_3, sc_3, pb.n_heads, pb.n_kv_heads,
+                            pb.head_dim, pb.block_tokens, stream=main, **kw)
+    torch.cuda.synchronize()
+    assert gpu.take_status()[0] == 0
+    ref = [x.cpu().numpy() for x in (out_t, imp_t, sc_t)]
+    for name, got in (("one stream", (out_1, imp_1, sc_1)), ("two streams", (out_2, imp_2, sc_2))):
+        got = [x.cpu().numpy() for x in got]
+        assert np.array_equal(got[0], ref[0]), f"{name}: output"
+        assert np.array_equal(got[1], ref[1]), f"{name}: importance"
+        assert np.array_equal(got[2], ref[2], equal_nan=True), f"{name}: scores"
+    assert np.array_equal(out_3.cpu().numpy(), ref[0]), "second decode"
+    # and the tracked call itself against the oracle (importance added to init)
+    for b in range(pb.batch):
+        L = int(pb.ctx_lens[b])
+        got = ref[1][b] - init[b]
+        if window == 0:
+            _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, q_pos[b],
+                                          pb.n_heads, pb.n_kv_heads, pb.head_dim, importance=True)
+            assert np.max(np.abs(got[:L] - ref_imp)) <= 1e-4 * pb.n_heads, f"importance b={b}"
+        else:
+            pos = oracle.sparse_positions(L, q_pos[b], window, global_stride)
+            assert abs(got[pos].sum() - pb.n_heads) <= 1e-3, f"window importance b={b}"
+
+
+@pytest.mark.parametrize("lens,window,global_stride", [
+    ([4096, 700, 1, 2500], 0, 0),                      # direct partition
+    ([4096, 700, 1, 2500], 512, 64),                   # window with strided globals
+    ([3000 + 97 * i for i in range(20)], 0, 0),        # stream-K partition
+])
+def test_tracked_pipelined_chain(gpu, lens, window, global_stride):
+    """Three layers through the pipelined tracked decode (layer l's launch
+    also sums layer l-1's importance; the last layer's sum is its own call)
+    equal three tracked calls bit for bit: outputs, scores and importance."""
+    B = len(lens)
+    layers = [W.paged_batch(lens, seed=31 + i) for i in range(3)]
+    q_pos = [max(0, L - 1 - i % 3) for i, L in enumerate(lens)]
+    pb0 = layers[0]
+    ctx, qp = to_dev(pb0.ctx_lens), to_dev(np.asarray(q_pos, np.int32))
+    max_ctx = max(lens)
+    init = np.random.default_rng(33).random((3, B, max_ctx + 3))
+    kw = dict(window=window, global_stride=global_stride, q_pos=qp)
+    dev = [(to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool), to_dev(pb.tables)) for pb in layers]
+    ref = []
+    for li, (q, kp, vp, tab) in enumerate(dev):
+        out = torch.full_like(q, float("nan"))
+        imp = torch.from_numpy(init[li].copy()).cuda()
+        sc = torch.full((B, pb0.n_heads, max_ctx + 2), float("nan"), device="cuda")
+        gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out, imp, pb0.n_heads, pb0.n_kv_heads,
+                                 pb0.head_dim, pb0.block_tokens, scores=sc, **kw)
+        ref.append([x.cpu().numpy() for x in (out, imp, sc)])
+    outs = [torch.full_like(d[0], float("nan")) for d in dev]
+    imps = [torch.from_numpy(init[li].copy()).cuda() for li in range(3)]
+    scs = [torch.full((B, pb0.n_heads, max_ctx + 2), float("nan"), device="cuda") for _ in range(2)]
+    got_sc = []
+    for li, (q, kp, vp, tab) in enumerate(dev):
+        prev = scs[(li - 1) % 2] if li > 0 else None
+        gpu.paged_decode_tracked_pipelined(q, kp, vp, tab, ctx, outs[li], scs[li % 2], prev,
+                                           imps[li - 1] if li > 0 else None, pb0.n_heads,
+                                           pb0.n_kv_heads, pb0.head_dim, pb0.block_tokens, **kw)
+        if li > 0:
+            got_sc.append(scs[(li - 1) % 2].cpu().numpy())  # after its sum ran (same stream)
+    got_sc.append(scs[2 % 2].cpu().numpy())
+    gpu.paged_decode_importance(ctx, scs[2 % 2], imps[2], pb0.n_heads, window=window,
+                                global_stride=global_stride, q_pos=qp)
+    torch.cuda.synchronize()
+    assert gpu.take_status()[0] == 0
+    for li in range(3):
+        assert np.array_equal(outs[li].cpu().numpy(), ref[li][0]), f"layer {li}: output"
+        assert np.array_equal(imps[li].cpu().numpy(), ref[li][1]), f"layer {li}: importance"
+        assert np.array_equal(got_sc[li], ref[li][2], equal_nan=True), f"layer {li}: scores"
+    # the chain's own checks: probabilities of each sequence's attended set sum to n_heads
+    for li in range(3):
+        got = imps[li].cpu().numpy() - init[li]
+        assert np.allclose(got.sum(axis=1), pb0.n_heads, atol=1e-3), f"layer {li}: sums"
+    # the previous scores may not be this call's scores buffer
+    with pytest.raises(Exception):
+        q, kp, vp, tab = dev[0]
+        gpu.paged_decode_tracked_pipelined(q, kp, vp, tab, ctx, outs[0], scs[0], scs[0], imps[0],
+                                           pb0.n_heads, pb0.n_kv_heads, pb0.head_dim,
+                                           pb0.block_tokens, **kw)
+
+
 def _check_tracked(pb, out, imp, init=None):
     assert_close(out, W.reference_decode(pb), "tracked out")
     for b in range(pb.batch):
