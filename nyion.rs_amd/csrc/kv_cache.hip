@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "kv_write.hpp"
 
 namespace nyion {
 
@@ -46,71 +47,7 @@ __device__ __forceinline__ void q4_quantize_group(const float* x, int len, uint3
 
 // ------------------------------------------------------------- kernels
 
-// bf16 -> f32 is exact (the bf16 bits are the high half of the f32).
-__device__ __forceinline__ float4 bf16x4_to_f32(uint2 w) {
-    return float4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                  __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
-}
-
-struct WriteArgs {
-    void* k_pool;
-    void* v_pool;
-    const int32_t* tables;  // [batch][table_stride]
-    const int32_t* positions;  // per-sequence position (append) or nullptr
-    const float* k;  // [rows][Hkv][D] f32, or nullptr when the bf16 source is used
-    const float* v;
-    const uint16_t* k16;  // [rows][Hkv][D] bf16 bits (prefill path)
-    const uint16_t* v16;
-    int table_stride;
-    int start_pos;  // used when positions == nullptr
-    int rows;       // tokens (single sequence) or sequences (append)
-    int per_seq;    // 1: row r is sequence r at positions[r]; 0: row r is token start_pos+r of seq 0
-    int n_kv_heads;
-    int head_dim;
-    int bt_log2;
-    int num_blocks;
-    long long block_stride;  // row units
-    long long head_stride;
-    int token_stride;
-    unsigned* status;  // bf16 source: the device's range-status word (V beyond binary16)
-    // zone geometry: sequence s's page offsets at page_bases + s * zone.n_pages
-    // (tables unused); nullptr: block tables
-    const int64_t* page_bases;
-    ZoneMap zone;
-};
-
-__device__ __forceinline__ long long write_row_offset(const WriteArgs& a, int r, int h) {
-    const int seq = a.per_seq ? r : 0;
-    const int pos = a.per_seq ? a.positions[r] : a.start_pos + r;
-    if (pos < 0) return -1;
-    RowMap m;
-    m.table = a.tables + (long long)seq * a.table_stride;
-    m.block_stride = a.block_stride;
-    m.head_stride = a.head_stride;
-    m.token_stride = a.token_stride;
-    m.bt_log2 = a.bt_log2;
-    m.num_blocks = a.num_blocks;
-    m.table_len = a.table_stride;
-    m.zone = a.zone;
-    m.zone.page_base = a.page_bases ? a.page_bases + (long long)seq * a.zone.n_pages : nullptr;
-    return row_offset(m, pos, h);
-}
-
-typedef _Float16 halfx2_t __attribute__((ext_vector_type(2)));
-
-// Two f32 -> one word of two binary16 (round to nearest even), lo first.
-__device__ __forceinline__ uint32_t f16x2_bits(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, halfx2_t{(_Float16)lo, (_Float16)hi});
-}
-
 // One thread per (row, head, 4 values): f32 rows, or binary16 rows (F16).
-// Largest |v| of four bf16 values (the bits of two words).
-__device__ __forceinline__ float v_absmax(uint2 w) {
-    const float a = __uint_as_float(w.x << 16), b = __uint_as_float(w.x & 0xffff0000u);
-    const float c = __uint_as_float(w.y << 16), d = __uint_as_float(w.y & 0xffff0000u);
-    return fmaxf(fmaxf(fabsf(a), fabsf(b)), fmaxf(fabsf(c), fabsf(d)));
-}
-
 // With a bf16 source the kernel also records, in the range-status word,
 // whether some V value reaches 65520 in magnitude: the prefill computed
 // P.V with V in binary16, which cannot hold it (checked here, where V is
@@ -125,25 +62,7 @@ __global__ void kv_write_flat_kernel(WriteArgs a) {
         const int x = (int)(i % vec);
         const int h = (int)((i / vec) % a.n_kv_heads);
         const int r = (int)(i / ((long long)vec * a.n_kv_heads));
-        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 4 * x;
-        if (a.k16) vmax = fmaxf(vmax, v_absmax(*(const uint2*)(a.v16 + src)));
-        const long long off = write_row_offset(a, r, h);
-        if (off < 0) continue;
-        float4 kk, vv;
-        if (a.k16) {
-            kk = bf16x4_to_f32(*(const uint2*)(a.k16 + src));
-            vv = bf16x4_to_f32(*(const uint2*)(a.v16 + src));
-        } else {
-            kk = *(const float4*)(a.k + src);
-            vv = *(const float4*)(a.v + src);
-        }
-        if (F16) {
-            *(uint2*)((uint16_t*)a.k_pool + off + 4 * x) = uint2{f16x2_bits(kk.x, kk.y), f16x2_bits(kk.z, kk.w)};
-            *(uint2*)((uint16_t*)a.v_pool + off + 4 * x) = uint2{f16x2_bits(vv.x, vv.y), f16x2_bits(vv.z, vv.w)};
-        } else {
-            *(float4*)((float*)a.k_pool + off + 4 * x) = kk;
-            *(float4*)((float*)a.v_pool + off + 4 * x) = vv;
-        }
+        vmax = fmaxf(vmax, write_kv_vec<F16>(a, r, h, x));
     }
     if (a.k16) report_range(a.status, vmax >= 65520.f, kRangePrefillV);
 }
@@ -497,11 +416,11 @@ int kv_write_impl(void* k_pool, void* v_pool, const int32_t* block_table, int bl
     return launch_write(a, kv_dtype, stream);
 }
 
-int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
-                       int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
-                       int n_tokens, const uint16_t* k, const uint16_t* v, hipStream_t stream) {
+int prefill_write_args(WriteArgs& a, void* k_pool, void* v_pool, const int32_t* block_table,
+                       int block_tokens, int num_blocks, int n_kv_heads, int head_dim, int kv_dtype,
+                       int start_pos, int n_tokens, const uint16_t* k, const uint16_t* v) {
     int rc;
-    WriteArgs a{};
+    a = WriteArgs{};
     if ((rc = fill_write_args(a, k_pool, v_pool, block_tokens, num_blocks, n_kv_heads, head_dim,
                               kv_dtype)) != NYION_OK)
         return rc;
@@ -518,14 +437,24 @@ int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, i
     a.start_pos = start_pos;
     a.rows = n_tokens;
     a.per_seq = 0;
-    // the V range check of the prefill: fused into the f32 / binary16
-    // write, on its own before a Q4 write
-    if (kv_dtype == NYION_KV_Q4_20B) {
-        if ((rc = v_range_check(v, (long long)n_tokens * n_kv_heads * head_dim, stream)) != NYION_OK)
-            return rc;
-    } else {
-        a.status = device_status_word();
-    }
+    // the V range check of the prefill rides on the f32 / binary16 write
+    if (kv_dtype != NYION_KV_Q4_20B) a.status = device_status_word();
+    return NYION_OK;
+}
+
+int kv_write_bf16_impl(void* k_pool, void* v_pool, const int32_t* block_table, int block_tokens,
+                       int num_blocks, int n_kv_heads, int head_dim, int kv_dtype, int start_pos,
+                       int n_tokens, const uint16_t* k, const uint16_t* v, hipStream_t stream) {
+    int rc;
+    WriteArgs a;
+    if ((rc = prefill_write_args(a, k_pool, v_pool, block_table, block_tokens, num_blocks,
+                                 n_kv_heads, head_dim, kv_dtype, start_pos, n_tokens, k, v)) !=
+        NYION_OK)
+        return rc;
+    // a Q4 write has no V range check of its own: the check runs first
+    if (kv_dtype == NYION_KV_Q4_20B &&
+        (rc = v_range_check(v, (long long)n_tokens * n_kv_heads * head_dim, stream)) != NYION_OK)
+        return rc;
     return launch_write(a, kv_dtype, stream);
 }
 

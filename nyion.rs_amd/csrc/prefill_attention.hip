@@ -36,6 +36,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "kv_write.hpp"
 
 namespace nyion {
 
@@ -70,6 +71,12 @@ struct PrefillArgs {
     int n_items;   // kv heads x head subsets x row-block groups
     int causal;
     float scale_log2;
+    // the chunk's paged K/V write into f32 or binary16 pools, done by the
+    // kernel (kv_write != 0): each workgroup of head subset 0 writes its own
+    // tokens' rows for its kv head after its attention work
+    WriteArgs kvw;
+    int kv_write;
+    int kv_f16;
 };
 
 constexpr int BN = 64;  // keys per tile
@@ -517,6 +524,22 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
             for (int dt = 0; dt < DT; dt++) orow[32 * dt + j] = o[dt][r] * inv;
         }
     }
+
+    // this workgroup's tokens' K/V rows for kv head g into the paged pools
+    // (every (token, kv head) by exactly one workgroup), with the V range
+    // check the binary16 P.V product needs
+    if (a.kv_write && hs == 0) {
+        constexpr int VEC = D / 4;
+        const int r0 = rbg * a.rb_per_wg * 32;
+        const int r1 = min(a.n, r0 + a.rb_per_wg * 32);
+        float vmax = 0.f;
+        for (int i = tid; i < (r1 - r0) * VEC; i += prefill_threads<D>()) {
+            const int r = r0 + i / VEC, x = i % VEC;
+            vmax = fmaxf(vmax, a.kv_f16 ? write_kv_vec<true>(a.kvw, r, g, x)
+                                        : write_kv_vec<false>(a.kvw, r, g, x));
+        }
+        report_range(a.kvw.status, vmax >= 65520.f, kRangePrefillV);
+    }
 }
 
 }  // namespace nyion
@@ -579,6 +602,18 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     a.causal = causal ? 1 : 0;
     const float sc = scale > 0.f ? scale : 1.0f / sqrtf((float)head_dim);
     a.scale_log2 = sc * 1.4426950408889634f;
+    if (k_pool || v_pool) {
+        if (!k_pool || !v_pool || !block_table)
+            return set_error(NYION_ERR_INVALID, "prefill: KV write needs k_pool, v_pool and block_table");
+        if (kv_dtype == NYION_KV_F32 || kv_dtype == NYION_KV_F16) {
+            if ((rc = prefill_write_args(a.kvw, k_pool, v_pool, block_table, block_tokens, num_blocks,
+                                         n_kv_heads, head_dim, kv_dtype, start_pos, n, k, v)) !=
+                NYION_OK)
+                return rc;
+            a.kv_write = 1;
+            a.kv_f16 = kv_dtype == NYION_KV_F16;
+        }
+    }
     dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
     if (head_dim == 128)
@@ -593,12 +628,9 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
         (rc = v_range_check(v_hist, (long long)n_hist * n_kv_heads * head_dim, st)) != NYION_OK)
         return rc;
     if (!k_pool && !v_pool) return v_range_check(v, (long long)n * n_kv_heads * head_dim, st);
-    if (k_pool || v_pool) {
-        if (!k_pool || !v_pool || !block_table)
-            return set_error(NYION_ERR_INVALID, "prefill: KV write needs k_pool, v_pool and block_table");
+    if (!a.kv_write)  // 4-bit pools: their own quantising write (with the V range check)
         return kv_write_bf16_impl(k_pool, v_pool, block_table, block_tokens, num_blocks, n_kv_heads,
                                   head_dim, kv_dtype, start_pos, n, k, v, st);
-    }
     return NYION_OK;
 }
 
