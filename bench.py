@@ -594,7 +594,7 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
     vp = torch.empty_like(kp)
     flops = 4 * Hq * D * n * (n + 1) / 2
 
-    def attn(i):  # the prefill alone: attention kernel, then the V range check
+    def attn(i):  # the prefill alone (the kernel also checks V's binary16 range)
         nh.prefill_bf16(q, k, v, out, Hq, Hkv, D)
 
     def attn_kv(i):  # the configuration's work: prefill plus the paged KV write of the chunk
@@ -615,7 +615,7 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
             "tflops_with_kv_write": flops / (us_kv * 1e-6) / 1e12,
             "mfma_frac_with_kv_write": flops / (us_kv * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
             "us_prefill_call": us, "us_prefill_call_p10_p50_p90": _us3(pct), "reps": reps,
-            "prefill_call": "the attention kernel plus the V range check (a 16.8 MB read, ~4 us)",
+            "prefill_call": "the attention kernel (which also checks V's binary16 range; one launch)",
             "flops": flops, "tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
             "kv_write_bytes": 2 * n * Hkv * D * (2 + 4),
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,

@@ -77,6 +77,7 @@ struct PrefillArgs {
     WriteArgs kvw;
     int kv_write;
     int kv_f16;
+    int v_check;  // no pools: the same workgroups only check their V rows' range
 };
 
 constexpr int BN = 64;  // keys per tile
@@ -527,16 +528,19 @@ __global__ __launch_bounds__(prefill_threads<D>(), 512 / prefill_threads<D>()) v
 
     // this workgroup's tokens' K/V rows for kv head g into the paged pools
     // (every (token, kv head) by exactly one workgroup), with the V range
-    // check the binary16 P.V product needs
-    if (a.kv_write && hs == 0) {
+    // check the binary16 P.V product needs; without pools, the check alone
+    if ((a.kv_write || a.v_check) && hs == 0) {
         constexpr int VEC = D / 4;
         const int r0 = rbg * a.rb_per_wg * 32;
         const int r1 = min(a.n, r0 + a.rb_per_wg * 32);
         float vmax = 0.f;
         for (int i = tid; i < (r1 - r0) * VEC; i += prefill_threads<D>()) {
             const int r = r0 + i / VEC, x = i % VEC;
-            vmax = fmaxf(vmax, a.kv_f16 ? write_kv_vec<true>(a.kvw, r, g, x)
-                                        : write_kv_vec<false>(a.kvw, r, g, x));
+            if (!a.kv_write)
+                vmax = fmaxf(vmax, v_absmax(*(const uint2*)(a.v + ((long long)r * a.n_kv_heads + g) * D + 4 * x)));
+            else
+                vmax = fmaxf(vmax, a.kv_f16 ? write_kv_vec<true>(a.kvw, r, g, x)
+                                            : write_kv_vec<false>(a.kvw, r, g, x));
         }
         report_range(a.kvw.status, vmax >= 65520.f, kRangePrefillV);
     }
@@ -613,6 +617,9 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
             a.kv_write = 1;
             a.kv_f16 = kv_dtype == NYION_KV_F16;
         }
+    } else {
+        a.v_check = 1;
+        a.kvw.status = device_status_word();
     }
     dim3 grid(8 * ((a.n_items + 7) / 8));
     hipStream_t st = (hipStream_t)stream;
@@ -622,12 +629,13 @@ static int prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v,
         hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(prefill_threads<64>()), 0, st, a);
     if ((rc = check_launch("prefill")) != NYION_OK) return rc;
     // V enters the P.V product as binary16: values of magnitude >= 65520 are
-    // reported through the status word (the chunk's V by the KV write when
-    // there is one, else by a check of its own; the history's always here)
+    // reported through the status word (the chunk's V by the kernel's own
+    // tail, with or without its f32 / binary16 pool write, or by the Q4
+    // write's check; the history's here)
     if (n_hist > 0 &&
         (rc = v_range_check(v_hist, (long long)n_hist * n_kv_heads * head_dim, st)) != NYION_OK)
         return rc;
-    if (!k_pool && !v_pool) return v_range_check(v, (long long)n * n_kv_heads * head_dim, st);
+    if (!k_pool && !v_pool) return NYION_OK;  // the kernel checked the chunk's V itself
     if (!a.kv_write)  // 4-bit pools: their own quantising write (with the V range check)
         return kv_write_bf16_impl(k_pool, v_pool, block_table, block_tokens, num_blocks, n_kv_heads,
                                   head_dim, kv_dtype, start_pos, n, k, v, st);
