@@ -120,14 +120,17 @@ def test_prefill_c5_full_size_sampled_rows(gpu):
     assert err32 <= 5e-2, err32
 
 
-@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_F16, oracle.KV_Q4])
 def test_prefill_writes_paged_kv(gpu, kv_dtype):
+    """The chunk's K/V rows land in the pool at start_pos + row through the
+    block table: f32 and binary16 (round to nearest even) by the prefill
+    kernel itself, Q4-20B by the quantising write."""
     n, hkv, d, bt, start = 200, 2, 128, 16, 16
     q, k, v = W.prefill_inputs(n, 8, hkv, d, seed=2)
     nb = (start + n + bt - 1) // bt + 3
     table = np.random.default_rng(3).permutation(nb).astype(np.int32)
-    rb = d if kv_dtype == oracle.KV_F32 else oracle.q4_row_bytes(d)
-    dt = torch.float32 if kv_dtype == oracle.KV_F32 else torch.uint8
+    rb = {oracle.KV_F32: d, oracle.KV_F16: d}.get(kv_dtype, oracle.q4_row_bytes(d))
+    dt = {oracle.KV_F32: torch.float32, oracle.KV_F16: torch.int16}.get(kv_dtype, torch.uint8)
     kp = torch.zeros((nb, hkv, bt, rb), dtype=dt, device="cuda")
     vp = torch.zeros_like(kp)
     got = run_prefill(gpu, q, k, v, k_pool=kp, v_pool=vp,
@@ -141,6 +144,9 @@ def test_prefill_writes_paged_kv(gpu, kv_dtype):
     kb, vb = W.bf16_round(k), W.bf16_round(v)
     if kv_dtype == oracle.KV_F32:
         assert np.array_equal(kh, kb) and np.array_equal(vh, vb)
+    elif kv_dtype == oracle.KV_F16:
+        assert np.array_equal(kh.view(np.uint16), kb.astype(np.float16).view(np.uint16))
+        assert np.array_equal(vh.view(np.uint16), vb.astype(np.float16).view(np.uint16))
     else:
         assert np.array_equal(kh, oracle.q4_quantize_rows(kb))
         assert np.array_equal(vh, oracle.q4_quantize_rows(vb))
