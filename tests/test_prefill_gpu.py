@@ -120,13 +120,16 @@ def test_prefill_c5_full_size_sampled_rows(gpu):
     assert err32 <= 5e-2, err32
 
 
-@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_F16, oracle.KV_Q4])
-def test_prefill_writes_paged_kv(gpu, kv_dtype):
+@pytest.mark.parametrize("kv_dtype,d,hq", [(oracle.KV_F32, 128, 8), (oracle.KV_F16, 128, 8),
+                                           (oracle.KV_Q4, 128, 8), (oracle.KV_F32, 64, 8),
+                                           (oracle.KV_F16, 64, 2), (oracle.KV_F32, 128, 16)])
+def test_prefill_writes_paged_kv(gpu, kv_dtype, d, hq):
     """The chunk's K/V rows land in the pool at start_pos + row through the
     block table: f32 and binary16 (round to nearest even) by the prefill
-    kernel itself, Q4-20B by the quantising write."""
-    n, hkv, d, bt, start = 200, 2, 128, 16, 16
-    q, k, v = W.prefill_inputs(n, 8, hkv, d, seed=2)
+    kernel itself (head_dim 128 and 64 kernels, one and two head subsets per
+    kv head), Q4-20B by the quantising write."""
+    n, hkv, bt, start = 200, 2, 16, 16
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=2)
     nb = (start + n + bt - 1) // bt + 3
     table = np.random.default_rng(3).permutation(nb).astype(np.int32)
     rb = {oracle.KV_F32: d, oracle.KV_F16: d}.get(kv_dtype, oracle.q4_row_bytes(d))
