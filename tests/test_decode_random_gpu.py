@@ -69,3 +69,46 @@ def test_random_decode(gpu, seed):
     err = np.max(np.abs(got - ref))
     rel = err / max(np.max(np.abs(ref)), 1e-30)
     assert err <= ATOL and rel <= RTOL, f"{c}: max-abs {err:.3e} rel {rel:.3e}"
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_tracked_pipelined(gpu, seed):
+    """Random configurations (the draws above) through two layers of the
+    pipelined tracked decode (layer 1's launch also sums layer 0's
+    importance; layer 1's own sum is the standalone call): outputs,
+    importance and scores equal two tracked calls bit for bit."""
+    c = draw(500 + seed)
+    print(f"case {seed}: {c}", flush=True)
+    pbs = [W.paged_batch(c["ctx"], n_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"],
+                         block_tokens=c["bt"], seed=600 + 2 * seed + i, kv_dtype=c["kv"])
+           for i in range(2)]
+    ctx = to_dev(pbs[0].ctx_lens)
+    qp = None if c["q_pos"] is None else to_dev(np.asarray(c["q_pos"], np.int32))
+    max_ctx = int(pbs[0].ctx_lens.max())
+    B, H = pbs[0].batch, pbs[0].n_heads
+    kw = dict(kv_dtype=c["kv"], window=c["window"], global_stride=c["stride"], max_ctx=max_ctx,
+              q_pos=qp)
+    dev = [(to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool), to_dev(pb.tables)) for pb in pbs]
+    init = np.random.default_rng(700 + seed).random((2, B, max_ctx + 1))
+    ref = []
+    for i, (q, kp, vp, tab) in enumerate(dev):
+        out = torch.full_like(q, float("nan"))
+        imp = torch.from_numpy(init[i].copy()).cuda()
+        sc = torch.full((B, H, max_ctx + 2), float("nan"), device="cuda")
+        gpu.paged_decode_tracked(q, kp, vp, tab, ctx, out, imp, H, c["hkv"], c["hd"], c["bt"],
+                                 scores=sc, **kw)
+        ref.append([x.cpu().numpy() for x in (out, imp, sc)])
+    outs = [torch.full_like(d[0], float("nan")) for d in dev]
+    imps = [torch.from_numpy(init[i].copy()).cuda() for i in range(2)]
+    scs = [torch.full((B, H, max_ctx + 2), float("nan"), device="cuda") for _ in range(2)]
+    for i, (q, kp, vp, tab) in enumerate(dev):
+        gpu.paged_decode_tracked_pipelined(q, kp, vp, tab, ctx, outs[i], scs[i],
+                                           scs[0] if i else None, imps[0] if i else None, H,
+                                           c["hkv"], c["hd"], c["bt"], **kw)
+    gpu.paged_decode_importance(ctx, scs[1], imps[1], H, window=c["window"],
+                                global_stride=c["stride"], max_ctx=max_ctx, q_pos=qp)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert np.array_equal(outs[i].cpu().numpy(), ref[i][0]), f"{c}: layer {i} output"
+        assert np.array_equal(imps[i].cpu().numpy(), ref[i][1]), f"{c}: layer {i} importance"
+        assert np.array_equal(scs[i].cpu().numpy(), ref[i][2], equal_nan=True), f"{c}: layer {i} scores"
