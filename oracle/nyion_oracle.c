@@ -1,7 +1,8 @@
 /*
  * nyion_oracle.c — CPU restatement of the Nyion attention path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker and the CPU baseline).  The product
+ * TEST INFRASTRUCTURE ONLY (the tests' reference results and the CPU
+ * baseline).  The product
  * library never links or calls this file.  Build: oracle/Makefile, which
  * compiles with -ffp-contract=off so that every multiply-then-add written
  * below stays two roundings, exactly as the Rust source (no contraction)

@@ -1,8 +1,8 @@
 /*
  * nyion_oracle.h — CPU restatement of the Nyion attention path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path
- * is compared against, and the scalar/OpenMP CPU baseline that bench.py
+ * TEST INFRASTRUCTURE ONLY.  This library is the reference result the HIP
+ * path is compared against, and the scalar/OpenMP CPU baseline that bench.py
  * times beside the GPU.  Nothing in the product library (libnyion_hip.so)
  * links, loads or calls it; only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may.

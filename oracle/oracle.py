@@ -1,7 +1,7 @@
 """ctypes front-end of the CPU oracle (oracle/nyion_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker.  The product library never
+cpu_baseline leg of bench.py, as the reference result.  The product library never
 imports it.
 
 The oracle restates the reference's CPU attention (swamp-engine/src/ops.rs),

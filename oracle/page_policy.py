@@ -1,8 +1,8 @@
 """Restatement of the PagedKVCache page policy (swamp-engine/src/cache.rs).
 
-TEST INFRASTRUCTURE ONLY: the checker for the policy inside the product
-library's paged KV pool (nyion_page_policy_* / nyion_kv_pool_*).  Nothing in
-the product imports it.
+TEST INFRASTRUCTURE ONLY: what the tests compare the policy inside the
+product library's paged KV pool (nyion_page_policy_* / nyion_kv_pool_*)
+against.  Nothing in the product imports it.
 
 Followed line by line (paths relative to the reference repository root):
   cache.rs:277-309  alloc_hot_page_in_zone: a new page is hot, importance 0,

@@ -22,7 +22,7 @@ for sub in ("oracle", "nyion.rs_amd"):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-import oracle  # noqa: E402  (the checker)
+import oracle  # noqa: E402  (the reference results)
 
 
 @dataclasses.dataclass
