@@ -36,7 +36,7 @@ cpu_baseline: the C restatement of ops::attention (oracle/, the reference's
 AVX-512 dot/axpy order, OpenMP over heads) on the host cores, on a bounded
 sample of the headline batch (the first sequences, scaled by attended
 tokens), at all host cores and at 6 threads (the reference executor's rayon
-pool).
+pool); every CPU figure is the median over the runs that fit its time budget.
 """
 from __future__ import annotations
 
@@ -186,15 +186,17 @@ def _cores():
 
 
 def _cpu_time(fn, budget_s=2.0, max_calls=2000):
-    """Mean seconds per call of fn after one warm call, over about budget_s."""
+    """Median seconds per call of fn after one warm call, over the calls that
+    fit in about budget_s (at least three)."""
     fn()
-    n, t0 = 0, time.perf_counter()
+    times, t0 = [], time.perf_counter()
     while True:
+        t1 = time.perf_counter()
         fn()
-        n += 1
+        times.append(time.perf_counter() - t1)
         el = time.perf_counter() - t0
-        if el > budget_s or n >= max_calls:
-            return el / n, n
+        if (el > budget_s and len(times) >= 3) or len(times) >= max_calls:
+            return float(np.median(times)), len(times)
 
 
 def _cpu_model():
