@@ -740,8 +740,16 @@ def bench_c1(nh, torch, steps, warmup):
     ms = timed(call, steps * 10, warmup, torch)
     us = event_mean(call, steps * 4, torch) * 1e3
     pct = event_pcts(call, max(steps, 20), torch)
+    # algorithmic bytes: K and V of 4 kv heads x 128 positions x 64 f32 (262144)
+    # + q and out (2 x 32 x 64 x 4) = 278528; at 8 TB/s that is 0.035 us, so
+    # the call is bound by launch and dependent-access latency, not by HBM
+    nbytes = 278528
+    rl = hbm_roofline(nbytes, us, pmc_traffic("c1"))
+    rl.update({"kernel": "decode_kernel<64,f32,contiguous> (the Attention node, one launch)",
+               "bytes_per_launch": nbytes, "launch_us": round(us, 3),
+               "ideal_us_at_peak": round(nbytes / (HBM_PEAK_GBS * 1e3), 4)})
     return {"us_per_layer": ms * 1e3, "call_us_event_mean": us, "call_us_p10_p50_p90": _us3(pct),
-            "bytes_per_layer": 278528}
+            "bytes_per_layer": nbytes, "roofline": rl}
 
 
 def bench_abi(nh, torch, steps, warmup):

@@ -78,7 +78,9 @@ const char* nyion_version(void);
  * `stream`, waits for it, takes (reads and clears) the word and returns
  * NYION_OK, or NYION_ERR_RANGE with nyion_last_error() naming what
  * overflowed since the last take.  The word is per device, not per stream:
- * work on other streams of the device lands in the same word.  No
+ * work on other streams of the device lands in the same word.  Takes on one
+ * device from several threads are serialised by the library, so each report
+ * reaches exactly one taker.  No
  * counterpart in the reference, whose CPU path computes in f32 throughout
  * (swamp-engine/src/ops.rs:170-278). */
 int nyion_take_status(nyion_stream_t stream);

@@ -587,6 +587,10 @@ int nyion_zone_kv_write(void* k_pool, void* v_pool, int64_t pool_units, const in
                          n_tokens);
     if (kv_dtype != NYION_KV_Q4_20B && (!aligned(k, 16) || !aligned(v, 16)))
         return set_error(NYION_ERR_INVALID, "zone kv write: k/v must be 16-byte aligned");
+    if (zone_pos(start_pos + n_tokens - 1).page >= n_pages)
+        return set_error(NYION_ERR_INVALID,
+                         "zone kv write: position %d is on page %d, the table has %d pages",
+                         start_pos + n_tokens - 1, zone_pos(start_pos + n_tokens - 1).page, n_pages);
     a.page_bases = page_base;
     a.k = k;
     a.v = v;

@@ -157,7 +157,13 @@ static int mojo_sparse_impl(const float* q, const float* k_q4, const float* v_q4
     }
     const size_t row_bytes = (size_t)((head_dim + 31) / 32) * 20 * sizeof(float);
     const size_t q_bytes = (size_t)n_heads * head_dim * sizeof(float);
-    const size_t kv_bytes = n_sparse > 0 ? (size_t)(max_pos + 1) * row_bytes : 0;
+    // rows 0..max_pos of K and of V are read; at most 2^31 positions, and the
+    // pair must fit in device memory (checked by the allocation below)
+    const size_t kv_bytes = n_sparse > 0 ? ((size_t)max_pos + 1) * row_bytes : 0;
+    if (kv_bytes > ((size_t)1 << 36))
+        return set_error(NYION_ERR_INVALID,
+                         "sparse_attention_q4: position %d needs %zu bytes of K rows (limit 64 GiB)",
+                         max_pos, kv_bytes);
     const size_t pos_bytes = (size_t)n_sparse * sizeof(int32_t);
     // the five arrays in 256-byte aligned pieces of the staging array when
     // they fit it, else in buffers allocated for the call

@@ -192,11 +192,17 @@ int nyion_take_status(nyion_stream_t stream) {
     unsigned* w = device_status_word();
     if (!w) return set_error(NYION_ERR_LAUNCH, "status word of the current device is unavailable");
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(status_take_kernel, dim3(1), dim3(1), 0, st, w);
-    if ((rc = check_launch("status")) != NYION_OK) return rc;
     unsigned got = 0;
-    NYION_CHECK_HIP(hipMemcpyAsync(&got, w + 1, sizeof got, hipMemcpyDeviceToHost, st));
-    NYION_CHECK_HIP(hipStreamSynchronize(st));
+    {
+        // word 1 carries one take's result back: takes on one device (from
+        // any thread or stream) run one at a time, so each reads its own
+        static std::mutex take_mu[kMaxDevices];
+        std::lock_guard<std::mutex> g(take_mu[current_device()]);
+        hipLaunchKernelGGL(status_take_kernel, dim3(1), dim3(1), 0, st, w);
+        if ((rc = check_launch("status")) != NYION_OK) return rc;
+        NYION_CHECK_HIP(hipMemcpyAsync(&got, w + 1, sizeof got, hipMemcpyDeviceToHost, st));
+        NYION_CHECK_HIP(hipStreamSynchronize(st));
+    }
     if (!got) return NYION_OK;
     std::string msg;
     if (got & kRangePrefillV)

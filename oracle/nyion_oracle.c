@@ -446,11 +446,15 @@ int orc_attention(float* out, const float* q, const orc_kv_layout* kv, int seq_l
 
 int orc_attention_positions(float* out, const float* q, const orc_kv_layout* kv,
                             const int32_t* positions, int n_pos, int n_heads, int n_kv_heads,
-                            int head_dim, int nthreads) {
+                            int head_dim, double* importance, int nthreads) {
     if (!out || !q || !kv || !positions || n_pos <= 0) return -1;
     if (check_heads(n_heads, n_kv_heads, head_dim)) return -1;
     int n_rep = n_heads / n_kv_heads;
     float scale = 1.0f / sqrtf((float)head_dim);
+    /* importance[i] += sum over heads of the probability of positions[i],
+     * added in head order as orc_attention does. */
+    float* probs = importance ? (float*)malloc(sizeof(float) * (size_t)n_pos * (size_t)n_heads) : NULL;
+    if (importance && !probs) return -3;
     int err = 0;
 #pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
     {
@@ -461,13 +465,135 @@ int orc_attention_positions(float* out, const float* q, const orc_kv_layout* kv,
             err = -3;
         } else {
 #pragma omp for schedule(dynamic, 1)
-            for (int h = 0; h < n_heads; h++)
+            for (int h = 0; h < n_heads; h++) {
                 head_positions(out + (size_t)h * head_dim, q + (size_t)h * head_dim, kv, h / n_rep,
                                positions, n_pos, head_dim, scale, scores, tmp);
+                if (probs) memcpy(probs + (size_t)h * n_pos, scores, sizeof(float) * (size_t)n_pos);
+            }
         }
         free(scores);
         free(tmp);
     }
+    if (probs) {
+        if (!err)
+            for (int h = 0; h < n_heads; h++)
+                for (int i = 0; i < n_pos; i++) importance[i] += (double)probs[(size_t)h * n_pos + i];
+        free(probs);
+    }
+    return err;
+}
+
+/* ------------------------------------------------------------------------
+ * attention_sparse_q4 (swamp-engine/src/ops.rs:597-723): attention_sparse's
+ * position set over Q4-20B rows, read with that function's own rules:
+ *   - group g of a row is the 20 bytes at (slot * groups + g) * 20 of the
+ *     (layer, kv head) page block (ops.rs:639-644), f16 d and dmin first;
+ *   - the 16 nibble bytes give elements 0..15 from their low nibbles and
+ *     16..31 from their high nibbles (ops.rs:653-656), where the writer
+ *     (cache.rs:655-663) and dequant_block interleave them;
+ *   - element = fma(d, nibble, dmin) (ops.rs:661-662, 703-704);
+ *   - q.k in 16 FMA lanes over 16-element chunks, lanes added in order
+ *     (ops.rs:664-674), times scale;
+ *   - softmax: max, exp(s - max) summed in position order, times 1/sum
+ *     (ops.rs:678-682);
+ *   - out = sum of fma(v, w, out) in position order over the positions
+ *     whose weight w is not below 1e-8 (ops.rs:686-720).
+ * head_dim must be a multiple of 32 (the reference reads 32 q values per
+ * group).  global_stride <= 0 means no globals (the reference divides by
+ * it).
+ * --------------------------------------------------------------------- */
+void orc_q4_a5_row(const uint8_t* in, int head_dim, float* out) {
+    int groups = head_dim / 32;
+    for (int g = 0; g < groups; g++) {
+        const uint8_t* blk = in + g * 20;
+        float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        float dmin = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+        for (int j = 0; j < 16; j++) {
+            uint8_t b = blk[4 + j];
+            out[g * 32 + j] = fmaf(d, (float)(b & 0x0f), dmin);
+            out[g * 32 + 16 + j] = fmaf(d, (float)(b >> 4), dmin);
+        }
+    }
+}
+
+int orc_sparse_q4_positions(int seq_len, int q_pos, int window, int global_stride, int32_t* out,
+                            int cap) {
+    return sparse_into(seq_len, q_pos, window, global_stride, out, cap);
+}
+
+ORC_CLONES
+static void head_sparse_q4(float* out, const float* qh, const orc_kv_layout* kv, int kvh,
+                           const int32_t* pos, int n_pos, int head_dim, float scale,
+                           float* scores, float* tmp) {
+    float mx = -INFINITY;
+    for (int i = 0; i < n_pos; i++) {
+        orc_q4_a5_row((const uint8_t*)kv->k_base + row_index(kv, pos[i], kvh), head_dim, tmp);
+        float acc[16];
+        for (int l = 0; l < 16; l++) acc[l] = 0.0f;
+        for (int c = 0; c < head_dim; c += 16)
+            for (int l = 0; l < 16; l++) acc[l] = fmaf(tmp[c + l], qh[c + l], acc[l]);
+        float dot = 0.0f;
+        for (int l = 0; l < 16; l++) dot = dot + acc[l];
+        float s = dot * scale;
+        scores[i] = s;
+        if (s > mx) mx = s;
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < n_pos; i++) {
+        float e = expf(scores[i] - mx);
+        scores[i] = e;
+        sum += e;
+    }
+    float inv = 1.0f / sum;
+    for (int i = 0; i < n_pos; i++) scores[i] *= inv;
+    for (int d = 0; d < head_dim; d++) out[d] = 0.0f;
+    for (int i = 0; i < n_pos; i++) {
+        float w = scores[i];
+        if (w < 1e-8f) continue;
+        orc_q4_a5_row((const uint8_t*)kv->v_base + row_index(kv, pos[i], kvh), head_dim, tmp);
+        for (int d = 0; d < head_dim; d++) out[d] = fmaf(tmp[d], w, out[d]);
+    }
+}
+
+int orc_attention_sparse_q4(float* out, const float* q, const orc_kv_layout* kv, int seq_len,
+                            int q_pos, int n_heads, int n_kv_heads, int head_dim, int window,
+                            int global_stride, int nthreads) {
+    if (!out || !q || !kv || kv->dtype != ORC_KV_Q4 || head_dim % 32) return -1;
+    if (check_heads(n_heads, n_kv_heads, head_dim)) return -1;
+    int cap = (window > 0 ? window : 0) + 130;
+    if (cap > seq_len + 1) cap = seq_len + 1;
+    int32_t* pos = (int32_t*)malloc(sizeof(int32_t) * (size_t)cap);
+    if (!pos) return -3;
+    int n_pos = sparse_into(seq_len, q_pos, window, global_stride, pos, cap);
+    if (n_pos < 0) {
+        free(pos);
+        return n_pos == -2 ? -3 : -1;
+    }
+    int n_rep = n_heads / n_kv_heads;
+    float scale = 1.0f / sqrtf((float)head_dim);
+    int err = 0;
+    if (n_pos == 0) {
+        memset(out, 0, sizeof(float) * (size_t)n_heads * (size_t)head_dim);
+        free(pos);
+        return 0;
+    }
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)n_pos);
+        float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        if (!scores || !tmp) {
+#pragma omp atomic write
+            err = -3;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int h = 0; h < n_heads; h++)
+                head_sparse_q4(out + (size_t)h * head_dim, q + (size_t)h * head_dim, kv, h / n_rep,
+                               pos, n_pos, head_dim, scale, scores, tmp);
+        }
+        free(scores);
+        free(tmp);
+    }
+    free(pos);
     return err;
 }
 

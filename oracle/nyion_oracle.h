@@ -46,6 +46,15 @@
  *                                              blocks (fused_gemv_q6k.rs:329-
  *                                              356), a numpy restatement and
  *                                              float64 dequantise-then-dot
+ *   orc_attention_positions importance       : equals orc_attention's over the
+ *                                              full position set; float64 brute
+ *                                              force; sums to n_heads
+ *   orc_q4_a5_row / orc_attention_sparse_q4  : hand-built groups whose A5 order
+ *                                              and writer order differ (one-hot
+ *                                              q, single-position V read back),
+ *                                              the 1e-8 skip on a zero row,
+ *                                              float64 brute force on a tiny
+ *                                              shape
  *   orc_mojo_sparse_attention_q4             : one tile (<= 64 positions) equals
  *                                              orc_attention_positions on the
  *                                              dequantised rows; equal scores
@@ -126,9 +135,12 @@ int orc_fugu_positions(int seq_len, int q_pos, int window, int sentinel_stride,
 int orc_attention(float* out, const float* q, const orc_kv_layout* kv,
                   int seq_len, int q_pos, int n_heads, int n_kv_heads,
                   int head_dim, double* importance, int nthreads);
+/* importance (nullable): importance[i] += sum over heads of the probability
+ * of positions[i] (f64, heads in order). */
 int orc_attention_positions(float* out, const float* q, const orc_kv_layout* kv,
                             const int32_t* positions, int n_pos, int n_heads,
-                            int n_kv_heads, int head_dim, int nthreads);
+                            int n_kv_heads, int head_dim, double* importance,
+                            int nthreads);
 /* One causal attention per listed query row r: q row r, keys [0, r]. */
 int orc_attention_rows(float* out, const float* q, int64_t q_row_stride,
                        int64_t out_row_stride, const orc_kv_layout* kv,
@@ -174,6 +186,18 @@ int   orc_gemv_q6k(const uint8_t* w, const float* x, float* out, int n_rows, int
 void  orc_mojo_sparse_attention_q4(const float* q, const float* k_q4, const float* v_q4,
                                    const int32_t* positions, float* out, int n_heads,
                                    int head_dim, int n_sparse);
+
+/* attention_sparse_q4 (swamp-engine/src/ops.rs:597-723) over Q4-20B rows
+ * addressed by kv (dtype ORC_KV_Q4): attention_sparse's position set, the
+ * rows read with that function's nibble order (low nibbles elements 0-15,
+ * high nibbles 16-31 of each group) and fma(d, nibble, dmin), weights below
+ * 1e-8 skipped.  orc_q4_a5_row is that row decode alone. */
+void orc_q4_a5_row(const uint8_t* in, int head_dim, float* out);
+int  orc_sparse_q4_positions(int seq_len, int q_pos, int window, int global_stride,
+                             int32_t* out, int cap);
+int  orc_attention_sparse_q4(float* out, const float* q, const orc_kv_layout* kv,
+                             int seq_len, int q_pos, int n_heads, int n_kv_heads,
+                             int head_dim, int window, int global_stride, int nthreads);
 
 int orc_max_threads(void);
 

@@ -103,6 +103,15 @@ def lib():
         L.orc_attention_positions.restype = C.c_int
         L.orc_attention_positions.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(KVLayout),
                                               C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                              C.c_void_p, C.c_int]
+        L.orc_q4_a5_row.restype = None
+        L.orc_q4_a5_row.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+        L.orc_sparse_q4_positions.restype = C.c_int
+        L.orc_sparse_q4_positions.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                              C.c_int]
+        L.orc_attention_sparse_q4.restype = C.c_int
+        L.orc_attention_sparse_q4.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(KVLayout), C.c_int,
+                                              C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                               C.c_int]
         L.orc_attention_rows.restype = C.c_int
         L.orc_attention_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
@@ -180,15 +189,42 @@ def attention(q: np.ndarray, layout: KVLayout, seq_len: int, q_pos: int, n_heads
 
 
 def attention_positions(q: np.ndarray, layout: KVLayout, positions: np.ndarray, n_heads: int,
-                        n_kv_heads: int, head_dim: int, threads: int = 1):
+                        n_kv_heads: int, head_dim: int, threads: int = 1,
+                        importance: bool = False):
+    """Softmax over exactly `positions`.  importance=True also returns the f64
+    sum over heads of each listed position's probability (same order as
+    `positions`)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     pos = np.ascontiguousarray(positions, dtype=np.int32)
     out = np.empty(n_heads * head_dim, dtype=np.float32)
+    imp = np.zeros(len(pos), dtype=np.float64) if importance else None
     rc = lib().orc_attention_positions(out.ctypes.data, q.ctypes.data, C.byref(layout),
                                        pos.ctypes.data, len(pos), n_heads, n_kv_heads, head_dim,
-                                       threads)
+                                       _ptr(imp), threads)
     if rc != 0:
         raise ValueError(f"orc_attention_positions failed rc={rc}")
+    return (out, imp) if importance else out
+
+
+def q4_a5_row(row: np.ndarray, head_dim: int) -> np.ndarray:
+    """One Q4-20B row decoded as attention_sparse_q4 reads it (ops.rs:640-662)."""
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    out = np.empty(head_dim, dtype=np.float32)
+    lib().orc_q4_a5_row(row.ctypes.data, head_dim, out.ctypes.data)
+    return out
+
+
+def attention_sparse_q4(q: np.ndarray, layout: KVLayout, seq_len: int, q_pos: int, n_heads: int,
+                        n_kv_heads: int, head_dim: int, window: int, global_stride: int,
+                        threads: int = 1) -> np.ndarray:
+    """ops::attention_sparse_q4 (ops.rs:597-723) over a Q4-20B layout."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    rc = lib().orc_attention_sparse_q4(out.ctypes.data, q.ctypes.data, C.byref(layout), seq_len,
+                                       q_pos, n_heads, n_kv_heads, head_dim, window,
+                                       global_stride, threads)
+    if rc != 0:
+        raise ValueError(f"orc_attention_sparse_q4 failed rc={rc}")
     return out
 
 

@@ -112,3 +112,17 @@ def test_random_tracked_pipelined(gpu, seed):
         assert np.array_equal(outs[i].cpu().numpy(), ref[i][0]), f"{c}: layer {i} output"
         assert np.array_equal(imps[i].cpu().numpy(), ref[i][1]), f"{c}: layer {i} importance"
         assert np.array_equal(scs[i].cpu().numpy(), ref[i][2], equal_nan=True), f"{c}: layer {i} scores"
+    # and the tracked calls' importance against the oracle, per position
+    for i, pb in enumerate(pbs):
+        for b in range(B):
+            L = int(pb.ctx_lens[b])
+            qpb = L - 1 if c["q_pos"] is None else c["q_pos"][b]
+            got = ref[i][1][b] - init[i][b]
+            if c["window"] > 0:
+                want = W.window_importance(pb, b, qpb, c["window"], c["stride"], got.shape[0])
+            else:
+                _, imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, qpb, H, c["hkv"],
+                                          c["hd"], importance=True)
+                want = np.zeros(got.shape[0])
+                want[:L] = imp
+            W.assert_importance(got, want, f"{c}: layer {i} importance b={b}")

@@ -87,7 +87,7 @@ def test_tracked_f16(gpu):
         L = int(pb.ctx_lens[b])
         _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, q_pos[b], pb.n_heads,
                                       pb.n_kv_heads, pb.head_dim, importance=True)
-        assert np.max(np.abs(got[b, :L] - ref_imp)) <= 1e-4 * pb.n_heads, f"f16 importance b={b}"
+        W.assert_importance(got[b, :L], ref_imp, f"f16 importance b={b}")
         assert np.all(got[b, q_pos[b] + 1:] == 0.0), f"f16 importance past valid_end b={b}"
 
 

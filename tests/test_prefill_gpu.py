@@ -120,6 +120,38 @@ def test_prefill_c5_full_size_sampled_rows(gpu):
     assert err32 <= 5e-2, err32
 
 
+def test_prefill_c5_full_size_with_paged_write(gpu):
+    """The configuration's whole work: the 8192-token chunk (32/8 heads, D=128)
+    attended and written into an f32 pool of 16-token blocks through a shuffled
+    table (the save_at loop of executor.rs:106-111, cache.rs:749-811).  Every
+    pool row of every token and kv head equals the bf16-rounded input (the
+    chunk's K/V as the kernel reads them), blocks outside the table stay
+    untouched, the output equals the call without pools bit for bit, and
+    sampled rows match the oracle."""
+    n, hq, hkv, d, bt = 8192, 32, 8, 128, 16
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=0)
+    nb = n // bt + 5
+    table = np.random.default_rng(9).permutation(nb)[: n // bt].astype(np.int32)
+    kp = torch.full((nb, hkv, bt, d), 7.0, device="cuda")
+    vp = torch.full((nb, hkv, bt, d), 7.0, device="cuda")
+    got = run_prefill(gpu, q, k, v, k_pool=kp, v_pool=vp,
+                      block_table=torch.from_numpy(table).cuda(), block_tokens=bt,
+                      kv_dtype=oracle.KV_F32, start_pos=0)
+    assert gpu.take_status()[0] == 0
+    bare = run_prefill(gpu, q, k, v)
+    assert np.array_equal(got, bare), "output with the pool write differs from the bare call"
+    kpn, vpn = kp.cpu().numpy(), vp.cpu().numpy()
+    t = np.arange(n)
+    assert np.array_equal(kpn[table[t // bt], :, t % bt], W.bf16_round(k)), "K pool rows"
+    assert np.array_equal(vpn[table[t // bt], :, t % bt], W.bf16_round(v)), "V pool rows"
+    spare = np.setdiff1d(np.arange(nb), table)
+    assert len(spare) == 5 and np.all(kpn[spare] == 7.0) and np.all(vpn[spare] == 7.0)
+    rng = np.random.default_rng(10)
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(n - 16, n),
+                                     rng.integers(0, n, 96)])).astype(np.int32)
+    check(got, oracle_rows(q, k, v, rows), rows, "prefill 8192 with paged write")
+
+
 @pytest.mark.parametrize("kv_dtype,d,hq", [(oracle.KV_F32, 128, 8), (oracle.KV_F16, 128, 8),
                                            (oracle.KV_Q4, 128, 8), (oracle.KV_F32, 64, 8),
                                            (oracle.KV_F16, 64, 2), (oracle.KV_F32, 128, 16)])
@@ -305,6 +337,49 @@ def test_chunked_prefill_through_paged_cache(gpu, kv_dtype):
         ref = oracle_ctx_rows(q[sl], k[sl], v[sl], kq[:pos], vq[:pos], r)
         check(got[sl], ref, r, f"chunked q4 at {pos}")
         pos += c
+
+
+def test_chunked_prefill_f32_history_error(gpu):
+    """A chunk after a history the f32 cache holds at full f32 precision (rows
+    written by earlier decode steps, not by a bf16 prefill): the kernel attends
+    the history gathered to bf16.  Against the oracle on that bf16 history it
+    is held to the attention tolerance; against the reference's own semantics
+    (ops::attention over the f32 cache, executor.rs:131-137, with the chunk's
+    own bf16 q/k/v) the error is reported, bounded like the bf16 input cast of
+    the full-size prefill."""
+    hq, hkv, d, bt, n_hist, n = 8, 2, 128, 16, 1000, 300
+    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=51)
+    _, kh, vh = W.prefill_inputs(n_hist, hq, hkv, d, seed=52)
+    nb = n_hist // bt + 2
+    table_np = np.random.default_rng(53).permutation(nb).astype(np.int32)
+    t = np.arange(n_hist)
+    kpool = np.zeros((nb, hkv, bt, d), np.float32)
+    vpool = np.zeros_like(kpool)
+    kpool[table_np[t // bt], :, t % bt] = kh
+    vpool[table_np[t // bt], :, t % bt] = vh
+    table = torch.from_numpy(table_np).cuda()
+    dkh = torch.empty((n_hist, hkv, d), dtype=torch.bfloat16, device="cuda")
+    dvh = torch.empty_like(dkh)
+    gpu.kv_gather_bf16(torch.from_numpy(kpool).cuda(), table, bt, hkv, d, oracle.KV_F32, n_hist, dkh)
+    gpu.kv_gather_bf16(torch.from_numpy(vpool).cuda(), table, bt, hkv, d, oracle.KV_F32, n_hist, dvh)
+    out = torch.full((n, hq, d), float("nan"), device="cuda")
+    gpu.prefill_bf16_ctx(to_dev_bf16(q), to_dev_bf16(k), to_dev_bf16(v), dkh, dvh, out, hq, hkv, d)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    rows = np.arange(n)
+    check(got, oracle_ctx_rows(q, k, v, kh, vh, rows), rows, "f32 history, bf16 semantics")
+    # the reference's semantics: f32 history, the chunk's bf16 values
+    kall = np.concatenate([kh, W.bf16_round(k)])
+    vall = np.concatenate([vh, W.bf16_round(v)])
+    lay = oracle.token_major_layout(kall, vall, hkv, d)
+    qall = np.zeros((n_hist + n, hq * d), np.float32)
+    qall[n_hist:] = W.bf16_round(q).reshape(n, -1)
+    ref32 = oracle.attention_rows(qall, lay, rows + n_hist, hq, hkv, d,
+                                  threads=oracle.max_threads())[n_hist:].reshape(n, hq, d)
+    err32 = float(np.max(np.abs(got.astype(np.float64) - ref32)))
+    rel32 = err32 / float(np.max(np.abs(ref32)))
+    print(f"chunked prefill vs f32 history: max-abs-err {err32:.3e} rel {rel32:.3e}")
+    assert err32 <= 5e-2, err32
 
 
 @pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q4])

@@ -241,3 +241,19 @@ def test_zone_decode_rejects_short_table(gpu):
     with pytest.raises(gpu.NyionError):
         run_zone_decode(gpu, q, k, v, bases[:, :100], 1, 0, [4200], 1, oracle.KV_F32,
                         max_ctx=4200)
+
+
+def test_zone_write_rejects_rows_past_the_table(gpu):
+    """A write whose last row lies on a page past the page table is refused
+    before anything is written (rows are never dropped silently)."""
+    zp = W.zone_pool(4400, n_layers=1, n_kv_heads=1, head_dim=64, kv_dtype=oracle.KV_F32, seed=51)
+    k = to_dev(np.ones((200, 1, 64), np.float32))
+    kd, vd = to_dev(zp.k_pool), to_dev(zp.v_pool)
+    # rows 4100..4299: the last is on page 128 + (4299 - 4096) // 128 = 129
+    with pytest.raises(gpu.NyionError):
+        gpu.zone_kv_write(kd, vd, to_dev(zp.page_base[:129]), 1, 0, 1, 64, oracle.KV_F32, 4100,
+                          k, k)
+    assert "page 129" in gpu.last_error()
+    gpu.zone_kv_write(kd, vd, to_dev(zp.page_base[:130]), 1, 0, 1, 64, oracle.KV_F32, 4100, k, k)
+    torch.cuda.synchronize()
+    assert not np.array_equal(kd.cpu().numpy(), zp.k_pool)

@@ -213,6 +213,46 @@ def reference_decode(pb: PagedBatch, window=0, global_stride=0, q_pos=None, thre
     return out
 
 
+# Importance (attention_tracked's per-position sum over heads of the softmax
+# probability, f64) is compared per position against the oracle: f32
+# probabilities carry ~1e-7 relative error per head, so 1e-5 of the position's
+# own value (plus 1e-7 for positions that hold almost nothing) leaves two
+# orders of magnitude of margin, while a head whose probabilities sit one
+# position off, or a head left out at one position, moves that position by
+# a whole per-head probability (~3 % of the position's importance at 32
+# heads): tests/test_importance_tolerance.py checks that such mistakes fail.
+IMP_RTOL, IMP_ATOL = 1e-5, 1e-7
+
+
+def importance_excess(got, ref, rtol=IMP_RTOL, atol=IMP_ATOL):
+    """Per-position |got - ref| / (atol + rtol |ref|); above 1 fails."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref) / (atol + rtol * np.abs(ref))
+
+
+def assert_importance(got, ref, what=""):
+    ex = importance_excess(got, ref)
+    bad = int(np.sum(~(ex <= 1.0)))
+    worst = float(np.nanmax(ex)) if ex.size else 0.0
+    assert bad == 0, (f"{what}: importance of {bad} positions outside {IMP_ATOL:g} + "
+                      f"{IMP_RTOL:g}*|ref| (worst {worst:.2f}x the bound)")
+    return worst
+
+
+def window_importance(pb: "PagedBatch", b: int, q_pos: int, window: int, global_stride: int,
+                      n: int) -> np.ndarray:
+    """The oracle's importance of sequence b over a window (with strided
+    globals) as an array of n positions, zero outside the attended set."""
+    L = int(pb.ctx_lens[b])
+    pos = oracle.sparse_positions(L, q_pos, window, global_stride)
+    _, imp = oracle.attention_positions(pb.q[b], pb.layout(b), pos, pb.n_heads, pb.n_kv_heads,
+                                        pb.head_dim, importance=True)
+    full = np.zeros(n, np.float64)
+    full[pos] = imp
+    return full
+
+
 def prefill_inputs(n, n_heads=32, n_kv_heads=8, head_dim=128, seed=0):
     """Prefill shapes: fp32 N(0,1) q [n][Hq][D], k, v [n][Hkv][D]."""
     rng = np.random.default_rng(seed)
