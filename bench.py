@@ -57,7 +57,8 @@ for sub in ("nyion.rs_amd", "oracle", "tests"):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = ("decode-attn µs/layer + achieved HBM GB/s (% peak); prefill TFLOP/s (% MFMA)")
-ALL = ("c1", "c2", "c2t", "c3", "c3h", "c3q", "c4", "c5", "abi", "zone", "gemv", "gemv6", "pool")
+ALL = ("c1", "c2", "c2t", "c3", "c3h", "c3q", "c4", "a5", "c5", "abi", "zone", "gemv", "gemv6",
+       "pool")
 
 
 def log(msg):
@@ -544,6 +545,130 @@ def bench_c4(nh, torch, steps, warmup, seed=0):
         del kp, vp, tab, calls, ws
         torch.cuda.empty_cache()
     return res
+
+
+A5_R = 32  # rotated page-base tables for the attention_sparse_q4 line
+
+
+def a5_zone_tables(rng, R, B, ctx, w, stride, n_kv_heads, row):
+    """Zone page bases of R rotation sets for B sequences (one layer): the
+    pages the call attends (the window's and the strided globals') get
+    distinct, shuffled places in one pool per (set, sequence); every other
+    page is absent (never read).  Returns ([R][B][n_pages] int64, pool bytes,
+    attended positions)."""
+    ve = ctx - 1
+    ws = ve - w + 1 if ve > w else 0
+    pos = list(range(ws, ve + 1))
+    if stride:
+        pos = [stride * g for g in range(min(ws // stride, 128))] + pos
+
+    def page(t):  # cache.rs:593-598 page_id / 235-237 block_size_for
+        if t < 4096:
+            return t >> 5, 32
+        if t < 131072:
+            return 128 + ((t - 4096) >> 7), 128
+        return 1120 + ((t - 131072) >> 10), 1024
+
+    pages = sorted({page(t) for t in pos})
+    n_pages = page(ctx - 1)[0] + 1
+    bases = np.full((R, B, n_pages), -1, np.int64)
+    off = 0
+    for r in range(R):
+        for b in range(B):
+            for i in rng.permutation(len(pages)):
+                p, bs = pages[i]
+                bases[r, b, p] = off
+                off += n_kv_heads * bs * row
+    return bases, off, len(pos)
+
+
+def bench_a5(nh, torch, steps, warmup, seed=0):
+    """ops::attention_sparse_q4 (ops.rs:597-723) on the 4-bit window workload's
+    shape: 8 sequences, ctx 131072, window 4096, 32/4 heads, D=64, zone pages
+    of Q4-20B rows (one layer), global stride 0 and 64, cold (A5_R rotated
+    page tables)."""
+    B, ctx, w, Hq, Hkv, D = 8, 131072, 4096, 32, 4, 64
+    rb = 40
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((B, Hq, D), generator=g, device="cuda")
+    ctxt = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    res = {}
+    for stride in (0, 64):
+        bases, nbytes_pool, n_pos = a5_zone_tables(rng, A5_R, B, ctx, w, stride, Hkv, rb)
+        kp = torch.empty(nbytes_pool, dtype=torch.uint8, device="cuda")
+        vp = torch.empty_like(kp)
+        rows = nbytes_pool // rb
+        chunk = 1 << 22
+        for pool in (kp, vp):
+            flat = pool.view(-1, rb)
+            for s0 in range(0, rows, chunk):
+                n = min(chunk, rows - s0)
+                x = torch.randn((n, D), generator=g, device="cuda")
+                nh.q4_quantize(x, n, D, flat[s0: s0 + n])
+        tab = torch.from_numpy(bases).cuda()
+        torch.cuda.synchronize()
+        calls = [nh.prepare_attention_sparse_q4(q, kp, vp, tab[r], 1, 0, ctxt, out, Hq, Hkv, D, w,
+                                                stride, ctx) for r in range(A5_R)]
+
+        def call(i):
+            calls[i % A5_R]()
+
+        nbytes = 2 * B * n_pos * Hkv * rb + 2 * B * Hq * D * 4
+        settle(call, torch)
+        ms = timed(call, max(steps, A5_R), warmup, torch)
+        reps = max(steps, 2 * A5_R)
+        us = event_mean(call, reps, torch) * 1e3
+        pct = event_pcts(call, reps, torch)
+        res[f"stride{stride}"] = {
+            "us_per_layer": us, "us_per_layer_wall": ms * 1e3, "us_p10_p50_p90": _us3(pct),
+            "reps": reps, "positions": n_pos, "bytes_packed": nbytes,
+            "gbs_packed": nbytes / (us * 1e-6) / 1e9,
+            "cold": f"{A5_R} rotated page tables over {2 * nbytes_pool / 1e6:.0f} MB of K+V pools",
+            "roofline": hbm_roofline(nbytes, us, None)}
+        del kp, vp, tab, calls
+        torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline_a5(seed=0):
+    """The oracle's attention_sparse_q4 (ops.rs:597-723) on all 8 sequences of
+    the 4-bit window workload (window 4096, global stride 0), rows quantised."""
+    import oracle
+
+    B, ctx, w, hkv, hd = 8, 131072, 4096, 4, 64
+    rng = np.random.default_rng(seed)
+    rb = oracle.q4_row_bytes(hd)
+    pos = oracle.sparse_positions(ctx, ctx - 1, w, 0)
+    lo = int(pos[0])
+    # rows [lo, ctx) of each sequence, contiguous per kv head; earlier rows are never read
+    ks = [oracle.q4_quantize_rows(rng.standard_normal((hkv * (ctx - lo), hd), dtype=np.float32))
+          for _ in range(B)]
+    vs = [oracle.q4_quantize_rows(rng.standard_normal((hkv * (ctx - lo), hd), dtype=np.float32))
+          for _ in range(B)]
+    q = rng.standard_normal((B, 32, hd), dtype=np.float32)
+    lays = []
+    for b in range(B):
+        k = ks[b].reshape(hkv, ctx - lo, rb)
+        v = vs[b].reshape(hkv, ctx - lo, rb)
+        # a layout whose row of position t is row t - lo of the arrays
+        lay = oracle.contiguous_layout(np.ascontiguousarray(k), np.ascontiguousarray(v), ctx - lo,
+                                       hd, oracle.KV_Q4)
+        lay.k_base -= lo * rb
+        lay.v_base -= lo * rb
+        lays.append(lay)
+    thr = _cores()
+
+    def run():
+        for b in range(B):
+            oracle.attention_sparse_q4(q[b], lays[b], ctx, ctx - 1, 32, hkv, hd, w, 0, threads=thr)
+
+    dt, n = _cpu_time(run)
+    nbytes = 2 * B * len(pos) * hkv * rb
+    return {"value": dt * 1e6, "unit": "us/layer", "cores": thr, "kind": "port",
+            "gbs_packed": nbytes / dt / 1e9,
+            "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0"}
 
 
 def cpu_baseline_c4(seed=0):
@@ -1133,6 +1258,10 @@ def main():
         log("Q4 KV, ctx 131072, window 4096 (cold: rotated tables)")
         res["c4"] = bench_c4(nh, torch, steps, warmup)
         torch.cuda.empty_cache()
+    if "a5" in only:
+        log("attention_sparse_q4 on zone pages, ctx 131072, window 4096 (cold)")
+        res["a5"] = bench_a5(nh, torch, steps, warmup)
+        torch.cuda.empty_cache()
     if "c5" in only:
         log("causal prefill N=8192 with paged KV write")
         res["c5"] = bench_c5(nh, torch, steps, warmup)
@@ -1152,7 +1281,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         for key, fn in (("c1", cpu_baseline_c1), ("c2", cpu_baseline_c2), ("c4", cpu_baseline_c4),
-                        ("c5", cpu_baseline_c5)):
+                        ("a5", cpu_baseline_a5), ("c5", cpu_baseline_c5)):
             if key in res:
                 log(f"CPU baseline (oracle) for {key}")
                 res[key]["cpu_baseline"] = fn()

@@ -359,6 +359,32 @@ int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void
                                 int max_ctx, float scale, float* d_out, void* d_workspace,
                                 size_t workspace_bytes, nyion_stream_t stream);
 
+/* ops::attention_sparse_q4 (swamp-engine/src/ops.rs:597-723) over one layer
+ * of zone pools of Q4-20B rows (pool_bytes bytes each, page_bases as for
+ * nyion_zone_decode_attention).  Per sequence b: valid_end = min(q_pos[b],
+ * ctx_lens[b] - 1) (q_pos null: ctx_lens[b] - 1); the positions are
+ * attention_sparse's (global_stride * i for i < min(window_start /
+ * global_stride, 128), then window_start .. valid_end, window_start =
+ * valid_end - window + 1 when valid_end > window, else 0; global_stride <= 0
+ * gives no globals where the reference divides by it).  Rows are read with
+ * that function's own rules: group g of the row is the 20 bytes at (slot *
+ * groups + g) * 20 of the (layer, kv head) block of the position's page,
+ * its nibble bytes give elements 0-15 (low nibbles) and 16-31 (high
+ * nibbles), element = fma(d, nibble, dmin); q.k in the reference's 16-lane
+ * FMA order times 1/sqrt(head_dim); weights below 1e-8 are skipped.  Rows
+ * of absent pages are skipped.  head_dim 64 or 128, at most 32 q heads per
+ * kv head; max_ctx >= every ctx_lens[b] and covered by the table.  The
+ * workspace (256-byte aligned, no initial contents) is sized by
+ * nyion_attention_sparse_q4_workspace_size. */
+size_t nyion_attention_sparse_q4_workspace_size(int batch, int n_heads, int head_dim, int window,
+                                                int max_ctx);
+int nyion_attention_sparse_q4(const float* d_q, const void* k_pool, const void* v_pool,
+                              int64_t pool_bytes, const int64_t* page_bases, int max_pages_per_seq,
+                              int n_layers, int layer, const int32_t* ctx_lens, const int32_t* q_pos,
+                              int batch, int n_heads, int n_kv_heads, int head_dim, int window,
+                              int global_stride, int max_ctx, float* d_out, void* d_workspace,
+                              size_t workspace_bytes, nyion_stream_t stream);
+
 /* ------------------------------------------ per-layer ring and Fugu policy */
 
 /* Sliding-window KV rings of the GPU decode path: PerLayerGpuState

@@ -124,6 +124,9 @@ SIGNATURES = {
     "nyion_zone_kv_gather": (i32, [vp, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_zone_decode_attention": (i32, [vp, vp, vp, i64, vp, i32, i32, i32, vp, vp, i32, i32,
                                           i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
+    "nyion_attention_sparse_q4_workspace_size": (sz, [i32, i32, i32, i32, i32]),
+    "nyion_attention_sparse_q4": (i32, [vp, vp, vp, i64, vp, i32, i32, i32, vp, vp, i32, i32, i32,
+                                        i32, i32, i32, i32, vp, vp, sz, vp]),
     "nyion_page_policy_create": (vp, [i32, i32, i32]),
     "nyion_page_policy_destroy": (None, [vp]),
     "nyion_page_policy_ensure": (i32, [vp, i32, i32, vp, i32, C.POINTER(C.c_int)]),
@@ -618,6 +621,52 @@ def zone_decode(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens, out, n
         stream_handle(stream))
     check(rc, "nyion_zone_decode_attention")
     return workspace
+
+
+def attention_sparse_q4(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens, out, n_heads,
+                        n_kv_heads, head_dim, window, global_stride, max_ctx=None, q_pos=None,
+                        workspace=None, stream=None):
+    """ops::attention_sparse_q4 over zone pools of Q4-20B rows (uint8 tensors);
+    q [B][Hq][D] f32, page_bases [B][max_pages] int64, ctx_lens [B] int32."""
+    B = q.shape[0]
+    if max_ctx is None:
+        max_ctx = int(ctx_lens.max().item())
+    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, head_dim, window, max_ctx)
+    if workspace is None and need:
+        workspace = _torch().empty(need, dtype=_torch().uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = load().nyion_attention_sparse_q4(
+        ptr(q), ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_bases), page_bases.shape[1],
+        n_layers, layer, ptr(ctx_lens), ptr(q_pos), B, n_heads, n_kv_heads, head_dim, window,
+        global_stride, max_ctx, ptr(out), ptr(workspace), ws_bytes, stream_handle(stream))
+    check(rc, "nyion_attention_sparse_q4")
+    return workspace
+
+
+def prepare_attention_sparse_q4(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens, out,
+                                n_heads, n_kv_heads, head_dim, window, global_stride, max_ctx,
+                                q_pos=None, workspace=None, stream=None):
+    """attention_sparse_q4 with every argument resolved once: a no-argument
+    callable that only crosses the C ABI."""
+    B = q.shape[0]
+    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, head_dim, window, max_ctx)
+    if workspace is None and need:
+        workspace = _torch().empty(need, dtype=_torch().uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    fn = load().nyion_attention_sparse_q4
+    args = (ptr(q), ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_bases),
+            page_bases.shape[1], n_layers, layer, ptr(ctx_lens), ptr(q_pos), B, n_heads,
+            n_kv_heads, head_dim, window, global_stride, max_ctx, ptr(out), ptr(workspace),
+            ws_bytes, stream_handle(stream))
+    keep = (q, k_pool, v_pool, page_bases, ctx_lens, out, q_pos, workspace)
+
+    def call():
+        rc = fn(*args)
+        if rc != 0:
+            check(rc, "nyion_attention_sparse_q4")
+
+    call.keep = keep
+    return call
 
 
 def sparse_attention_q4(q, k_q4, v_q4, positions, n_heads, head_dim, window=0, global_stride=0):
