@@ -373,11 +373,13 @@ int nyion_zone_decode_attention(const float* d_q, const void* k_pool, const void
  * nibbles), element = fma(d, nibble, dmin); q.k in the reference's 16-lane
  * FMA order times 1/sqrt(head_dim); weights below 1e-8 are skipped.  Rows
  * of absent pages are skipped.  head_dim 64 or 128, at most 32 q heads per
- * kv head; max_ctx >= every ctx_lens[b] and covered by the table.  The
- * workspace (256-byte aligned, no initial contents) is sized by
- * nyion_attention_sparse_q4_workspace_size. */
-size_t nyion_attention_sparse_q4_workspace_size(int batch, int n_heads, int head_dim, int window,
-                                                int max_ctx);
+ * kv head; max_ctx >= every ctx_lens[b] and covered by the table; q and
+ * out 16-byte aligned.  The workspace (256-byte aligned) is sized by
+ * nyion_attention_sparse_q4_workspace_size and zero-filled before its first
+ * use (nyion_decode_workspace_init); every call leaves its arrival counters
+ * at zero.  Calls sharing a workspace must not overlap. */
+size_t nyion_attention_sparse_q4_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
+                                                int window, int max_ctx);
 int nyion_attention_sparse_q4(const float* d_q, const void* k_pool, const void* v_pool,
                               int64_t pool_bytes, const int64_t* page_bases, int max_pages_per_seq,
                               int n_layers, int layer, const int32_t* ctx_lens, const int32_t* q_pos,

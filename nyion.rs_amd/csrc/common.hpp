@@ -80,6 +80,15 @@ __device__ __forceinline__ void report_range(unsigned* status, bool bad, unsigne
         __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Split-K partials cross workgroups that may sit on different XCDs, whose
+// L2s are not coherent with each other: they are stored and loaded with the
+// sc1 cache policy (what agent-scope relaxed atomic loads and stores carry on
+// this target) through buffer instructions, 16 bytes per instruction.
+constexpr int kSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
 static inline bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
 static inline int ilog2(long long x) {
     int r = 0;

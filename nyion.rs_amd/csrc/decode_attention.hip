@@ -65,14 +65,6 @@ typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(8)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Split-K partials cross workgroups that may sit on different XCDs, whose
-// L2s are not coherent with each other: they are stored and loaded with the
-// sc1 cache policy (what agent-scope relaxed atomic loads and stores carry on
-// this target) through buffer instructions, 16 bytes per instruction.
-constexpr int kSc1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
-}
 
 enum DecodeMode { MODE_FULL = 0, MODE_WINDOW = 1, MODE_LIST = 2 };
 

@@ -19,7 +19,7 @@
 //
 // Work: a segment is (sequence, kv head); its position list is cut into
 // pieces of 256 positions, one workgroup each (the grid covers the host's
-// bound on the list).  Three launches, no cross-workgroup waits:
+// bound on the list).  Two launches, no cross-workgroup waits:
 //   1. scores: one thread per position decodes its K row, scores every q
 //      head of the group, stores the scores and the piece's per-head
 //      (max, sum of exp) partials;
@@ -27,8 +27,8 @@
 //      head's max and 1/sum (pieces in order), turns its scores into
 //      weights (dropping those below 1e-8), decodes its V rows into LDS in
 //      16 KiB batches and accumulates sum(w * v) in position order;
-//   3. merge: the output is the sum of the pieces' partial outputs in piece
-//      order (skipped when one piece covers every sequence).
+//      the segment's last piece to finish (an arrival counter) adds the
+//      pieces' partial outputs in piece order (one piece: written directly).
 // Bytes per attended (token, kv head): K and V rows, 2 * 20 * head_dim / 32.
 #include <math.h>
 
@@ -36,9 +36,9 @@
 
 namespace nyion {
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 constexpr int kSq4Threads = 256;    // positions per piece
-// V rows decoded into LDS per batch: 16 KiB of f32, one 16-element unit per thread
-template <int D> constexpr int sq4_vrows() { return 4096 / D; }
 constexpr int kSq4MaxGroup = 32;    // q heads per kv head
 constexpr int kSq4MaxGlobals = 128;  // ops.rs:615
 
@@ -53,6 +53,7 @@ struct Sq4Args {
     float* scores;              // [seg][group][pieces * 256]
     float2* ml;                 // [seg][pieces][group] (max, sum of exp)
     float* part;                // [seg][pieces][group][D]
+    int* counters;              // [seg] arrivals, zero between calls
     ZoneMap zone;
     int n_heads, n_kv_heads, group, pieces, window, global_stride;
     float scale;
@@ -105,54 +106,92 @@ __device__ __forceinline__ void sq4_half(const uint32_t* w5, int half, float* ou
     }
 }
 
+// Wavefront max / sum through DPP row operations (a fixed tree, so the sum
+// is the same on every call): lane pairs, quads, half rows, rows, then the
+// rows combined through row broadcasts; every lane gets lane 63's result.
+template <bool MAX>
+__device__ __forceinline__ float sq4_op(float x, float y) {
+    return MAX ? fmaxf(x, y) : x + y;
+}
+
+template <bool MAX, int CTRL, int ROW_MASK>
+__device__ __forceinline__ float sq4_dpp_step(float x) {
+    const float id = MAX ? -INFINITY : 0.0f;
+    const float y = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+    return sq4_op<MAX>(x, y);
+}
+
+template <bool MAX>
+__device__ __forceinline__ float sq4_wave_reduce(float x) {
+    x = sq4_dpp_step<MAX, 0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
+    x = sq4_dpp_step<MAX, 0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
+    x = sq4_dpp_step<MAX, 0x141, 0xf>(x);  // row_half_mirror
+    x = sq4_dpp_step<MAX, 0x140, 0xf>(x);  // row_mirror: each row's lanes hold the row's value
+    x = sq4_dpp_step<MAX, 0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x = sq4_dpp_step<MAX, 0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+typedef const __attribute__((address_space(4))) float* sq4_cfloat_ptr;
+
 template <int D>
 __global__ __launch_bounds__(kSq4Threads) void sq4_scores_kernel(Sq4Args a) {
     constexpr int G = D / 32;           // groups per row
     constexpr int W = G * 5;            // 4-byte words per row
-    extern __shared__ float sm[];
-    float* q_s = sm;                     // [group][D]
-    float* sc_s = sm + a.group * D;      // [group][256]
+    extern __shared__ float4 sm4[];  // 16-byte aligned: float4 accesses
+    float* sm = (float*)sm4;
+    float* sc_s = sm;                   // [group][256]
     const int seg = blockIdx.y, piece = blockIdx.x;
     const int b = seg / a.n_kv_heads, h = seg % a.n_kv_heads;
     const int tid = threadIdx.x;
     const Sq4List l = sq4_list(a, b);
-    const float* qb = a.q + ((long long)b * a.n_heads + (long long)h * a.group) * D;
-    for (int i = tid; i < a.group * D; i += kSq4Threads) q_s[i] = qb[i];
     const int i = piece * kSq4Threads + tid;
     long long off = -1;
     if (i < l.n) off = sq4_row(a, b, sq4_pos(a, l, i), h, W * 4);
-    float kf[D];
+    // q of the group is the same for every lane: it is read through the
+    // constant address space into scalar registers, each FMA taking its q
+    // operand from there.  Its 64-byte lines are requested together here
+    // (32 at a time), so the per-head loads below hit the scalar cache.
+    const sq4_cfloat_ptr qb =
+        (sq4_cfloat_ptr)(a.q + ((long long)b * a.n_heads + (long long)h * a.group) * D);
+    for (int x0 = 0; x0 < a.group * D; x0 += 32 * 16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 32; x++) t += x0 + 16 * x < a.group * D ? qb[x0 + 16 * x] : 0.0f;
+        asm volatile("" ::"s"(t));
+    }
+    // the row's words (plain loads: the lanes' 40- or 80-byte rows share cache
+    // lines, which the later words of the row hit in L1)
+    uint32_t w[W];
+#pragma unroll
+    for (int x = 0; x < W; x++) w[x] = 0;
     if (off >= 0) {
         const uint32_t* rw = (const uint32_t*)(a.k + off);
-        uint32_t w[W];
 #pragma unroll
-        for (int x = 0; x < W; x++) w[x] = __builtin_nontemporal_load(rw + x);
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            sq4_half(w + 5 * g, 0, kf + 32 * g);
-            sq4_half(w + 5 * g, 1, kf + 32 * g + 16);
-        }
+        for (int x = 0; x < W; x++) w[x] = rw[x];
     }
-    __syncthreads();
+    float kf[D];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        sq4_half(w + 5 * g, 0, kf + 32 * g);
+        sq4_half(w + 5 * g, 1, kf + 32 * g + 16);
+    }
+    float* srow = a.scores + (long long)seg * a.group * ((long long)a.pieces * kSq4Threads) + i;
     for (int r = 0; r < a.group; r++) {
-        float s = -INFINITY;
-        if (off >= 0) {
-            const float* qr = q_s + r * D;
-            float acc[16];
+        float acc[16];
 #pragma unroll
-            for (int x = 0; x < 16; x++) acc[x] = 0.0f;
+        for (int x = 0; x < 16; x++) acc[x] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < D; c += 16)
+        for (int c = 0; c < D; c += 16)
 #pragma unroll
-                for (int x = 0; x < 16; x++) acc[x] = __builtin_fmaf(kf[c + x], qr[c + x], acc[x]);
-            float dot = 0.0f;
+            for (int x = 0; x < 16; x++) acc[x] = __builtin_fmaf(kf[c + x], qb[r * D + c + x], acc[x]);
+        float dot = 0.0f;
 #pragma unroll
-            for (int x = 0; x < 16; x++) dot = dot + acc[x];
-            s = dot * a.scale;
-        }
+        for (int x = 0; x < 16; x++) dot = dot + acc[x];
+        const float s = off >= 0 ? dot * a.scale : -INFINITY;
         sc_s[r * kSq4Threads + tid] = s;
-        if (i < l.n)
-            a.scores[((long long)seg * a.group + r) * ((long long)a.pieces * kSq4Threads) + i] = s;
+        if (i < l.n) srow[(long long)r * a.pieces * kSq4Threads] = s;
     }
     __syncthreads();
     // per head: the piece's max and sum of exp(s - max), one wavefront per head
@@ -161,30 +200,36 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_scores_kernel(Sq4Args a) {
         float v[4];
 #pragma unroll
         for (int x = 0; x < 4; x++) v[x] = sc_s[r * kSq4Threads + lane + 64 * x];
-        float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float m = sq4_wave_reduce<true>(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
         float e = 0.0f;
         if (m != -INFINITY) {
 #pragma unroll
             for (int x = 0; x < 4; x++) e += v[x] == -INFINITY ? 0.0f : expf(v[x] - m);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o);
+        e = sq4_wave_reduce<false>(e);
         if (lane == 0) a.ml[((long long)seg * a.pieces + piece) * a.group + r] = float2{m, e};
     }
 }
+
+// LDS rows of decoded V per batch: 32 KiB of f32 (two batches of 128 rows at
+// head_dim 64, four of 64 at head_dim 128), rows padded by 4 floats, so that
+// three workgroups fit a CU's LDS.
+template <int D> constexpr int sq4_vrows() { return 8192 / D; }
+template <int D> constexpr int sq4_vstride() { return D + 4; }
+constexpr int kSq4Hb = 8;  // heads per thread in the weighted sum
 
 template <int D>
 __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
     constexpr int G = D / 32;
     constexpr int W = G * 5;
-    constexpr int kMaxOut = kSq4MaxGroup * D / kSq4Threads;
-    extern __shared__ float sm[];
-    float* w_s = sm;                             // [group][256] weights (0: skipped)
-    constexpr int VR = sq4_vrows<D>();
-    float* v_s = sm + a.group * kSq4Threads;     // [VR][D] decoded V rows
-    float* mi_s = v_s + VR * D;                  // [group][2] (max, 1/sum)
+    constexpr int VR = sq4_vrows<D>(), VS = sq4_vstride<D>();
+    constexpr int Q = D / 4;  // 4-dim quads per row
+    const int WP = (a.group + kSq4Hb - 1) / kSq4Hb * kSq4Hb;  // weights per row, padded
+    extern __shared__ float4 sm4[];  // 16-byte aligned: float4 accesses
+    float* sm = (float*)sm4;
+    float* w_s = sm;                    // [256][WP] weights (0: skipped or padding)
+    float* v_s = w_s + kSq4Threads * WP;  // [VR][VS] decoded V rows; then split sums
+    float* mi_s = v_s + VR * VS;        // [group][2] (max, 1/sum)
     const int seg = blockIdx.y, piece = blockIdx.x;
     const int b = seg / a.n_kv_heads, h = seg % a.n_kv_heads;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -193,24 +238,35 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
     const int n_here = l.n - first < kSq4Threads ? l.n - first : kSq4Threads;
     // pieces holding positions (a context past max_ctx is cut at the grid)
     const int used = min((l.n + kSq4Threads - 1) / kSq4Threads, a.pieces);
+    // this thread's V row (position first + tid), in flight during the merge
+    long long off = -1;
+    if (tid < n_here) off = sq4_row(a, b, sq4_pos(a, l, first + tid), h, W * 4);
+    uint32_t vw[W];
+#pragma unroll
+    for (int x = 0; x < W; x++) vw[x] = 0;
+    if (off >= 0) {
+        const uint32_t* rw = (const uint32_t*)(a.v + off);
+#pragma unroll
+        for (int x = 0; x < W; x++) vw[x] = rw[x];
+    }
     // the head's max and 1/sum over the pieces, in piece order
     for (int r = wave; r < a.group; r += kSq4Threads / 64) {
         const float2* mlr = a.ml + (long long)seg * a.pieces * a.group + r;
-        float m = -INFINITY;
-        for (int p = lane; p < used; p += 64) m = fmaxf(m, mlr[(long long)p * a.group].x);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float2 mine = lane < used ? mlr[(long long)lane * a.group] : float2{-INFINITY, 0.0f};
+        float m = mine.x;
+        for (int p = lane + 64; p < used; p += 64) m = fmaxf(m, mlr[(long long)p * a.group].x);
+        m = sq4_wave_reduce<true>(m);
         float sum = 0.0f;
         if (m != -INFINITY) {
-            for (int p0 = 0; p0 < used; p0 += 64) {
-                float e = 0.0f;
+            float e = mine.x == -INFINITY ? 0.0f : mine.y * expf(mine.x - m);
+            sum = sq4_wave_reduce<false>(e);
+            for (int p0 = 64; p0 < used; p0 += 64) {  // more than 64 pieces
+                e = 0.0f;
                 if (p0 + lane < used) {
                     const float2 x = mlr[(long long)(p0 + lane) * a.group];
                     e = x.x == -INFINITY ? 0.0f : x.y * expf(x.x - m);
                 }
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o);
-                sum += e;
+                sum += sq4_wave_reduce<false>(e);
             }
         }
         if (lane == 0) {
@@ -219,86 +275,157 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
         }
     }
     __syncthreads();
-    for (int r = 0; r < a.group; r++) {
-        float w = 0.0f;
-        if (tid < n_here) {
-            const float s = a.scores[((long long)seg * a.group + r) * ((long long)a.pieces * kSq4Threads) +
-                                     first + tid];
-            if (s != -INFINITY) {
-                w = expf(s - mi_s[2 * r]) * mi_s[2 * r + 1];
-                if (w < 1e-8f) w = 0.0f;  // ops.rs:692
+    {
+        // every head's weight of this position; score loads in flight together
+        float sv[kSq4MaxGroup];
+        const float* src = a.scores + (long long)seg * a.group * ((long long)a.pieces * kSq4Threads) +
+                           first + tid;
+#pragma unroll
+        for (int r = 0; r < kSq4MaxGroup; r++)
+            sv[r] = r < a.group && tid < n_here ? src[(long long)r * a.pieces * kSq4Threads] : -INFINITY;
+#pragma unroll
+        for (int r = 0; r < kSq4MaxGroup; r++) {
+            if (r < WP) {
+                float w = 0.0f;
+                if (r < a.group && sv[r] != -INFINITY) {
+                    w = expf(sv[r] - mi_s[2 * r]) * mi_s[2 * r + 1];
+                    if (w < 1e-8f) w = 0.0f;  // ops.rs:692
+                }
+                w_s[tid * WP + r] = w;
             }
         }
-        w_s[r * kSq4Threads + tid] = w;
     }
-    const int n_out = a.group * D;
-    float acc[kMaxOut];
+    // weighted sum: a thread owns one 4-dim quad of kSq4Hb heads (block hb)
+    // over one of `splits` consecutive ranges of each batch's rows
+    const int nhb = WP / kSq4Hb;
+    const int quad = tid % Q, rest = tid / Q;
+    const int hb = rest % nhb, split = rest / nhb;
+    const int splits = (kSq4Threads / Q) / nhb;
+    const bool active = split < splits;
+    float acc[kSq4Hb][4];
 #pragma unroll
-    for (int x = 0; x < kMaxOut; x++) acc[x] = 0.0f;
-    for (int r0 = 0; r0 < n_here; r0 += VR) {
+    for (int k = 0; k < kSq4Hb; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) acc[k][x] = 0.0f;
+    for (int b0 = 0; b0 < n_here; b0 += VR) {
         __syncthreads();  // weights written / the previous batch consumed
-        // decode rows r0 .. r0 + VR - 1 of the piece: 16-element units, D/16 per row
-        for (int u = tid; u < VR * (D / 16); u += kSq4Threads) {
-            const int p = u / (D / 16), gu = u % (D / 16);
-            float vals[16];
-            long long off = -1;
-            if (r0 + p < n_here) off = sq4_row(a, b, sq4_pos(a, l, first + r0 + p), h, W * 4);
-            if (off >= 0) {
-                const uint32_t* gw = (const uint32_t*)(a.v + off) + 5 * (gu >> 1);
-                uint32_t w5[5];
+        if (tid >= b0 && tid < b0 + VR) {
+            float* dst = v_s + (tid - b0) * VS;
 #pragma unroll
-                for (int x = 0; x < 5; x++) w5[x] = __builtin_nontemporal_load(gw + x);
-                sq4_half(w5, gu & 1, vals);
-            } else {
+            for (int g = 0; g < G; g++) {
+                float vals[16];
+                sq4_half(vw + 5 * g, 0, vals);
 #pragma unroll
-                for (int x = 0; x < 16; x++) vals[x] = 0.0f;
+                for (int x = 0; x < 4; x++)
+                    *(float4*)(dst + 32 * g + 4 * x) =
+                        float4{vals[4 * x], vals[4 * x + 1], vals[4 * x + 2], vals[4 * x + 3]};
+                sq4_half(vw + 5 * g, 1, vals);
+#pragma unroll
+                for (int x = 0; x < 4; x++)
+                    *(float4*)(dst + 32 * g + 16 + 4 * x) =
+                        float4{vals[4 * x], vals[4 * x + 1], vals[4 * x + 2], vals[4 * x + 3]};
             }
-            float4* dst = (float4*)(v_s + p * D + 16 * gu);
-#pragma unroll
-            for (int x = 0; x < 4; x++)
-                dst[x] = float4{vals[4 * x], vals[4 * x + 1], vals[4 * x + 2], vals[4 * x + 3]};
         }
         __syncthreads();
-        const int rows = n_here - r0 < VR ? n_here - r0 : VR;
+        const int rows = n_here - b0 < VR ? n_here - b0 : VR;
+        const int chunk = (rows + splits - 1) / splits;
+        const int p_lo = split * chunk, p_hi = min(rows, p_lo + chunk);
+        if (active) {
+            const float* vq = v_s + 4 * quad;
+            const float* wq = w_s + (b0 * WP) + kSq4Hb * hb;
+            for (int p = p_lo; p < p_hi; p++) {
+                const float4 v = *(const float4*)(vq + p * VS);
+                const float4 w0 = *(const float4*)(wq + p * WP);
+                const float4 w1 = *(const float4*)(wq + p * WP + 4);
+                const float w[kSq4Hb] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int x = 0; x < kMaxOut; x++) {
-            const int o = tid + kSq4Threads * x;
-            if (o < n_out) {
-                const int r = o / D, d = o % D;
-                const float* wr = w_s + r * kSq4Threads + r0;
-                for (int p = 0; p < rows; p++) {
-                    const float w = wr[p];
-                    if (w != 0.0f) acc[x] = __builtin_fmaf(v_s[p * D + d], w, acc[x]);
+                for (int k = 0; k < kSq4Hb; k++) {
+                    // a skipped weight leaves the sum as it is (no 0 * v)
+                    const bool on = w[k] != 0.0f;
+                    acc[k][0] = on ? __builtin_fmaf(v.x, w[k], acc[k][0]) : acc[k][0];
+                    acc[k][1] = on ? __builtin_fmaf(v.y, w[k], acc[k][1]) : acc[k][1];
+                    acc[k][2] = on ? __builtin_fmaf(v.z, w[k], acc[k][2]) : acc[k][2];
+                    acc[k][3] = on ? __builtin_fmaf(v.w, w[k], acc[k][3]) : acc[k][3];
                 }
             }
         }
     }
-    // pieces past the list write zeros, so the merge reads defined values
-    const bool direct = a.pieces == 1;
+    // the splits' sums, added in split order
+    __syncthreads();  // v_s is free
+    float* red = v_s;  // [splits][WP][D]
+    if (active) {
 #pragma unroll
-    for (int x = 0; x < kMaxOut; x++) {
-        const int o = tid + kSq4Threads * x;
-        if (o < n_out) {
-            const int r = o / D, d = o % D;
-            if (direct)
-                a.out[((long long)b * a.n_heads + (long long)h * a.group + r) * D + d] = acc[x];
-            else
-                a.part[(((long long)seg * a.pieces + piece) * a.group + r) * D + d] = acc[x];
+        for (int k = 0; k < kSq4Hb; k++)
+            *(float4*)(red + ((long long)split * WP + kSq4Hb * hb + k) * D + 4 * quad) =
+                float4{acc[k][0], acc[k][1], acc[k][2], acc[k][3]};
+    }
+    __syncthreads();
+    const bool direct = a.pieces == 1;
+    float* out_b = a.out + ((long long)b * a.n_heads + (long long)h * a.group) * D;
+    float* part_s = a.part + (long long)seg * a.pieces * a.group * D;
+    const __amdgpu_buffer_rsrc_t rpart =
+        partial_rsrc(part_s, direct ? 0u : (uint32_t)(a.pieces * a.group * D * 4));
+    for (int o4 = tid; o4 < a.group * Q; o4 += kSq4Threads) {
+        const int r = o4 / Q, qd = o4 % Q;
+        float4 t = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+        for (int sp = 0; sp < splits; sp++) {
+            const float4 x = *(const float4*)(red + ((long long)sp * WP + r) * D + 4 * qd);
+            t.x += x.x;
+            t.y += x.y;
+            t.z += x.z;
+            t.w += x.w;
+        }
+        if (direct) {
+            *(float4*)(out_b + r * D + 4 * qd) = t;
+        } else if (piece < used) {  // pieces past the list hold nothing to add
+            const u32x4_t d = {__float_as_uint(t.x), __float_as_uint(t.y), __float_as_uint(t.z),
+                               __float_as_uint(t.w)};
+            __builtin_amdgcn_raw_buffer_store_b128(d, rpart, ((piece * a.group + r) * D + 4 * qd) * 4, 0,
+                                                   kSc1);
         }
     }
-}
-
-template <int D>
-__global__ __launch_bounds__(kSq4Threads) void sq4_merge_kernel(Sq4Args a) {
-    const int seg = blockIdx.y;
-    const int b = seg / a.n_kv_heads, h = seg % a.n_kv_heads;
-    const int o = blockIdx.x * kSq4Threads + threadIdx.x;
-    if (o >= a.group * D) return;
-    const Sq4List l = sq4_list(a, b);
-    const int used = min((l.n + kSq4Threads - 1) / kSq4Threads, a.pieces);
-    float s = 0.0f;
-    for (int p = 0; p < used; p++) s += a.part[((long long)seg * a.pieces + p) * a.group * D + o];
-    a.out[((long long)b * a.n_heads + (long long)h * a.group) * D + o] = s;
+    if (direct) return;
+    // publish: every wavefront's write-through stores complete, then the
+    // piece's arrival is counted; the segment's last piece to arrive adds
+    // the pieces' partial outputs in piece order and resets the counter
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int last;
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.counters + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               a.pieces - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int o4 = tid; o4 < a.group * Q; o4 += kSq4Threads) {
+        const int r = o4 / Q, qd = o4 % Q;
+        const uint32_t off0 = (r * D + 4 * qd) * 4, step = a.group * D * 4;
+        float4 t = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        int p = 0;
+        for (; p + 8 <= used; p += 8) {  // eight loads in flight, added in piece order
+            u32x4_t x[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                x[k] = __builtin_amdgcn_raw_buffer_load_b128(rpart, off0 + (p + k) * step, 0, kSc1);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                t.x += __uint_as_float(x[k][0]);
+                t.y += __uint_as_float(x[k][1]);
+                t.z += __uint_as_float(x[k][2]);
+                t.w += __uint_as_float(x[k][3]);
+            }
+        }
+        for (; p < used; p++) {
+            const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rpart, off0 + p * step, 0, kSc1);
+            t.x += __uint_as_float(x[0]);
+            t.y += __uint_as_float(x[1]);
+            t.z += __uint_as_float(x[2]);
+            t.w += __uint_as_float(x[3]);
+        }
+        *(float4*)(out_b + r * D + 4 * qd) = t;
+    }
+    if (tid == 0) __hip_atomic_store(a.counters + seg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 static long long sq4_bound(int window, int max_ctx) {
@@ -308,39 +435,39 @@ static long long sq4_bound(int window, int max_ctx) {
 
 struct Sq4Sizes {
     int pieces;
-    size_t scores, ml, part;
+    size_t scores, ml, part, counters;
+    size_t total() const { return scores + ml + part + counters; }
 };
 
-static Sq4Sizes sq4_sizes(int batch, int n_heads, int head_dim, int window, int max_ctx) {
+static Sq4Sizes sq4_sizes(int batch, int n_heads, int n_kv_heads, int head_dim, int window,
+                          int max_ctx) {
     Sq4Sizes z;
     z.pieces = (int)((sq4_bound(window, max_ctx) + kSq4Threads - 1) / kSq4Threads);
     const size_t rows = (size_t)batch * n_heads;  // (sequence, q head)
     z.scores = rows * z.pieces * kSq4Threads * sizeof(float);
     z.ml = rows * z.pieces * sizeof(float2);
     z.part = z.pieces > 1 ? rows * z.pieces * head_dim * sizeof(float) : 0;
+    z.counters = z.pieces > 1 ? (size_t)batch * n_kv_heads * sizeof(int) : 0;
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     z.scores = up(z.scores);
     z.ml = up(z.ml);
     z.part = up(z.part);
+    z.counters = up(z.counters);
     return z;
 }
 
 template <int D>
 static int sq4_launch(Sq4Args& a, int batch, hipStream_t st) {
     const dim3 grid(a.pieces, batch * a.n_kv_heads);
-    const size_t lds1 = (size_t)a.group * (D + kSq4Threads) * sizeof(float);
-    const size_t lds2 = ((size_t)a.group * (kSq4Threads + 2) + sq4_vrows<D>() * D) * sizeof(float);
+    const int wp = (a.group + kSq4Hb - 1) / kSq4Hb * kSq4Hb;
+    const size_t lds1 = (size_t)a.group * kSq4Threads * sizeof(float);
+    const size_t lds2 = ((size_t)kSq4Threads * wp + sq4_vrows<D>() * sq4_vstride<D>() + 2 * a.group) *
+                        sizeof(float);
     hipLaunchKernelGGL(sq4_scores_kernel<D>, grid, dim3(kSq4Threads), lds1, st, a);
     int rc = check_launch("attention_sparse_q4 scores");
     if (rc != NYION_OK) return rc;
     hipLaunchKernelGGL(sq4_values_kernel<D>, grid, dim3(kSq4Threads), lds2, st, a);
-    if ((rc = check_launch("attention_sparse_q4 values")) != NYION_OK) return rc;
-    if (a.pieces > 1) {
-        const dim3 g3((a.group * D + kSq4Threads - 1) / kSq4Threads, batch * a.n_kv_heads);
-        hipLaunchKernelGGL(sq4_merge_kernel<D>, g3, dim3(kSq4Threads), 0, st, a);
-        rc = check_launch("attention_sparse_q4 merge");
-    }
-    return rc;
+    return check_launch("attention_sparse_q4 values");
 }
 
 }  // namespace nyion
@@ -349,11 +476,10 @@ using namespace nyion;
 
 extern "C" {
 
-size_t nyion_attention_sparse_q4_workspace_size(int batch, int n_heads, int head_dim, int window,
-                                                int max_ctx) {
-    if (batch <= 0 || n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
-    const Sq4Sizes z = sq4_sizes(batch, n_heads, head_dim, window, max_ctx);
-    return z.scores + z.ml + z.part;
+size_t nyion_attention_sparse_q4_workspace_size(int batch, int n_heads, int n_kv_heads, int head_dim,
+                                                int window, int max_ctx) {
+    if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
+    return sq4_sizes(batch, n_heads, n_kv_heads, head_dim, window, max_ctx).total();
 }
 
 int nyion_attention_sparse_q4(const float* d_q, const void* k_pool, const void* v_pool,
@@ -391,13 +517,16 @@ int nyion_attention_sparse_q4(const float* d_q, const void* k_pool, const void* 
         return set_error(NYION_ERR_INVALID,
                          "attention_sparse_q4: max_ctx %d needs %d pages per sequence, the table has %d",
                          max_ctx, max_ctx > 0 ? zone_pos(max_ctx - 1).page + 1 : 0, max_pages_per_seq);
-    const Sq4Sizes z = sq4_sizes(batch, n_heads, head_dim, window, max_ctx);
-    if (!d_workspace || workspace_bytes < z.scores + z.ml + z.part)
+    const Sq4Sizes z = sq4_sizes(batch, n_heads, n_kv_heads, head_dim, window, max_ctx);
+    if ((long long)z.pieces * group * head_dim * 4 >= (1LL << 31))
+        return set_error(NYION_ERR_UNSUPPORTED, "attention_sparse_q4: window %d too long", window);
+    if (!d_workspace || workspace_bytes < z.total())
         return set_error(NYION_ERR_WORKSPACE,
                          "attention_sparse_q4: workspace of %zu bytes, %zu needed", workspace_bytes,
-                         z.scores + z.ml + z.part);
-    if (!aligned(d_workspace, 256) || !aligned(d_q, 4) || !aligned(d_out, 4))
-        return set_error(NYION_ERR_INVALID, "attention_sparse_q4: workspace must be 256-byte aligned");
+                         z.total());
+    if (!aligned(d_workspace, 256) || !aligned(d_q, 16) || !aligned(d_out, 16))
+        return set_error(NYION_ERR_INVALID,
+                         "attention_sparse_q4: q/out must be 16-byte and the workspace 256-byte aligned");
     Sq4Args a{};
     a.q = d_q;
     a.k = (const uint8_t*)k_pool;
@@ -409,6 +538,7 @@ int nyion_attention_sparse_q4(const float* d_q, const void* k_pool, const void* 
     a.scores = (float*)d_workspace;
     a.ml = (float2*)((char*)d_workspace + z.scores);
     a.part = z.part ? (float*)((char*)d_workspace + z.scores + z.ml) : nullptr;
+    a.counters = z.counters ? (int*)((char*)d_workspace + z.scores + z.ml + z.part) : nullptr;
     a.zone = zone;
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;

@@ -124,7 +124,7 @@ SIGNATURES = {
     "nyion_zone_kv_gather": (i32, [vp, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]),
     "nyion_zone_decode_attention": (i32, [vp, vp, vp, i64, vp, i32, i32, i32, vp, vp, i32, i32,
                                           i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]),
-    "nyion_attention_sparse_q4_workspace_size": (sz, [i32, i32, i32, i32, i32]),
+    "nyion_attention_sparse_q4_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "nyion_attention_sparse_q4": (i32, [vp, vp, vp, i64, vp, i32, i32, i32, vp, vp, i32, i32, i32,
                                         i32, i32, i32, i32, vp, vp, sz, vp]),
     "nyion_page_policy_create": (vp, [i32, i32, i32]),
@@ -631,9 +631,10 @@ def attention_sparse_q4(q, k_pool, v_pool, page_bases, n_layers, layer, ctx_lens
     B = q.shape[0]
     if max_ctx is None:
         max_ctx = int(ctx_lens.max().item())
-    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, head_dim, window, max_ctx)
+    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, n_kv_heads, head_dim, window,
+                                                           max_ctx)
     if workspace is None and need:
-        workspace = _torch().empty(need, dtype=_torch().uint8, device=q.device)
+        workspace = alloc_workspace(need, q.device)  # zero-filled: the arrival counters
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = load().nyion_attention_sparse_q4(
         ptr(q), ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_bases), page_bases.shape[1],
@@ -649,9 +650,10 @@ def prepare_attention_sparse_q4(q, k_pool, v_pool, page_bases, n_layers, layer, 
     """attention_sparse_q4 with every argument resolved once: a no-argument
     callable that only crosses the C ABI."""
     B = q.shape[0]
-    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, head_dim, window, max_ctx)
+    need = load().nyion_attention_sparse_q4_workspace_size(B, n_heads, n_kv_heads, head_dim, window,
+                                                           max_ctx)
     if workspace is None and need:
-        workspace = _torch().empty(need, dtype=_torch().uint8, device=q.device)
+        workspace = alloc_workspace(need, q.device)  # zero-filled: the arrival counters
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     fn = load().nyion_attention_sparse_q4
     args = (ptr(q), ptr(k_pool), ptr(v_pool), k_pool.numel(), ptr(page_bases),

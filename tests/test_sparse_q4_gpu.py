@@ -51,6 +51,9 @@ def expected(q, zp, layer, n, q_pos, window, stride):
     (64, 16, 2, 300, 0),      # no globals
     (128, 32, 1, 600, 37),    # 32 q heads on one kv head, D=128
     (128, 8, 8, 5000, 16),    # window longer than every context: all positions
+    (64, 40, 2, 700, 50),     # 20 q heads per kv head (two heads per thread, the second partial)
+    (128, 12, 2, 2000, 0),    # 6 q heads per kv head at D=128
+    (64, 12, 4, 3000, 9),     # 3 q heads per kv head (position ranges split five ways)
 ])
 def test_sparse_q4_across_4096(gpu, hd, hq, hkv, window, stride):
     ctx = [4100, 4500, 700, 1]
