@@ -728,6 +728,23 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
         nh.prefill_bf16(q, k, v, out, Hq, Hkv, D, k_pool=kp, v_pool=vp, block_table=tab,
                         block_tokens=bt)
 
+    # the same chunk written into Q4-20B pools (the quantising write is its own
+    # launch after the attention kernel)
+    rbq = 4 * D // 32 * 5
+    kq = torch.empty((nblk, Hkv, bt, rbq), dtype=torch.uint8, device="cuda")
+    vq = torch.empty_like(kq)
+
+    def attn_kv_q4(i):
+        nh.prefill_bf16(q, k, v, out, Hq, Hkv, D, k_pool=kq, v_pool=vq, block_table=tab,
+                        block_tokens=bt, kv_dtype=nh.KV_Q4_20B)
+
+    # the row-wise quantiser alone on the chunk's K rows as f32 (65536 rows of 128)
+    kf = k.float().contiguous()
+    kqf = torch.empty((n * Hkv, rbq), dtype=torch.uint8, device="cuda")
+
+    def quant(i):
+        nh.q4_quantize(kf, n * Hkv, D, kqf)
+
     reps = max(20, steps)
     settle(attn_kv, torch)
     ms_kv = timed(attn_kv, reps, max(2, warmup // 5), torch)
@@ -735,9 +752,16 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
     pct = event_pcts(attn, reps, torch)
     us_kv = event_mean(attn_kv, reps, torch) * 1e3
     pct_kv = event_pcts(attn_kv, reps, torch)
+    us_kv_q4 = event_mean(attn_kv_q4, reps, torch) * 1e3
+    us_quant = event_mean(quant, reps, torch) * 1e3
+    quant_bytes = n * Hkv * D * 4 + n * Hkv * rbq
     tf = flops / (us * 1e-6) / 1e12
     busy = _profile_value("prefill_c5_mfma_counters.txt", "mfma_busy_frac", "c5")
     return {"us_with_kv_write": us_kv, "us_with_kv_write_p10_p50_p90": _us3(pct_kv),
+            "us_with_kv_write_q4": us_kv_q4,
+            "tflops_with_kv_write_q4": flops / (us_kv_q4 * 1e-6) / 1e12,
+            "q4_quantize_65536x128": {"us": us_quant, "bytes": quant_bytes,
+                                      "gbs": quant_bytes / (us_quant * 1e-6) / 1e9},
             "us_with_kv_write_wall": ms_kv * 1e3,
             "tflops_with_kv_write": flops / (us_kv * 1e-6) / 1e12,
             "mfma_frac_with_kv_write": flops / (us_kv * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,

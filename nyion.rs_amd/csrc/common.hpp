@@ -72,6 +72,10 @@ int v_range_check(const uint16_t* v, long long n, hipStream_t stream);
 // device (looked up once per device; nullptr with the error set on failure).
 void* decode_scratch_ptr();
 
+// Fills the current device's exp_q16_16 table of mojo_softmax_padic (once per
+// device).
+int softmax_padic_setup();
+
 // Sets `bit` in the status word from one lane when any lane of the
 // wavefront has `bad` (vector atomic on global memory).
 __device__ __forceinline__ void report_range(unsigned* status, bool bad, unsigned bit) {

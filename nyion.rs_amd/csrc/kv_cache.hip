@@ -45,6 +45,53 @@ __device__ __forceinline__ void q4_quantize_group(const float* x, int len, uint3
     }
 }
 
+// Eight lanes quantise one 32-element group together (lanes 8j .. 8j+7 of a
+// wavefront, every lane active): lane k holds elements 4k .. 4k+3.  The
+// group's max |x| and min x are taken across the eight lanes with DPP (the
+// operations are exact, so the order does not matter), d and dmin are the
+// same f32 values q4_quantize_group computes, and each lane rounds its own
+// four elements.  Returns, in lanes k = 0..4 of the eight, word k of the
+// group's 20 bytes (the header, then the nibble words).
+template <int CTRL>
+__device__ __forceinline__ float q4_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, 0xf,
+                                                      0xf, false));
+}
+
+__device__ __forceinline__ uint32_t q4_quantize_group8(float4 x) {
+    // from 0 and FLT_MAX as the reference's fold (a NaN element is passed over)
+    float mx = fmaxf(fmaxf(fmaxf(0.0f, fabsf(x.x)), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    float mn = fminf(fminf(fminf(FLT_MAX, x.x), x.y), fminf(x.z, x.w));
+    mx = fmaxf(mx, q4_dpp<0xb1>(mx));   // quad_perm [1,0,3,2]
+    mn = fminf(mn, q4_dpp<0xb1>(mn));
+    mx = fmaxf(mx, q4_dpp<0x4e>(mx));   // quad_perm [2,3,0,1]
+    mn = fminf(mn, q4_dpp<0x4e>(mn));
+    mx = fmaxf(mx, q4_dpp<0x141>(mx));  // row_half_mirror: the eight lanes
+    mn = fminf(mn, q4_dpp<0x141>(mn));
+    const float d = (mx > 1e-10f) ? mx / 7.0f : 0.0f;
+    const float dmin = mn;
+    uint32_t bits = 0;  // this lane's four nibbles: bytes 2k and 2k+1 of the nibble area
+    if (d > 1e-10f) {
+        const float e[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float r = roundf((e[i] - dmin) / d);
+            r = fminf(fmaxf(r, 0.0f), 15.0f);
+            bits |= ((uint32_t)r) << (4 * i);
+        }
+    }
+    // nibble word j (1..4) = lanes 2j-2 (low half) and 2j-1 (high half)
+    const uint32_t other =
+        (uint32_t)__builtin_amdgcn_update_dpp((int)bits, (int)bits, 0xb1, 0xf, 0xf, false);
+    const uint32_t pair = bits | (other << 16);  // valid in even lanes
+    const int k = threadIdx.x & 7;
+    const int base = threadIdx.x & ~7;
+    // lane k (1..4) takes the pair word of lane 2k-2 of its group
+    const uint32_t nib = (uint32_t)__shfl((int)pair, base + 2 * (k > 0 ? k - 1 : 0));
+    const uint32_t hdr = f32_to_f16_bits(d) | (f32_to_f16_bits(dmin) << 16);
+    return k == 0 ? hdr : nib;
+}
+
 // ------------------------------------------------------------- kernels
 
 // One thread per (row, head, 4 values): f32 rows, or binary16 rows (F16).
@@ -87,7 +134,42 @@ int v_range_check(const uint16_t* v, long long n, hipStream_t stream) {
     return check_launch("prefill V range check");
 }
 
-// One thread per (row, head, group): quantise K and V groups.
+// Eight lanes per (row, head, group), 4 elements a lane (head_dim a multiple
+// of 32): the f32 or bf16 rows are read contiguously across the wavefront.
+// The grid-stride loop runs whole wavefronts (the DPP exchange needs every
+// lane), items past the end store nothing.
+__global__ __launch_bounds__(256) void kv_write_q4x8_kernel(WriteArgs a) {
+    const int groups = a.head_dim / 32;
+    const long long n = (long long)a.rows * a.n_kv_heads * groups * 8;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i0 = (long long)blockIdx.x * blockDim.x; i0 < n; i0 += stride) {
+        const long long i = i0 + threadIdx.x;
+        const bool ok = i < n;
+        const long long item = ok ? i >> 3 : 0;
+        const int k = (int)(i & 7);
+        const int g = (int)(item % groups);
+        const int h = (int)((item / groups) % a.n_kv_heads);
+        const int r = (int)(item / ((long long)groups * a.n_kv_heads));
+        const long long src = ((long long)r * a.n_kv_heads + h) * a.head_dim + 32 * g + 4 * k;
+        float4 kx, vx;
+        if (a.k16) {
+            kx = bf16x4_to_f32(*(const uint2*)(a.k16 + src));
+            vx = bf16x4_to_f32(*(const uint2*)(a.v16 + src));
+        } else {
+            kx = *(const float4*)(a.k + src);
+            vx = *(const float4*)(a.v + src);
+        }
+        const uint32_t wk = q4_quantize_group8(kx);
+        const uint32_t wv = q4_quantize_group8(vx);
+        const long long off = ok ? write_row_offset(a, r, h) : -1;
+        if (off >= 0 && k < 5) {
+            *(uint32_t*)((uint8_t*)a.k_pool + off + kQ4GroupBytes * g + 4 * k) = wk;
+            *(uint32_t*)((uint8_t*)a.v_pool + off + kQ4GroupBytes * g + 4 * k) = wv;
+        }
+    }
+}
+
+// One thread per (row, head, group): quantise K and V groups (any head_dim).
 __global__ void kv_write_q4_kernel(WriteArgs a) {
     const int groups = (a.head_dim + 31) / 32;
     const long long n = (long long)a.rows * a.n_kv_heads * groups;
@@ -304,7 +386,27 @@ __global__ void q4_dequant_kernel(const uint8_t* in, long long n_rows, int head_
     }
 }
 
-// Row-wise Q4-20B quantise: one thread per (row, group).
+// Row-wise Q4-20B quantise, eight lanes per group (head_dim a multiple of
+// 32, in 16-byte aligned): whole wavefronts per grid-stride step.
+__global__ __launch_bounds__(256) void q4_quantize_x8_kernel(const float* in, long long n_rows,
+                                                             int head_dim, uint8_t* out) {
+    const int groups = head_dim / 32;
+    const int rb = q4_row_bytes(head_dim);
+    const long long n = n_rows * groups * 8;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i0 = (long long)blockIdx.x * blockDim.x; i0 < n; i0 += stride) {
+        const long long i = i0 + threadIdx.x;
+        const bool ok = i < n;
+        const long long item = ok ? i >> 3 : 0;  // (row, group), in order
+        const float4 x = *(const float4*)(in + item * 32 + 4 * (i & 7));
+        const uint32_t w = q4_quantize_group8(x);
+        const long long r = item / groups;
+        const int g = (int)(item % groups);
+        if (ok && (i & 7) < 5) *(uint32_t*)(out + r * rb + kQ4GroupBytes * g + 4 * (i & 7)) = w;
+    }
+}
+
+// Row-wise Q4-20B quantise: one thread per (row, group) (any head_dim).
 __global__ void q4_quantize_kernel(const float* in, long long n_rows, int head_dim, uint8_t* out) {
     const int groups = (head_dim + 31) / 32;
     const int rb = q4_row_bytes(head_dim);
@@ -384,6 +486,10 @@ static int launch_write(const WriteArgs& a, int kv_dtype, hipStream_t stream) {
             hipLaunchKernelGGL(kv_write_flat_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
         else
             hipLaunchKernelGGL(kv_write_flat_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
+    } else if (a.head_dim % 32 == 0 && (a.k16 ? aligned(a.k16, 8) && aligned(a.v16, 8)
+                                                : aligned(a.k, 16) && aligned(a.v, 16))) {
+        const long long n = (long long)a.rows * a.n_kv_heads * (a.head_dim / 32) * 8;
+        hipLaunchKernelGGL(kv_write_q4x8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
     } else {
         const long long n = (long long)a.rows * a.n_kv_heads * ((a.head_dim + 31) / 32);
         hipLaunchKernelGGL(kv_write_q4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, a);
@@ -726,9 +832,15 @@ int nyion_q4_quantize(const float* in, int64_t n_rows, int head_dim, uint8_t* ou
     if (!in || !out || n_rows <= 0 || head_dim <= 0)
         return set_error(NYION_ERR_INVALID, "q4 quantize: arguments");
     if (!aligned(out, 4)) return set_error(NYION_ERR_INVALID, "q4 quantize: output not 4-byte aligned");
-    const long long n = (long long)n_rows * ((head_dim + 31) / 32);
-    hipLaunchKernelGGL(q4_quantize_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
-                       (hipStream_t)stream, in, (long long)n_rows, head_dim, out);
+    if (head_dim % 32 == 0 && aligned(in, 16)) {
+        const long long n = (long long)n_rows * (head_dim / 32) * 8;
+        hipLaunchKernelGGL(q4_quantize_x8_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                           (hipStream_t)stream, in, (long long)n_rows, head_dim, out);
+    } else {
+        const long long n = (long long)n_rows * ((head_dim + 31) / 32);
+        hipLaunchKernelGGL(q4_quantize_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                           (hipStream_t)stream, in, (long long)n_rows, head_dim, out);
+    }
     return check_launch("q4 quantize");
 }
 

@@ -176,7 +176,8 @@ int nyion_init(int device) {
     if ((rc = require_device()) != NYION_OK) return rc;
     // set-up of the device's scratch array (nyion_paged_decode_attention_noalloc)
     if (!decode_scratch_ptr()) return NYION_ERR_LAUNCH;
-    return NYION_OK;
+    // and of mojo_softmax_padic's exp table, so that later calls copy nothing
+    return softmax_padic_setup();
 }
 
 int nyion_sync(void) {

@@ -11,8 +11,10 @@
 //   p_i = (u32)(e_i * inv) >> 16   for i < 16*floor(n/16)   (vector lanes)
 //   p_i = (i32)((i64)e_i * inv >> 16) for the tail            (scalar lanes)
 //   probs_i = p_i / 65536
-// expf is evaluated as the f32 rounding of a double-precision exp, i.e. the
-// correctly rounded expf.
+// exp_q16_16 takes one of 655360 negative inputs, so its values are a table:
+// each device holds round(expf(x / 65536) * 65536) for x in [-655360, -1],
+// computed once by the host with the C library's expf (the function the
+// reference's f32::exp calls), which makes the whole pipeline integer-exact.
 //
 // StokesKVCacheSim (lib.rs:27-85): keys and values live in device memory,
 // one slot per resident token; the host keeps the logical order and the
@@ -33,6 +35,12 @@
 // stand-in: softmax_stage_ptr() looks its device address up once per device).
 constexpr int kSoftmaxStage = 1 << 20;
 static __device__ __align__(256) float softmax_stage[2 * kSoftmaxStage];
+
+// exp_q16_16 of x = -1 - i at index i (2.5 MiB per device; the name is a
+// host-side stand-in: exp_table_ptr() looks its address up and fills it once
+// per device).
+constexpr int kExpEntries = 655360;
+static __device__ __align__(256) int32_t exp_q16_table[kExpEntries];
 
 namespace nyion {
 
@@ -65,20 +73,54 @@ __device__ __forceinline__ int32_t sat_i32(float x) {
     return (int32_t)x;
 }
 
-__device__ __forceinline__ int32_t exp_q16_16(int32_t x) {
+// Host side of exp_q16_16 (swamp-kernels/src/lib.rs:102-108) for x in
+// [-655360, -1]: x as f32 / 65536 (exact), expf, times 65536 (exact),
+// rounded half away from zero (f32::round), max 0, as i32.
+static int32_t exp_q16_16_host(int32_t x) {
+    const float e = expf((float)x / 65536.0f);
+    const float r = fmaxf(roundf(e * 65536.0f), 0.0f);
+    return (int32_t)r;
+}
+
+// Device address of this device's exp table, filled by the first caller on
+// the device (synchronous copy); nullptr with the error set on failure.
+static const int32_t* exp_table_ptr() {
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    static std::mutex locks[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    uintptr_t v = cache[dev].load(std::memory_order_acquire);
+    if (v) return (const int32_t*)v;
+    std::lock_guard<std::mutex> g(locks[dev]);
+    v = cache[dev].load(std::memory_order_acquire);
+    if (v) return (const int32_t*)v;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(exp_q16_table));
+    if (e == hipSuccess && ptr) {
+        std::vector<int32_t> t(kExpEntries);
+        for (int i = 0; i < kExpEntries; i++) t[i] = exp_q16_16_host(-1 - i);
+        e = hipMemcpy(ptr, t.data(), sizeof(int32_t) * kExpEntries, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        set_error(NYION_ERR_LAUNCH, "softmax_padic: exp table set-up failed: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    cache[dev].store((uintptr_t)ptr, std::memory_order_release);
+    return (const int32_t*)ptr;
+}
+
+__device__ __forceinline__ int32_t exp_q16_16(const int32_t* table, int32_t x) {
     if (x < -655360) return 0;
     if (x >= 0) return 65536;
-    const float xr = (float)x / 65536.0f;
-    const float ex = (float)exp((double)xr);
-    float r = roundf(ex * 65536.0f);
-    r = fmaxf(r, 0.0f);
-    return sat_i32(r);
+    return table[-1 - x];
 }
 
 // One workgroup of 1024 threads; e_i is kept in `probs` (as bits) between
 // the passes.
 __global__ __launch_bounds__(1024) void softmax_padic_kernel(const float* logits, float* probs,
-                                                             int n, float inv_tmp) {
+                                                             int n, float inv_tmp,
+                                                             const int32_t* exp_table) {
     __shared__ int32_t smax[16];
     __shared__ long long ssum[16];
     const int tid = threadIdx.x;
@@ -95,7 +137,7 @@ __global__ __launch_bounds__(1024) void softmax_padic_kernel(const float* logits
     long long sum = 0;
     for (int i = tid; i < n; i += 1024) {
         const int32_t f = sat_i32((logits[i] * inv_tmp) * 65536.0f);
-        const int32_t e = exp_q16_16((int32_t)((uint32_t)f - (uint32_t)mx));
+        const int32_t e = exp_q16_16(exp_table, (int32_t)((uint32_t)f - (uint32_t)mx));
         ((int32_t*)probs)[i] = e;
         sum += e;
     }
@@ -142,6 +184,11 @@ __global__ void stokes_gather_kernel(const float* src, const int* slots, int cou
 
 }  // namespace nyion
 
+namespace nyion {
+// Set-up of the current device's exp table (called by nyion_init).
+int softmax_padic_setup() { return exp_table_ptr() ? NYION_OK : NYION_ERR_LAUNCH; }
+}  // namespace nyion
+
 using namespace nyion;
 
 extern "C" {
@@ -153,9 +200,11 @@ int nyion_softmax_padic_dev(const float* d_logits, float* d_probs, int n, float 
     if ((rc = require_device()) != NYION_OK) return rc;
     if (!d_logits || !d_probs || n <= 0)
         return set_error(NYION_ERR_INVALID, "softmax_padic: null pointer or n <= 0");
+    const int32_t* table = exp_table_ptr();
+    if (!table) return NYION_ERR_LAUNCH;
     const float inv_tmp = 1.0f / fmaxf(temperature, 1e-6f);
     hipLaunchKernelGGL(softmax_padic_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, d_logits,
-                       d_probs, n, inv_tmp);
+                       d_probs, n, inv_tmp, table);
     return check_launch("softmax_padic");
 }
 

@@ -41,6 +41,24 @@ def test_q4_quantize_bit_exact(gpu):
     assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: {got[bad[0]]} vs {ref[bad[0]]}"
 
 
+@pytest.mark.parametrize("hd,shift", [(128, 0), (96, 0), (64, 1), (80, 0)])
+def test_q4_quantize_paths(gpu, hd, shift):
+    """The eight-lane quantiser (head_dim a multiple of 32, 16-byte aligned
+    rows) and the per-group one (a partial group, or rows one float off the
+    16-byte boundary) write the same bytes as the oracle."""
+    rng = np.random.default_rng(hd + shift)
+    x = (rng.standard_normal((3001, hd)) * rng.choice([1e-3, 1.0, 50.0], size=(3001, 1))).astype(np.float32)
+    x[7, :] = 0.0
+    x[8, 3] = np.nan
+    ref = oracle.q4_quantize_rows(x)
+    buf = torch.zeros(x.size + 4, dtype=torch.float32, device="cuda")
+    buf[shift:shift + x.size] = torch.from_numpy(x.reshape(-1)).cuda()
+    out = torch.zeros(ref.shape, dtype=torch.uint8, device="cuda")
+    gpu.q4_quantize(buf[shift:], x.shape[0], hd, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
 def test_q4_dequant_bit_exact(gpu):
     rng = np.random.default_rng(1)
     x = edge_rows(rng)
