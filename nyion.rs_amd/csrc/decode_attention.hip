@@ -316,6 +316,7 @@ __device__ __forceinline__ void decode_v(const Tile<D, KVT>& t, int r, float* vv
 template <int D>
 struct State {
     floatx4 acc[D / 16];
+    floatx4 acc_m;  // Q4-20B: sum of p * dmin/32 (the same for every dim of a lane's column)
     float m;
     float l;
 };
@@ -359,31 +360,45 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         // KV; qv[NC + g] = sum of head j's q over group g), one accumulator
         // per group, then each row's d and dmin (headers of rows 4kq+r, from
         // the lanes that loaded them).
+        // The headers go through a per-wavefront LDS slot, [group][row], so
+        // that each lane reads those of its four rows 4kq .. 4kq+3 with one
+        // 16-byte read per group.
+        __shared__ __attribute__((aligned(16))) uint32_t sm_khdr[4][D / 32][16];
+        uint32_t(*hs)[16] = sm_khdr[threadIdx.x >> 6];
+        if (kq < D / 32) hs[kq][threadIdx.x & 15] = t.khdr;
         floatx4 sg[D / 32];
 #pragma unroll
         for (int g = 0; g < D / 32; g++) sg[g] = floatx4{0.f, 0.f, 0.f, 0.f};
         const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
         for (int x = 0; x < D / 16; x++) {
-            // nibbles e0..e3 of dims 16x + 4kq .. +3 as binary16 1024 + e, less 1024
+            // nibbles e0..e3 of dims 16x + 4kq .. +3 as binary16 1024 + e, less
+            // 1024: bytes [e0 e2 64 64] and [e1 e3 64 64], then one byte
+            // permute per pair of values
             const uint32_t w = t.kn[x];
-            const uint32_t p01 = (w & 0xfu) | ((w & 0xf0u) << 12);
-            const uint32_t p23 = ((w >> 8) & 0xfu) | ((w & 0xf000u) << 4);
-            const halfx2 h01 = __builtin_bit_cast(halfx2, p01 | 0x64006400u) - k1024;
-            const halfx2 h23 = __builtin_bit_cast(halfx2, p23 | 0x64006400u) - k1024;
+            const uint32_t lo = (w & 0x0f0fu) | 0x64640000u;
+            const uint32_t hi = ((w >> 4) & 0x0f0fu) | 0x64640000u;
+            const halfx2 h01 = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(hi, lo, 0x06040200u)) - k1024;
+            const halfx2 h23 = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(hi, lo, 0x07050301u)) - k1024;
             const halfx4 kx = {h01[0], h01[1], h23[0], h23[1]};
             const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
             const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
             sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, sg[x >> 1], 0, 0, 0);
             sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, sg[x >> 1], 0, 0, 0);
         }
+        uint32_t hr[D / 32][4];
+#pragma unroll
+        for (int g = 0; g < D / 32; g++) {
+            const u32x4 h4 = *(const u32x4*)&hs[g][4 * kq];
+#pragma unroll
+            for (int r = 0; r < 4; r++) hr[g][r] = h4[r];
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             float acc = 0.f;
 #pragma unroll
             for (int g = 0; g < D / 32; g++) {
-                const uint32_t h = __shfl(t.khdr, 16 * g + 4 * kq + r);
-                const float d = f16_bits_to_f32(h), dmin = f16_bits_to_f32(h >> 16);
+                const float d = f16_bits_to_f32(hr[g][r]), dmin = f16_bits_to_f32(hr[g][r] >> 16);
                 acc = __builtin_fmaf(d, sg[g][r], __builtin_fmaf(dmin, qv[NC + g], acc));
             }
             s[r] = acc;
@@ -426,6 +441,7 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             const float ar = __shfl(alpha, 4 * kq + r);
 #pragma unroll
             for (int x = 0; x < DPL; x++) st.acc[x][r] *= ar;
+            if constexpr (KVT == NYION_KV_Q4_20B) st.acc_m[r] *= ar;
         }
     }
     float pr[4];
@@ -463,27 +479,66 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         // which is exact and keeps d*15 + dmin <= 2^20 inside binary16 range)
         const halfx4 pa = {(_Float16)(32.f * pr[0]), (_Float16)(32.f * pr[1]), (_Float16)(32.f * pr[2]),
                            (_Float16)(32.f * pr[3])};
-        float dv[4], mv[4];
-        bool ok[4];
+        // v/32 = (d/32) nib + dmin/32 as three exact binary16 terms: hi =
+        // (d/32) nib rounded, lo = fma(d/32, nib, -hi) (exact: the product has
+        // at most 15 significant bits), and dmin/32, whose product with P is
+        // the same for every element of the lane's column and is accumulated
+        // once per tile (acc_m).  d/32 and dmin/32 are exact for |d|, |dmin|
+        // >= 2^-9 (below, the scaled header rounds by at most 2^-25), and
+        // d/32 * 15 stays inside binary16 range.  Pairs of rows (0, 1) and
+        // (2, 3) share one packed operation.
+        const halfx2 s32 = {(_Float16)0.03125f, (_Float16)0.03125f};
+        uint32_t d01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x05040100u);
+        uint32_t d23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x05040100u);
+        uint32_t m01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x07060302u);
+        uint32_t m23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x07060302u);
+        if (MASKED) {  // masked rows may hold uninitialised slots: their terms are 0
+            const uint32_t q = (mask >> (4 * kq)) & 0xfu;
+            const uint32_t k01 = ((q & 1u) ? 0xffffu : 0u) | ((q & 2u) ? 0xffff0000u : 0u);
+            const uint32_t k23 = ((q & 4u) ? 0xffffu : 0u) | ((q & 8u) ? 0xffff0000u : 0u);
+            d01 &= k01;
+            m01 &= k01;
+            d23 &= k23;
+            m23 &= k23;
+        }
+        const halfx2 dd01 = __builtin_bit_cast(halfx2, d01) * s32, dd23 = __builtin_bit_cast(halfx2, d23) * s32;
+        const halfx2 mm01 = __builtin_bit_cast(halfx2, m01) * s32, mm23 = __builtin_bit_cast(halfx2, m23) * s32;
+        st.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{mm01[0], mm01[1], mm23[0], mm23[1]},
+                                                         st.acc_m, 0, 0, 0);
+        // each row's nibbles split into even and odd elements, one per byte,
+        // with 0x64 in the spare bytes (binary16 1024 + e after a permute)
+        const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        uint32_t ev[4][2], od[4][2];  // [row][word]: one word at head_dim 64, two at 128
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            dv[r] = f16_bits_to_f32(t.vhdr[r]) * 0.03125f;
-            mv[r] = f16_bits_to_f32(t.vhdr[r] >> 16) * 0.03125f;
-            ok[r] = !MASKED || ((mask >> (4 * kq + r)) & 1u);
+            if constexpr (DPL == 4) {
+                ev[r][0] = (t.v[r] & 0x0f0fu) | 0x64640000u;
+                od[r][0] = ((t.v[r] >> 4) & 0x0f0fu) | 0x64640000u;
+            } else {  // eight nibbles: two words each
+                const uint32_t e = t.v[r] & 0x0f0f0f0fu, o = (t.v[r] >> 4) & 0x0f0f0f0fu;
+                ev[r][0] = (e & 0xffffu) | 0x64640000u;
+                ev[r][1] = (e >> 16) | 0x64640000u;
+                od[r][0] = (o & 0xffffu) | 0x64640000u;
+                od[r][1] = (o >> 16) | 0x64640000u;
+            }
         }
 #pragma unroll
         for (int z = 0; z < DPL; z++) {  // element z: nibble z of the lane's word
-            halfx4 vh, vl;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                // masked rows may hold uninitialised slots: keep NaN out
-                const float v = ok[r] ? q4_dequant(dv[r], mv[r], (t.v[r] >> (4 * z)) & 0xfu) : 0.f;
-                vh[r] = (_Float16)v;
-                vl[r] = (_Float16)(v - (float)vh[r]);
-            }
-            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vh, st.acc[z], 0, 0, 0);
-            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vl, st.acc[z], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            const int wz = (z >> 1) >> 1, bz = (z >> 1) & 1;  // word and byte of the element
+            const uint32_t sel = bz ? 0x07050301u : 0x06040200u;
+            const uint32_t n01 = (z & 1) ? __builtin_amdgcn_perm(od[1][wz], od[0][wz], sel)
+                                         : __builtin_amdgcn_perm(ev[1][wz], ev[0][wz], sel);
+            const uint32_t n23 = (z & 1) ? __builtin_amdgcn_perm(od[3][wz], od[2][wz], sel)
+                                         : __builtin_amdgcn_perm(ev[3][wz], ev[2][wz], sel);
+            const halfx2 e01 = __builtin_bit_cast(halfx2, n01) - k1024;
+            const halfx2 e23 = __builtin_bit_cast(halfx2, n23) - k1024;
+            const halfx2 h01 = dd01 * e01, h23 = dd23 * e23;
+            const halfx2 l01 = __builtin_elementwise_fma(dd01, e01, -h01);
+            const halfx2 l23 = __builtin_elementwise_fma(dd23, e23, -h23);
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{h01[0], h01[1], h23[0], h23[1]},
+                                                              st.acc[z], 0, 0, 0);
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{l01[0], l01[1], l23[0], l23[1]},
+                                                              st.acc[z], 0, 0, 0);
         }
     } else {
 #pragma unroll
@@ -1139,6 +1194,7 @@ void decode_kernel(DecodeArgs a) {
         State<D> st;
 #pragma unroll
         for (int x = 0; x < DPL; x++) st.acc[x] = floatx4{0.f, 0.f, 0.f, 0.f};
+        st.acc_m = floatx4{0.f, 0.f, 0.f, 0.f};
         st.m = -INFINITY;
         st.l = 0.f;
 
@@ -1188,6 +1244,11 @@ void decode_kernel(DecodeArgs a) {
                                           return gather_offsets<D, KVT>(a, e, m, b, kvh, 16 * (wa + i),
                                                                         e.L, false, j, kq, ko, vo, pos);
                                       });
+        }
+
+        if constexpr (KVT == NYION_KV_Q4_20B) {  // the dmin/32 term belongs to every dim
+#pragma unroll
+            for (int x = 0; x < DPL; x++) st.acc[x] += st.acc_m;
         }
 
         // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
