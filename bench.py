@@ -902,12 +902,11 @@ def bench_c1(nh, torch, steps, warmup):
 
 
 def bench_abi(nh, torch, steps, warmup):
-    """The project-ABI entry without scratch (gpu_attention_device,
+    """The project-ABI entry with no scratch argument (gpu_attention_device,
     fused_attention.cu:194-213: the reference allocates an n_heads*seq_len
-    scores buffer per call; this library allocates nothing and, given no
-    buffer, runs one workgroup per (kv head, head group)) against
-    nyion_attention_node given that scores buffer (ScratchBuffers::d_scores,
-    swamp-gpu/src/lib.rs:290-331).  Contiguous f32 KV [Hkv][4096][64], 32/4
+    scores buffer per call; this library keeps one split-K buffer per
+    stream, allocated by the first call) against nyion_attention_node given
+    that scores buffer (ScratchBuffers::d_scores, swamp-gpu/src/lib.rs:290-331).  Contiguous f32 KV [Hkv][4096][64], 32/4
     heads, 40 rotated caches (336 MB, beyond the 256 MB Infinity Cache)."""
     Hq, Hkv, D, ctx, R = 32, 4, 64, 4096, 40
     g = torch.Generator(device="cuda").manual_seed(0)

@@ -119,8 +119,14 @@ size_t nyion_attention_node_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads,
 /* Project ABI names of the unlinked CUDA file, same arguments (f32 KV,
  * [n_kv_heads][kv_stride][head_dim]): gpu_attention_device
  * (swamp-gpu/kernels/fused_attention.cu:194-204) and gpu_attention_streamed
- * (fused_attention.cu:483-494).  Return 0 / -1 as those did; unlike them,
- * they allocate nothing per call. */
+ * (fused_attention.cu:483-494).  Return 0 / -1 as those did.  The CUDA
+ * originals allocated an n_heads*seq_len scores buffer per call; here the
+ * node's split-K scratch is a device buffer per (device, stream), allocated
+ * by the first call on that stream that needs more than it holds and kept
+ * until the process ends (so the first call on a stream may not be inside
+ * a graph capture).  Calls on one stream are ordered by it; calls on
+ * different streams use different buffers and may overlap.  A buffer that
+ * must grow is replaced after the stream's queued work has finished. */
 int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* d_v_cache,
                          float* d_output, int n_heads, int n_kv_heads, int seq_len,
                          int head_dim, int kv_stride);
@@ -148,7 +154,8 @@ void gpu_graph_destroy(void* graph_handle);
  * (fused_attention.cu:534-545) and gpu_graph_create_attention_half
  * (fused_attention.cu:672-717).  K/V values are used as stored (binary16
  * products, f32 accumulation; q and the softmax weights as in the pool
- * layout note above). */
+ * layout note above).  gpu_attention_streamed_half takes its split-K
+ * scratch as gpu_attention_streamed does. */
 int gpu_attention_streamed_half(const float* d_q, const uint16_t* d_k_cache,
                                 const uint16_t* d_v_cache, float* d_output, int n_heads,
                                 int n_kv_heads, int seq_len, int head_dim, int kv_stride,

@@ -51,6 +51,9 @@
 #include <math.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "common.hpp"
 
@@ -2118,6 +2121,60 @@ int nyion_attention_node(const float* d_q, const void* d_k, const void* d_v, flo
     return launch_plan(pl, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+// Split-K scratch of the project-ABI names, which take no scratch argument
+// (the CUDA originals cudaMalloc'ed a scores buffer per call): one device
+// buffer per (device, stream), allocated by the first call on that stream
+// that needs more than the stream's buffer holds and kept until the process
+// ends.  Calls on one stream are ordered by the stream; calls on different
+// streams use different buffers.  A buffer that has to grow is replaced
+// after its stream's queued work is done.
+static float* legacy_scratch(hipStream_t stream, size_t bytes) {
+    static std::mutex mu;
+    static std::map<std::pair<int, uintptr_t>, std::pair<float*, size_t>> bufs;
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    std::lock_guard<std::mutex> g(mu);
+    auto& e = bufs[{dev, (uintptr_t)stream}];
+    if (e.first && e.second >= bytes) return e.first;
+    size_t want = (size_t)1 << 20;
+    while (want < bytes) want <<= 1;
+    if (e.first) {
+        if (hipStreamSynchronize(stream) != hipSuccess || hipFree(e.first) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(NYION_ERR_LAUNCH, "attention scratch: releasing the stream's buffer failed");
+            e = {nullptr, 0};
+            return nullptr;
+        }
+        e = {nullptr, 0};
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(NYION_ERR_OOM, "attention scratch: hipMalloc of %zu bytes failed", want);
+        return nullptr;
+    }
+    e = {(float*)p, want};
+    return (float*)p;
+}
+
+// The node with the stream's scratch standing in for d_scores.
+static int legacy_node(const float* d_q, const void* d_k, const void* d_v, float* d_out, int n_heads,
+                       int n_kv_heads, int seq_len, int head_dim, int kv_stride, int kv_dtype,
+                       hipStream_t stream) {
+    clear_error();
+    if (require_device() != NYION_OK) return -1;
+    float* scratch = legacy_scratch(stream, (size_t)n_heads * seq_len * sizeof(float));
+    if (!scratch) return -1;
+    const int rc = nyion_attention_node(d_q, d_k, d_v, scratch, d_out, (uint32_t)n_heads,
+                                        (uint32_t)n_kv_heads, (uint32_t)seq_len, (uint32_t)head_dim,
+                                        (uint32_t)kv_stride, kv_dtype, stream);
+    return rc == NYION_OK ? 0 : -1;
+}
+
+extern "C" {
+
 int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float* d_v_cache,
                            float* d_output, int n_heads, int n_kv_heads, int seq_len, int head_dim,
                            int kv_stride, nyion_stream_t stream) {
@@ -2125,10 +2182,8 @@ int gpu_attention_streamed(const float* d_q, const float* d_k_cache, const float
         set_error(NYION_ERR_INVALID, "gpu_attention_streamed: non-positive size");
         return -1;
     }
-    const int rc = nyion_attention_node(d_q, d_k_cache, d_v_cache, nullptr, d_output,
-                                        (uint32_t)n_heads, (uint32_t)n_kv_heads, (uint32_t)seq_len,
-                                        (uint32_t)head_dim, (uint32_t)kv_stride, NYION_KV_F32, stream);
-    return rc == NYION_OK ? 0 : -1;
+    return legacy_node(d_q, d_k_cache, d_v_cache, d_output, n_heads, n_kv_heads, seq_len, head_dim,
+                       kv_stride, NYION_KV_F32, (hipStream_t)stream);
 }
 
 int gpu_attention_device(const float* d_q, const float* d_k_cache, const float* d_v_cache,
@@ -2213,10 +2268,8 @@ int gpu_attention_streamed_half(const float* d_q, const uint16_t* d_k_cache,
         set_error(NYION_ERR_INVALID, "gpu_attention_streamed_half: non-positive size");
         return -1;
     }
-    const int rc = nyion_attention_node(d_q, d_k_cache, d_v_cache, nullptr, d_output,
-                                        (uint32_t)n_heads, (uint32_t)n_kv_heads, (uint32_t)seq_len,
-                                        (uint32_t)head_dim, (uint32_t)kv_stride, NYION_KV_F16, stream);
-    return rc == NYION_OK ? 0 : -1;
+    return legacy_node(d_q, d_k_cache, d_v_cache, d_output, n_heads, n_kv_heads, seq_len, head_dim,
+                       kv_stride, NYION_KV_F16, (hipStream_t)stream);
 }
 
 int gpu_graph_replay_attention(void* graph_handle, nyion_stream_t stream) {

@@ -4,6 +4,8 @@ Tolerance: max-abs-err <= 2e-3 and rel-err <= 1e-3, where rel-err
 is max|gpu - ref| / max|ref| over the compared tensor (fp32 accumulation on
 both sides).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -123,6 +125,44 @@ def test_attention_node_stride_and_project_names(gpu):
     gpu.attention_node(dq, dk, dv, out, 32, 4, S, 64, stride, scores=scores)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), ref, "node stride")
+
+
+def test_project_names_streams_and_growth(gpu):
+    """gpu_attention_streamed on two streams at once (each stream has its own
+    split-K buffer), then a longer context on one of them (its buffer is
+    replaced after the stream's queued work), and gpu_attention_device: each
+    output equals the node's with a caller scores buffer bit for bit, and
+    the oracle at tolerance."""
+    L = gpu.load()
+    rng = np.random.default_rng(23)
+    cases = []
+    for S in (3000, 4096, 20000):
+        q = rng.standard_normal((32, 64), dtype=np.float32)
+        k = rng.standard_normal((4, S, 64), dtype=np.float32)
+        v = rng.standard_normal((4, S, 64), dtype=np.float32)
+        cases.append((S, q, k, v, to_dev(q), to_dev(k), to_dev(v)))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.full((32, 64), float("nan"), device="cuda") for _ in range(4)]
+    torch.cuda.synchronize()
+    for i, (st, (S, _, _, _, dq, dk, dv)) in enumerate(((s1, cases[0]), (s2, cases[1]), (s1, cases[2]))):
+        for _ in range(3):
+            assert L.gpu_attention_streamed(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                            outs[i].data_ptr(), 32, 4, S, 64, S,
+                                            C.c_void_p(st.cuda_stream)) == 0
+    S, q, k, v, dq, dk, dv = cases[1]
+    assert L.gpu_attention_device(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), outs[3].data_ptr(),
+                                  32, 4, S, 64, S) == 0
+    torch.cuda.synchronize()
+    for i, ci in enumerate((0, 1, 2, 1)):
+        S, q, k, v, dq, dk, dv = cases[ci]
+        node = torch.full((32, 64), float("nan"), device="cuda")
+        scores = torch.empty(32 * S, dtype=torch.float32, device="cuda")
+        gpu.attention_node(dq, dk, dv, node, 32, 4, S, 64, S, scores=scores)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[i], node), f"case {i}"
+        ref = oracle.attention(q.reshape(-1), oracle.contiguous_layout(k, v, S, 64), S, S - 1, 32, 4,
+                               64).reshape(32, 64)
+        assert_close(outs[i].cpu().numpy(), ref, f"project name case {i}")
 
 
 # ---------------------------------------------------------------- paged full causal
