@@ -61,6 +61,19 @@ ALL = ("c1", "c2", "c2t", "c3", "c3h", "c3q", "c4", "a5", "c5", "abi", "zone", "
        "pool")
 
 
+# The GPU run's own input bytes (copied from HBM after the timed calls) and
+# its outputs, per workload: the CPU baselines time the oracle on exactly
+# these bytes and report how far the GPU's outputs are from the oracle's.
+SAMPLES = {}
+
+
+def _err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    e = float(np.max(np.abs(got - ref)))
+    return {"max_abs_err_vs_gpu": e, "rel_err_vs_gpu": e / max(float(np.max(np.abs(ref))), 1e-30)}
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -260,6 +273,18 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False, q4=False):
     def call(i):
         call1()
 
+    if not f16 and not q4:
+        # sequences 0 and 1 as [Hkv][L][D] rows, their q and this call's output
+        call1()
+        torch.cuda.synchronize()
+        smp = {"lens": [int(x) for x in lens[:2]], "q": q[:2].cpu().numpy(),
+               "out": out[:2].cpu().numpy(), "k": [], "v": []}
+        for b in range(2):
+            t = torch.arange(int(lens[b]), device="cuda")
+            blk = tab[b].long()[t // bt]
+            smp["k"].append(kp[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy())
+            smp["v"].append(vp[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy())
+        SAMPLES["c3"] = smp
     toks = int(lens.sum())
     row_bytes = 40 if q4 else D * (2 if f16 else 4)
     nbytes = 2 * toks * Hkv * row_bytes + int(nblk.sum()) * 4 + 2 * 64 * Hq * D * 4
@@ -276,34 +301,49 @@ def bench_c3(nh, torch, steps, warmup, seed=0, f16=False, q4=False):
             "partition_tokens": nh.partition_tokens(64, Hkv, D, maxc)}
 
 
-def cpu_baseline_c3(seed=0, n_sample=2, budget_s=5.0):
-    """Oracle on the first n_sample sequences of the 64-sequence batch (same
-    context lengths), scaled by attended tokens to the batch; at all host
-    cores and at 6 threads."""
+def cpu_baseline_c3(seed=0, n_sample=2, budget_s=5.0, sample=None):
+    """Oracle on the first n_sample sequences of the 64-sequence batch,
+    scaled by attended tokens to the batch; at all host cores and at 6
+    threads.  With `sample` (the GPU run's own rows of those sequences) the
+    oracle runs on those bytes and its outputs are compared with the GPU's."""
     import oracle
     import workloads as W
 
     lens = W.c3_lengths(seed=seed)
-    pb = W.paged_batch([int(x) for x in lens[:n_sample]], seed=seed)
+    if sample is not None:
+        q = sample["q"]
+        lays = [oracle.contiguous_layout(sample["k"][b], sample["v"][b], int(lens[b]), 64)
+                for b in range(n_sample)]
+        origin = "the GPU run's own q and K/V rows of those sequences, copied from HBM"
+    else:
+        pb = W.paged_batch([int(x) for x in lens[:n_sample]], seed=seed)
+        q = pb.q
+        lays = [pb.layout(b) for b in range(n_sample)]
+        origin = "a seeded draw of the same shapes"
     toks_sample, toks_all = int(lens[:n_sample].sum()), int(lens.sum())
     nbytes = 2 * toks_all * 4 * 64 * 4 + int(((lens + 15) // 16).sum()) * 4 + 2 * 64 * 32 * 64 * 4
     res = {}
     for label, thr in (("all", _cores()), ("6", 6)):
         def run():
-            for b in range(n_sample):
-                oracle.attention(pb.q[b], pb.layout(b), int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
-                                 threads=thr)
+            return [oracle.attention(q[b], lays[b], int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
+                                     threads=thr) for b in range(n_sample)]
         dt, n = _cpu_time(run, budget_s=budget_s)
         res[label] = (thr, n, dt, dt * toks_all / toks_sample)
     thr, n, dt, est = res["all"]
     thr6, n6, dt6, est6 = res["6"]
-    return {"value": round(nbytes / est / 1e9, 3), "unit": "GB/s", "cores": thr, "kind": "port",
-            "sample": (f"{n} runs over sequences 0-{n_sample - 1} of the batch ({toks_sample} tokens, "
-                       f"{dt * 1e3:.1f} ms per run at {thr} threads), scaled by attended tokens to "
-                       f"the batch's {toks_all}: {est * 1e3:.1f} ms per call; at 6 threads "
-                       f"{est6 * 1e3:.1f} ms ({nbytes / est6 / 1e9:.2f} GB/s)"),
-            "us_per_layer": est * 1e6, "us_per_layer_6_threads": est6 * 1e6,
-            "cpu_model": _cpu_model()}
+    out = {"value": round(nbytes / est / 1e9, 3), "unit": "GB/s", "cores": thr, "kind": "port",
+           "sample": (f"{n} runs over sequences 0-{n_sample - 1} of the batch ({toks_sample} tokens, "
+                      f"{dt * 1e3:.1f} ms per run at {thr} threads; inputs: {origin}), scaled by "
+                      f"attended tokens to the batch's {toks_all}: {est * 1e3:.1f} ms per call; at "
+                      f"6 threads {est6 * 1e3:.1f} ms ({nbytes / est6 / 1e9:.2f} GB/s)"),
+           "us_per_layer": est * 1e6, "us_per_layer_6_threads": est6 * 1e6,
+           "cpu_model": _cpu_model()}
+    if sample is not None:
+        ref = np.stack([o.reshape(32, 64) for o in
+                        [oracle.attention(q[b], lays[b], int(lens[b]), int(lens[b]) - 1, 32, 4, 64,
+                                          threads=thr) for b in range(n_sample)]])
+        out.update(_err(sample["out"], ref))
+    return out
 
 
 # ----------------------------------------------------------------------------
@@ -345,6 +385,15 @@ def bench_c2(nh, torch, steps, warmup, seed=0):
     settle(step, torch)
     ms = timed(step, steps, warmup, torch)
     pct_step = event_pcts(step, max(steps, 20), torch)
+    # layer 0 of the first copy: its rows in position order, q and output
+    calls[0][0]()
+    torch.cuda.synchronize()
+    q0, kp0, vp0, tab0 = layers[0][0]
+    t = torch.arange(ctx, device="cuda")
+    blk = tab0[0].long()[t // bt]
+    SAMPLES["c2"] = {"q": q0[0].cpu().numpy(), "out": outs[0][0].cpu().numpy(),
+                     "k": kp0[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy(),
+                     "v": vp0[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy()}
     reps = max(steps, 20) * L
     one = lambda i: calls[i % R][i % L]()  # noqa: E731
     us_call = event_mean(one, reps, torch) * 1e3
@@ -434,25 +483,38 @@ def bench_c2_tracked(nh, torch, steps, seed=0):
             "score_and_importance_bytes_per_layer": Hq * (ctx + 2) * 4 * 2 + (ctx + 2) * 8 * 2}
 
 
-def cpu_baseline_c2(seed=0):
-    """Oracle (C restatement of ops::attention) on one C2 layer at a time."""
+def cpu_baseline_c2(seed=0, sample=None):
+    """Oracle (C restatement of ops::attention) on one C2 layer at a time;
+    with `sample`, on the GPU run's own layer-0 bytes, its outputs compared
+    with the GPU's."""
     import oracle
     import workloads as W
 
-    pb = W.paged_batch([4096], seed=seed)
-    lay = pb.layout(0)
+    if sample is not None:
+        q = sample["q"]
+        lay = oracle.contiguous_layout(sample["k"], sample["v"], 4096, 64)
+        origin = "the GPU run's own layer-0 q and K/V rows, copied from HBM"
+    else:
+        pb = W.paged_batch([4096], seed=seed)
+        q, lay = pb.q[0], pb.layout(0)
+        origin = "a seeded draw of the same shapes"
     bytes_layer = 2 * 4096 * 4 * 64 * 4 + 256 * 4 + 2 * 32 * 64 * 4
     res = {}
     for label, thr in (("6", 6), ("all", _cores())):
-        dt, n = _cpu_time(lambda: oracle.attention(pb.q[0], lay, 4096, 4095, 32, 4, 64, threads=thr),
+        dt, n = _cpu_time(lambda: oracle.attention(q, lay, 4096, 4095, 32, 4, 64, threads=thr),
                           budget_s=3.0)
         res[label] = (thr, n, dt * 1e6)
     thr6, n6, us6 = res["6"]
     thra, na, usa = res["all"]
-    return {"value": bytes_layer / (usa * 1e-6) / 1e9, "unit": "GB/s", "cores": thra, "kind": "port",
-            "sample": (f"{na} single-layer decode calls (ctx 4096, 32/4 heads, D=64, paged f32) "
-                       f"at {thra} threads: {usa:.0f} us/layer; at 6 threads {us6:.0f} us/layer"),
-            "us_per_layer": usa, "us_per_layer_6_threads": us6}
+    out = {"value": bytes_layer / (usa * 1e-6) / 1e9, "unit": "GB/s", "cores": thra, "kind": "port",
+           "sample": (f"{na} single-layer decode calls (ctx 4096, 32/4 heads, D=64, f32; inputs: "
+                      f"{origin}) at {thra} threads: {usa:.0f} us/layer; at 6 threads {us6:.0f} "
+                      f"us/layer"),
+           "us_per_layer": usa, "us_per_layer_6_threads": us6}
+    if sample is not None:
+        ref = oracle.attention(q, lay, 4096, 4095, 32, 4, 64, threads=thra).reshape(32, 64)
+        out.update(_err(sample["out"], ref))
+    return out
 
 
 def cpu_baseline_c1():
@@ -536,6 +598,17 @@ def bench_c4(nh, torch, steps, warmup, seed=0):
         reps = max(steps, 2 * C4_R)
         us = event_mean(call, reps, torch) * 1e3
         pct = event_pcts(call, reps, torch)
+        if stride == 0:
+            # rotation 0: every sequence's window rows [Hkv][4096][40 B], q and output
+            calls[0]()
+            torch.cuda.synchronize()
+            t = torch.arange(ctx - w, ctx, device="cuda")
+            smp = {"q": q.cpu().numpy(), "out": out.cpu().numpy(), "k": [], "v": []}
+            for b in range(B):
+                blk = tab[0, b].long()[t // bt]
+                smp["k"].append(kp[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy())
+                smp["v"].append(vp[blk, :, t % bt].permute(1, 0, 2).contiguous().cpu().numpy())
+            SAMPLES["c4"] = smp
         res[f"stride{stride}"] = {
             "us_per_layer": us, "us_per_layer_wall": ms * 1e3, "us_p10_p50_p90": _us3(pct),
             "reps": reps, "bytes_packed": nbytes, "gbs_packed": nbytes / (us * 1e-6) / 1e9,
@@ -671,37 +744,55 @@ def cpu_baseline_a5(seed=0):
             "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0"}
 
 
-def cpu_baseline_c4(seed=0):
+def cpu_baseline_c4(seed=0, sample=None):
     """Oracle on the 4-bit window workload: 8 sequences, ctx 131072, window
-    4096 (the attended rows quantised, Q4-20B)."""
+    4096 (the attended rows, Q4-20B).  With `sample` (the GPU run's own
+    window rows, in position order) the oracle runs on those bytes, its
+    outputs compared with the GPU's."""
     import oracle
     import workloads as W
 
     B, ctx, w, bt, hkv, hd = 8, 131072, 4096, 16, 4, 64
-    rng = np.random.default_rng(seed)
-    nblk = ctx // bt
-    tables = rng.permutation(B * nblk).astype(np.int32).reshape(B, nblk)
     rb = oracle.q4_row_bytes(hd)
-    kp = np.zeros((B * nblk, hkv, bt, rb), np.uint8)
-    vp = np.zeros_like(kp)
-    pos = oracle.sparse_positions(ctx, ctx - 1, w, 0)
-    for b in range(B):
-        blk = tables[b, pos // bt]
-        kp[blk, :, pos % bt] = oracle.q4_quantize_rows(rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
-        vp[blk, :, pos % bt] = oracle.q4_quantize_rows(rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
-    q = rng.standard_normal((B, 32, hd), dtype=np.float32)
-    pb = W.PagedBatch(q, kp, vp, tables, np.full(B, ctx, np.int32), 32, hkv, hd, bt, oracle.KV_Q4, seed)
+    if sample is not None:
+        # the window's rows only: positions ctx-w .. ctx-1 are rows 0 .. w-1
+        q = sample["q"]
+        lays = [oracle.contiguous_layout(sample["k"][b], sample["v"][b], w, hd, oracle.KV_Q4)
+                for b in range(B)]
+        pos = np.arange(w, dtype=np.int32)
+        origin = "the GPU run's own q and window rows, copied from HBM"
+    else:
+        rng = np.random.default_rng(seed)
+        nblk = ctx // bt
+        tables = rng.permutation(B * nblk).astype(np.int32).reshape(B, nblk)
+        kp = np.zeros((B * nblk, hkv, bt, rb), np.uint8)
+        vp = np.zeros_like(kp)
+        pos = oracle.sparse_positions(ctx, ctx - 1, w, 0)
+        for b in range(B):
+            blk = tables[b, pos // bt]
+            kp[blk, :, pos % bt] = oracle.q4_quantize_rows(
+                rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+            vp[blk, :, pos % bt] = oracle.q4_quantize_rows(
+                rng.standard_normal((len(pos), hkv, hd), dtype=np.float32))
+        q = rng.standard_normal((B, 32, hd), dtype=np.float32)
+        pb = W.PagedBatch(q, kp, vp, tables, np.full(B, ctx, np.int32), 32, hkv, hd, bt,
+                          oracle.KV_Q4, seed)
+        lays = [pb.layout(b) for b in range(B)]
+        origin = "a seeded draw of the same shapes"
     thr = _cores()
 
     def run():
-        for b in range(B):
-            oracle.attention_positions(q[b], pb.layout(b), pos, 32, hkv, hd, threads=thr)
+        return [oracle.attention_positions(q[b], lays[b], pos, 32, hkv, hd, threads=thr)
+                for b in range(B)]
 
     dt, n = _cpu_time(run)
     nbytes = 2 * B * len(pos) * hkv * rb
-    return {"value": dt * 1e6, "unit": "us/layer", "cores": thr, "kind": "port",
-            "gbs_packed": nbytes / dt / 1e9,
-            "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0"}
+    out = {"value": dt * 1e6, "unit": "us/layer", "cores": thr, "kind": "port",
+           "gbs_packed": nbytes / dt / 1e9,
+           "sample": f"{n} runs of all 8 sequences, window 4096, global stride 0 (inputs: {origin})"}
+    if sample is not None:
+        out.update(_err(sample["out"], np.stack([o.reshape(32, hd) for o in run()])))
+    return out
 
 
 # ----------------------------------------------------------------------------
@@ -754,6 +845,13 @@ def bench_c5(nh, torch, steps, warmup, seed=0):
     pct_kv = event_pcts(attn_kv, reps, torch)
     us_kv_q4 = event_mean(attn_kv_q4, reps, torch) * 1e3
     us_quant = event_mean(quant, reps, torch) * 1e3
+    attn(0)
+    torch.cuda.synchronize()
+
+    def f32_of(x):  # bf16 tensor -> its exact f32 values on the host
+        return (x.view(torch.int16).cpu().numpy().astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    SAMPLES["c5"] = {"q": f32_of(q), "k": f32_of(k), "v": f32_of(v), "out": out.cpu().numpy()}
     quant_bytes = n * Hkv * D * 4 + n * Hkv * rbq
     tf = flops / (us * 1e-6) / 1e12
     busy = _profile_value("prefill_c5_mfma_counters.txt", "mfma_busy_frac", "c5")
@@ -846,29 +944,39 @@ def bench_c5_sustained(nh, torch, seconds, seed=0):
     return res
 
 
-def cpu_baseline_c5(seed=0, n_rows=256):
+def cpu_baseline_c5(seed=0, n_rows=256, sample=None):
     """The reference's prefill: one decode call per row (executor.rs:132-137),
     timed on n_rows rows spread over the 8192 and scaled by attended keys."""
     import oracle
     import workloads as W
 
     n, hq, hkv, d = 8192, 32, 8, 128
-    q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=seed)
-    qb, kb, vb = W.bf16_round(q), W.bf16_round(k), W.bf16_round(v)
-    lay = oracle.token_major_layout(kb, vb, hkv, d)
+    if sample is not None:  # the GPU run's own bf16 inputs, as their f32 values
+        qb, kb, vb = sample["q"], sample["k"], sample["v"]
+        origin = "the GPU run's own bf16 q, k, v, copied from HBM"
+    else:
+        q, k, v = W.prefill_inputs(n, hq, hkv, d, seed=seed)
+        qb, kb, vb = W.bf16_round(q), W.bf16_round(k), W.bf16_round(v)
+        origin = "a seeded draw of the same shapes, rounded to bf16"
+    lay = oracle.token_major_layout(np.ascontiguousarray(kb), np.ascontiguousarray(vb), hkv, d)
     rows = np.linspace(0, n - 1, n_rows).astype(np.int32)
     thr = _cores()
-    qf = qb.reshape(n, -1)
+    qf = np.ascontiguousarray(qb.reshape(n, -1))
     dt, runs = _cpu_time(lambda: oracle.attention_rows(qf, lay, rows, hq, hkv, d, threads=thr),
                          budget_s=3.0, max_calls=50)
     keys_sample = float((rows.astype(np.int64) + 1).sum())
     keys_all = n * (n + 1) / 2.0
     est = dt * keys_all / keys_sample
     flops = 4 * hq * d * keys_all
-    return {"value": flops / est / 1e12, "unit": "TFLOP/s (extrapolated)", "cores": thr,
-            "kind": "port", "us_extrapolated": est * 1e6,
-            "sample": (f"{runs} runs of {n_rows} evenly spaced rows, all 32 heads "
-                       f"({dt * 1e3:.1f} ms), scaled by attended keys to all 8192 rows")}
+    out = {"value": flops / est / 1e12, "unit": "TFLOP/s (extrapolated)", "cores": thr,
+           "kind": "port", "us_extrapolated": est * 1e6,
+           "sample": (f"{runs} runs of {n_rows} evenly spaced rows, all 32 heads "
+                      f"({dt * 1e3:.1f} ms; inputs: {origin}), scaled by attended keys to all "
+                      f"8192 rows")}
+    if sample is not None:
+        ref = oracle.attention_rows(qf, lay, rows, hq, hkv, d, threads=thr).reshape(n, hq, d)
+        out.update(_err(sample["out"][rows], ref[rows]))
+    return out
 
 
 # ----------------------------------------------------------------------------
@@ -1307,10 +1415,10 @@ def main():
                         ("a5", cpu_baseline_a5), ("c5", cpu_baseline_c5)):
             if key in res:
                 log(f"CPU baseline (oracle) for {key}")
-                res[key]["cpu_baseline"] = fn()
+                res[key]["cpu_baseline"] = (fn(sample=SAMPLES[key]) if key in SAMPLES else fn())
         if "c3" in res:
             log("CPU baseline (oracle) on a sample of the headline batch")
-            cpu = cpu_baseline_c3()
+            cpu = cpu_baseline_c3(sample=SAMPLES.get("c3"))
 
     c3 = res.get("c3")
     line = {
