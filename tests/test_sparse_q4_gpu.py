@@ -124,3 +124,29 @@ def test_sparse_q4_rejects_short_workspace(gpu):
     with pytest.raises(gpu.NyionError):
         run(gpu, q, k, v, bases, 1, 0, [700], 1, 512, 0,
             workspace=torch.empty(256, dtype=torch.uint8, device="cuda"))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_sparse_q4_random(gpu, seed):
+    """Seeded random configurations: head_dim 64 or 128, 1-8 kv heads and
+    1-16 q heads per kv head, batches of 1-4 sequences of 1-9000 tokens
+    (zone pages of 32 and 128 tokens), windows of 1-5000, global strides of
+    0-300, with and without q positions."""
+    rng = np.random.default_rng(3000 + seed)
+    hd = int(rng.choice([64, 128]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8, 16]))
+    ctx = [int(x) for x in rng.integers(1, 9001, size=int(rng.integers(1, 5)))]
+    window = int(rng.integers(1, 5001))
+    stride = int(rng.choice([0, 7, 64, 300]))
+    q_pos = [int(rng.integers(0, c)) for c in ctx] if rng.random() < 0.4 else None
+    n_layers, layer = 2, int(rng.integers(0, 2))
+    print(f"case {seed}: hd {hd} heads {hq}/{hkv} ctx {ctx} window {window} stride {stride} "
+          f"q_pos {q_pos}", flush=True)
+    pools, k, v, bases = zone_batch(ctx, n_layers, hkv, hd, oracle.KV_Q4, seed=4000 + seed)
+    q = rng.standard_normal((len(ctx), hq, hd)).astype(np.float32)
+    got = run(gpu, q, k, v, bases, n_layers, layer, ctx, hkv, window, stride, q_pos=q_pos)
+    for b, zp in enumerate(pools):
+        qp = ctx[b] - 1 if q_pos is None else q_pos[b]
+        assert_close(got[b], expected(q[b], zp, layer, ctx[b], qp, window, stride),
+                     f"case {seed} seq {b}")
