@@ -53,6 +53,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "common.hpp"
@@ -196,10 +197,13 @@ __device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e,
 //   f16: value c = 8x+4e+y (binary16 MFMA 2x+e, element y) holds dim
 //        32x + 8kq + 4e + y  (per x, the 4 quads of a row read 64 contiguous
 //        bytes)
-//   Q4 : as f32, in binary16 steps of 16 dims: step x = c/4 holds dims
-//        16x + 4kq .. +3, the lane's 4 nibbles of K row j
-// The Q operand uses the same map (qk_dim).  V operand of lane (col j, quad
-// kq), row 4kq+r: DPL = D/16 consecutive dims from DPL*j.
+//   Q4 : per 32-element group g, the lane's four nibble bytes 4kq .. 4kq+3
+//        (elements 8kq .. 8kq+7, element 2i in the low nibble of byte i) as
+//        two binary16 MFMAs: class a takes elements 8kq + {0, 4, 2, 6}, class
+//        b elements 8kq + {1, 5, 3, 7} (q_operand_q4)
+// The Q operand uses the same map (qk_dim; q_operand_q4 for Q4).  V operand
+// of lane (col j, quad kq), row 4kq+r: DPL = D/16 consecutive dims from
+// DPL*j.
 template <int D, int KVT>
 __device__ __forceinline__ int qk_dim(int c, int kq) {
     if constexpr (KVT == NYION_KV_F16)
@@ -226,7 +230,7 @@ struct Tile<D, NYION_KV_F16> {
 
 template <int D>
 struct Tile<D, NYION_KV_Q4_20B> {
-    uint32_t kn[D / 16];      // K row j, step x: the nibbles of dims 16x + 4kq .. +3 (low 16 bits)
+    uint32_t kn[D / 32];      // K row j, group g: nibble bytes 4kq .. 4kq+3
     uint32_t khdr;            // K row j, group kq % (D/32): f16 d | f16 dmin << 16
     uint32_t vhdr[4];
     uint32_t v[4];            // D/16 nibbles of V row 4kq+r (low 16 bits when D = 64)
@@ -269,14 +273,13 @@ __device__ __forceinline__ void load_tile(Tile<D, KVT>& t, const void* kb, const
                 t.v[r][x] = __builtin_nontemporal_load((const floatx4*)(vr + 4 * x));
         }
     } else {
-        // K row j: step x is group x/2, nibble bytes 8(x&1) + 2kq, +1; and
-        // the header of group kq % (D/32) (lane 16g + i then holds row i's
-        // header of group g)
+        // K row j: nibble bytes 4kq .. 4kq+3 of every group; and the header
+        // of group kq % (D/32) (lane 16g + i then holds row i's header of
+        // group g)
         const uint8_t* kr = (const uint8_t*)kb + koff;
 #pragma unroll
-        for (int x = 0; x < D / 16; x++)
-            t.kn[x] = __builtin_nontemporal_load(
-                (const uint16_t*)(kr + kQ4GroupBytes * (x >> 1) + 4 + 8 * (x & 1) + 2 * kq));
+        for (int g = 0; g < D / 32; g++)
+            t.kn[g] = __builtin_nontemporal_load((const uint32_t*)(kr + kQ4GroupBytes * g + 4 + 4 * kq));
         t.khdr = __builtin_nontemporal_load((const uint32_t*)(kr + kQ4GroupBytes * (kq % (D / 32))));
         const int ve0 = (D / 16) * j;
 #pragma unroll
@@ -324,6 +327,90 @@ struct State {
     float l;
 };
 
+// Max over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four quads of one column)
+// with gfx950's lane swaps: permlane16_swap(v, v) pairs each lane with its
+// partner in the neighbouring row of 16, permlane32_swap(v, v) with its
+// partner in the other half; no LDS round trip.
+__device__ __forceinline__ float max_across_quads(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Four values as binary16 (two words) and their binary16 residuals (two
+// more): hi + lo carries 22 significant bits of each value.
+__device__ __forceinline__ void pack_hi_lo(const float* v, float* w) {
+    const halfx4 hi = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    const halfx4 lo = {(_Float16)(v[0] - (float)hi[0]), (_Float16)(v[1] - (float)hi[1]),
+                       (_Float16)(v[2] - (float)hi[2]), (_Float16)(v[3] - (float)hi[3])};
+    const floatx2 hw = __builtin_bit_cast(floatx2, hi), lw = __builtin_bit_cast(floatx2, lo);
+    w[0] = hw[0];
+    w[1] = hw[1];
+    w[2] = lw[0];
+    w[3] = lw[1];
+}
+
+// Q operand of the Q4-20B QK product for lane (head j, quad kq), the B side
+// of the K tile's class a / class b MFMAs: per group g, words 8g .. 8g+3 =
+// elements 32g + 8kq + {0, 4, 2, 6} split by pack_hi_lo, words 8g+4 .. 8g+7
+// = elements 32g + 8kq + {1, 5, 3, 7} divided by 16, split the same way;
+// word D/4 + g = 2^-24 times the sum of the head's q over group g.  ok =
+// false (a pad head) gives zeros.  Returns whether some |q| >= 65520, whose
+// binary16 high part rounds to infinity.
+template <int D>
+__device__ __forceinline__ bool q_operand_q4(const float* qrow, bool ok, int kq, float* qv) {
+    bool big = false;
+#pragma unroll
+    for (int g = 0; g < D / 32; g++) {
+        const float4 z = {0.f, 0.f, 0.f, 0.f};
+        const float4 u = ok ? *(const float4*)(qrow + 32 * g + 8 * kq) : z;
+        const float4 w = ok ? *(const float4*)(qrow + 32 * g + 8 * kq + 4) : z;
+        const float e[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sum += e[i];
+            big |= fabsf(e[i]) >= 65520.f;
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        qv[D / 4 + g] = sum * 0x1p-24f;
+        const float ca[4] = {e[0], e[4], e[2], e[6]};
+        const float cb[4] = {e[1] * 0.0625f, e[5] * 0.0625f, e[3] * 0.0625f, e[7] * 0.0625f};
+        pack_hi_lo(ca, qv + 8 * g);
+        pack_hi_lo(cb, qv + 8 * g + 4);
+    }
+    return big;
+}
+
+// Headers of rows 4kq .. 4kq+3 of a gathered Q4-20B tile (khr[g][r]) come
+// from the lanes that loaded them (lane 16g + i holds row i's header of
+// group g) through a per-wavefront LDS slot [group][row]: one write and one
+// 16-byte read per group.  The wavefront's LDS operations complete in order,
+// so the slot needs no barrier.
+template <int D>
+__device__ __forceinline__ uint32_t (*q4_header_slot())[16] {
+    __shared__ __attribute__((aligned(16))) uint32_t sm_khdr[4][D / 32][16];
+    return sm_khdr[threadIdx.x >> 6];
+}
+
+template <int D>
+__device__ __forceinline__ void q4_headers_put(const Tile<D, NYION_KV_Q4_20B>& t, int kq) {
+    if (kq < D / 32) q4_header_slot<D>()[kq][threadIdx.x & 15] = t.khdr;
+}
+
+template <int D>
+__device__ __forceinline__ void q4_headers_get(int kq, uint32_t (*khr)[4]) {
+    uint32_t(*hs)[16] = q4_header_slot<D>();
+#pragma unroll
+    for (int g = 0; g < D / 32; g++) {
+        const u32x4 h4 = *(const u32x4*)&hs[g][4 * kq];
+#pragma unroll
+        for (int r = 0; r < 4; r++) khr[g][r] = h4[r];
+    }
+}
+
 // Rescale threshold of the online softmax, log2 units.  The running max of a
 // head is only moved when a tile's max exceeds it by more than this, so
 // exp2(s - m) <= 2^8 and the O rescale is rare after the first tiles.
@@ -335,7 +422,7 @@ constexpr float kRescaleLog2 = 8.0f;
 template <int D, int KVT, bool MASKED, bool TRACK>
 __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t, const float* qv,
                                              uint32_t mask, int kq, float scale_log2, float* srow,
-                                             const int* pos) {
+                                             const int* pos, const uint32_t (*khr)[4]) {
     constexpr int NC = D / 4;
     constexpr int DPL = D / 16;
     floatx4 s = {0.f, 0.f, 0.f, 0.f};
@@ -359,49 +446,44 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
     } else if constexpr (KVT == NYION_KV_Q4_20B) {
         // k = d*nib + dmin per 32-element group g, so q.k = sum_g d*(nib.q)_g
         // + dmin*sum(q_g): the nibbles are exact binary16 operands against q
-        // split into binary16 high and low parts (qv words as for binary16
-        // KV; qv[NC + g] = sum of head j's q over group g), one accumulator
-        // per group, then each row's d and dmin (headers of rows 4kq+r, from
-        // the lanes that loaded them).
-        // The headers go through a per-wavefront LDS slot, [group][row], so
-        // that each lane reads those of its four rows 4kq .. 4kq+3 with one
-        // 16-byte read per group.
-        __shared__ __attribute__((aligned(16))) uint32_t sm_khdr[4][D / 32][16];
-        uint32_t(*hs)[16] = sm_khdr[threadIdx.x >> 6];
-        if (kq < D / 32) hs[kq][threadIdx.x & 15] = t.khdr;
+        // split into binary16 high and low parts (q_operand_q4; qv[NC + g] =
+        // 2^-24 times the sum of head j's q over group g), one accumulator
+        // per group, then each row's d and dmin (khr[g][r]: the header of
+        // row 4kq+r, group g).  A nibble masked in place is a binary16
+        // denormal: bits e (elements 8kq + {0, 4, 2, 6}, class a) or 16e
+        // (elements 8kq + {1, 5, 3, 7}, class b, whose q carries 1/16), times
+        // 2^-24; the MFMA takes denormal inputs exactly, so the scores come
+        // out scaled by 2^-24 (undone with the softmax scale).  khr null (a
+        // gathered tile): the headers come from the lanes that loaded them,
+        // written to the exchange slot before the MFMAs and read after.
+        if (!khr) q4_headers_put<D>(t, kq);
         floatx4 sg[D / 32];
 #pragma unroll
-        for (int g = 0; g < D / 32; g++) sg[g] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-#pragma unroll
-        for (int x = 0; x < D / 16; x++) {
-            // nibbles e0..e3 of dims 16x + 4kq .. +3 as binary16 1024 + e, less
-            // 1024: bytes [e0 e2 64 64] and [e1 e3 64 64], then one byte
-            // permute per pair of values
-            const uint32_t w = t.kn[x];
-            const uint32_t lo = (w & 0x0f0fu) | 0x64640000u;
-            const uint32_t hi = ((w >> 4) & 0x0f0fu) | 0x64640000u;
-            const halfx2 h01 = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(hi, lo, 0x06040200u)) - k1024;
-            const halfx2 h23 = __builtin_bit_cast(halfx2, __builtin_amdgcn_perm(hi, lo, 0x07050301u)) - k1024;
-            const halfx4 kx = {h01[0], h01[1], h23[0], h23[1]};
-            const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
-            const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
-            sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, sg[x >> 1], 0, 0, 0);
-            sg[x >> 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, sg[x >> 1], 0, 0, 0);
-        }
-        uint32_t hr[D / 32][4];
-#pragma unroll
         for (int g = 0; g < D / 32; g++) {
-            const u32x4 h4 = *(const u32x4*)&hs[g][4 * kq];
-#pragma unroll
-            for (int r = 0; r < 4; r++) hr[g][r] = h4[r];
+            const uint32_t w = t.kn[g], w8 = w >> 8;
+            const halfx4 ka = __builtin_bit_cast(halfx4, u32x2{w & 0x000f000fu, w8 & 0x000f000fu});
+            const halfx4 kb = __builtin_bit_cast(halfx4, u32x2{w & 0x00f000f0u, w8 & 0x00f000f0u});
+            const float* qg = qv + 8 * g;
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                ka, __builtin_bit_cast(halfx4, floatx2{qg[0], qg[1]}), floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, __builtin_bit_cast(halfx4, floatx2{qg[2], qg[3]}),
+                                                          sg[g], 0, 0, 0);
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, __builtin_bit_cast(halfx4, floatx2{qg[4], qg[5]}),
+                                                          sg[g], 0, 0, 0);
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, __builtin_bit_cast(halfx4, floatx2{qg[6], qg[7]}),
+                                                          sg[g], 0, 0, 0);
+        }
+        uint32_t hx[D / 32][4];
+        if (!khr) {
+            q4_headers_get<D>(kq, hx);
+            khr = hx;
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             float acc = 0.f;
 #pragma unroll
             for (int g = 0; g < D / 32; g++) {
-                const float d = f16_bits_to_f32(hr[g][r]), dmin = f16_bits_to_f32(hr[g][r] >> 16);
+                const float d = f16_bits_to_f32(khr[g][r]), dmin = f16_bits_to_f32(khr[g][r] >> 16);
                 acc = __builtin_fmaf(d, sg[g][r], __builtin_fmaf(dmin, qv[NC + g], acc));
             }
             s[r] = acc;
@@ -413,10 +495,12 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
     }
 
+    // Q4-20B scores come out of the MFMAs scaled by 2^-24 (exact: a power of two)
+    const float sc = KVT == NYION_KV_Q4_20B ? scale_log2 * 16777216.f : scale_log2;
     float sv[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        sv[r] = s[r] * scale_log2;
+        sv[r] = s[r] * sc;
         if (MASKED) sv[r] = ((mask >> (4 * kq + r)) & 1u) ? sv[r] : -1e30f;
     }
     if (TRACK && srow) {
@@ -431,9 +515,7 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
                 if ((mq >> r) & 1u) srow[pos[r]] = sv[r];
         }
     }
-    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mt = max_across_quads(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
     if (__any(mt > st.m + kRescaleLog2)) {  // wave-uniform; first tile always
         const float mnew = fmaxf(st.m, mt);
         const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
@@ -563,11 +645,77 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
 template <int D, int KVT, bool TRACK>
 __device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, const float* qv,
                                         uint32_t mask, int kq, float scale_log2, float* srow,
-                                        const int* pos) {
+                                        const int* pos, const uint32_t (*khr)[4] = nullptr) {
     if (mask == 0xffffu)
-        consume_tile<D, KVT, false, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos);
+        consume_tile<D, KVT, false, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos, khr);
     else if (mask)
-        consume_tile<D, KVT, true, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos);
+        consume_tile<D, KVT, true, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos, khr);
+}
+
+// A Q4-20B tile of a contiguous walk (aligned blocks of >= 16 tokens, zone
+// units of 32): its 16 K rows and its 16 V rows are each one span of 16 * TS
+// bytes (TS = row bytes), loaded as CH = TS chunks of 16 bytes, lane l taking
+// chunks l and l + 64 (lanes past the span take its last chunk again): one
+// or two wide loads per span instead of a narrow load per row and field.
+template <int D>
+struct SpanTile {
+    static constexpr int TS = q4_row_bytes(D);
+    static constexpr int CH = TS;
+    static constexpr int KC = (CH + 63) / 64;
+    u32x4a k[KC], v[KC];
+};
+
+template <int D>
+__device__ __forceinline__ void load_span(SpanTile<D>& t, const void* kb, const void* vb, long long base,
+                                          int lane) {
+    const uint8_t* k = (const uint8_t*)kb + base;
+    const uint8_t* v = (const uint8_t*)vb + base;
+#pragma unroll
+    for (int c = 0; c < SpanTile<D>::KC; c++) {
+        const int ch = min(lane + 64 * c, SpanTile<D>::CH - 1);
+        t.k[c] = __builtin_nontemporal_load((const u32x4a*)(k + 16 * ch));
+        t.v[c] = __builtin_nontemporal_load((const u32x4a*)(v + 16 * ch));
+    }
+}
+
+// Operands of a span tile: the chunks go to a per-wavefront LDS slot (rows at
+// TS-byte strides, K then V), from which each lane reads the words the tile
+// layout gives it (Tile<D, Q4-20B>: K row j's nibble words, V rows 4kq+r's
+// header and nibbles) and the K headers of rows 4kq+r (khr[g][r]).  The
+// wavefront's LDS operations complete in order: the next tile's writes come
+// after these reads.
+template <int D>
+__device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_KV_Q4_20B>& t,
+                                           uint32_t (*khr)[4], int j, int kq) {
+    constexpr int TS = SpanTile<D>::TS, KC = SpanTile<D>::KC, DPL = D / 16;
+    __shared__ u32x4 sm_span[4][2][KC * 64];
+    const int lane = threadIdx.x & 63;
+    u32x4* ks = sm_span[threadIdx.x >> 6][0];
+    u32x4* vs = sm_span[threadIdx.x >> 6][1];
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+        ks[lane + 64 * c] = sp.k[c];
+        vs[lane + 64 * c] = sp.v[c];
+    }
+    const uint8_t* kr = (const uint8_t*)ks;
+    const uint8_t* vr = (const uint8_t*)vs;
+#pragma unroll
+    for (int g = 0; g < D / 32; g++) {
+        t.kn[g] = *(const uint32_t*)(kr + TS * j + kQ4GroupBytes * g + 4 + 4 * kq);
+#pragma unroll
+        for (int r = 0; r < 4; r++) khr[g][r] = *(const uint32_t*)(kr + TS * (4 * kq + r) + kQ4GroupBytes * g);
+    }
+    const int gv = (DPL * j) >> 5;                  // the group of the lane's V dims
+    const int nv = 4 + (((DPL * j) & 31) >> 1);     // their first nibble byte in the group
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint8_t* row = vr + TS * (4 * kq + r) + kQ4GroupBytes * gv;
+        t.vhdr[r] = *(const uint32_t*)row;
+        if constexpr (D == 64)
+            t.v[r] = *(const uint16_t*)(row + nv);
+        else
+            t.v[r] = *(const uint32_t*)(row + nv);
+    }
 }
 
 // Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
@@ -711,26 +859,69 @@ __device__ __forceinline__ uint32_t global_offsets(const DecodeArgs& a, const Ex
     return mask;
 }
 
-// Walk `n` tiles with the next tile's loads in flight during each MFMA chain.
-// Every step issues exactly one tile of loads (at the end, a repeat of the
-// last tile that is never consumed), so the number of loads in flight is the
-// same on every path and each tile waits only for its own loads.
-template <int D, int KVT, bool TRACK, typename Offsets>
+// Tiles whose loads a wavefront keeps in flight: the one being consumed and
+// NB - 1 ahead.  A Q4-20B span tile (head_dim 64) is 1280 bytes, a sixth of
+// an f32 tile, so it takes a ring of four.  Gathered tiles (position lists,
+// strided globals) keep two: their walks are short, and the extra tiles
+// loaded past a walk's end cost more than the deeper ring gains.
+template <int D, int KVT, bool SPAN>
+constexpr int tile_ring() {
+    return SPAN ? 4 : 2;
+}
+
+// Walk `n` tiles with the next NB - 1 tiles' loads in flight during each MFMA
+// chain.  The ring is unrolled NB times so that every slot is a fixed set of
+// registers (no copies between slots).  Every step issues exactly one tile of
+// loads (at the end, repeats of the last tile that are never consumed), so the
+// number of loads in flight is the same on every path and each tile waits
+// only for its own loads.  CONTIG: the offsets describe tiles of 16
+// consecutive rows (koff - j * TS is the first row of the tile), and Q4-20B
+// tiles are loaded as spans (SpanTile).
+template <int D, int KVT, bool TRACK, typename Offsets, bool CONTIG = false>
 __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, const float* qv, int n,
                                            int j, int kq, float* srow, Offsets offsets) {
-    Tile<D, KVT> ta, tb;
+    // head_dim 128 keeps per-row loads (twice the bytes per load; its span
+    // tiles and staged operands exceed the register budget)
+    constexpr bool SPAN = CONTIG && KVT == NYION_KV_Q4_20B && D == 64;
+    constexpr int NB = tile_ring<D, KVT, SPAN>();
+    constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
+    using RingTile = typename std::conditional<SPAN, SpanTile<D>, Tile<D, KVT>>::type;
+    RingTile t[NB];
+    uint32_t msk[NB];
     long long ko, vo[4];
-    int pa[4], pb[4];  // positions of this lane's score rows (used when TRACK)
+    int pos[NB][4];  // positions of this lane's score rows (used when TRACK)
+    const int lane = threadIdx.x & 63;
+    auto load = [&](RingTile& x) {
+        if constexpr (SPAN)
+            load_span<D>(x, a.k, a.v, ko - (long long)j * TS, lane);
+        else
+            load_tile<D, KVT>(x, a.k, a.v, ko, vo, j, kq);
+    };
+    auto eat = [&](const RingTile& x, uint32_t m, const int* p) {
+        if constexpr (SPAN) {
+            if (!m) return;
+            Tile<D, KVT> y;
+            uint32_t khr[D / 32][4];
+            stage_span<D>(x, y, khr, j, kq);
+            consume<D, KVT, TRACK>(st, y, qv, m, kq, a.scale_log2, srow, p, khr);
+        } else {
+            consume<D, KVT, TRACK>(st, x, qv, m, kq, a.scale_log2, srow, p);
+        }
+    };
     if (n <= 0) return;
-    uint32_t ma = offsets(0, ko, vo, pa);
-    load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
-    for (int i = 0; i < n; i += 2) {
-        uint32_t mb = offsets(min(i + 1, n - 1), ko, vo, pb);
-        load_tile<D, KVT>(tb, a.k, a.v, ko, vo, j, kq);
-        consume<D, KVT, TRACK>(st, ta, qv, ma, kq, a.scale_log2, srow, pa);
-        ma = offsets(min(i + 2, n - 1), ko, vo, pa);
-        load_tile<D, KVT>(ta, a.k, a.v, ko, vo, j, kq);
-        if (i + 1 < n) consume<D, KVT, TRACK>(st, tb, qv, mb, kq, a.scale_log2, srow, pb);
+#pragma unroll
+    for (int k = 0; k < NB - 1; k++) {
+        msk[k] = offsets(min(k, n - 1), ko, vo, pos[k]);
+        load(t[k]);
+    }
+    for (int i = 0; i < n; i += NB) {
+#pragma unroll
+        for (int k = 0; k < NB; k++) {
+            const int s = (k + NB - 1) % NB;  // the slot consumed NB - 1 steps from now
+            msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
+            load(t[s]);
+            if (k == 0 || i + k < n) eat(t[k], msk[k], pos[k]);
+        }
     }
 }
 
@@ -890,10 +1081,10 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         } else if (table) {
             w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
         }
-        walk_tiles<D, KVT, TRACK>(st, a, qv, nc, j, kq, srow,
-                                  [&](int i, long long& ko, long long* vo, int* pos) {
-                                      return aligned_offsets<D, KVT, ZONE>(a, w, f + i, j, kq, ko, vo, pos);
-                                  });
+        auto offs = [&](int i, long long& ko, long long* vo, int* pos) {
+            return aligned_offsets<D, KVT, ZONE>(a, w, f + i, j, kq, ko, vo, pos);
+        };
+        walk_tiles<D, KVT, TRACK, decltype(offs), true>(st, a, qv, nc, j, kq, srow, offs);
     }
 }
 
@@ -1142,36 +1333,28 @@ void decode_kernel(DecodeArgs a) {
         const int g_local = min(16, a.group - hg * 16);
         const int head0 = kvh * a.group + hg * 16;
 
-        // Q operand (B of the QK product): head j, dims by qk_dim.
-        // Q4-20B: NC + D/32 values, the group sums of head j's q after the NC
+        // Q operand (B of the QK product): head j, dims by qk_dim (Q4-20B:
+        // q_operand_q4, NC words and then the D/32 scaled group sums)
         float qv[KVT == NYION_KV_Q4_20B ? NC + D / 32 : NC];
         {
             const float* qrow = a.q + ((long long)b * a.n_heads + head0 + min(j, g_local - 1)) * D;
             const bool ok = j < g_local;
-            // the lane's dims come in runs of four (qk_dim(4i..4i+3) consecutive):
-            // one 16-byte load per run
-#pragma unroll
-            for (int i = 0; i < NC / 4; i++) {
-                const float4 r4 = ok ? *(const float4*)(qrow + qk_dim<D, KVT>(4 * i, kq)) : float4{0.f, 0.f, 0.f, 0.f};
-                qv[4 * i] = r4.x;
-                qv[4 * i + 1] = r4.y;
-                qv[4 * i + 2] = r4.z;
-                qv[4 * i + 3] = r4.w;
-            }
             if constexpr (KVT == NYION_KV_Q4_20B) {
-                // sum of head j's q over each 32-element group (steps 2g, 2g+1
-                // of every quad kq)
+                report_range(a.status, q_operand_q4<D>(qrow, ok, kq, qv), kRangeDecodeQ);
+            } else {
+                // the lane's dims come in runs of four (qk_dim(4i..4i+3)
+                // consecutive): one 16-byte load per run
 #pragma unroll
-                for (int g = 0; g < D / 32; g++) {
-                    float sum = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 8; i++) sum += qv[8 * g + i];
-                    sum += __shfl_xor(sum, 16);
-                    sum += __shfl_xor(sum, 32);
-                    qv[NC + g] = sum;
+                for (int i = 0; i < NC / 4; i++) {
+                    const float4 r4 =
+                        ok ? *(const float4*)(qrow + qk_dim<D, KVT>(4 * i, kq)) : float4{0.f, 0.f, 0.f, 0.f};
+                    qv[4 * i] = r4.x;
+                    qv[4 * i + 1] = r4.y;
+                    qv[4 * i + 2] = r4.z;
+                    qv[4 * i + 3] = r4.w;
                 }
             }
-            if constexpr (KVT == NYION_KV_F16 || KVT == NYION_KV_Q4_20B) {
+            if constexpr (KVT == NYION_KV_F16) {
                 // words 4x, 4x+1: the four values as binary16; 4x+2, 4x+3: the
                 // binary16 residuals.  |q| >= 65520 rounds the high part to
                 // infinity: reported through the status word.
@@ -1180,17 +1363,7 @@ void decode_kernel(DecodeArgs a) {
                 for (int cc = 0; cc < NC; cc++) big |= fabsf(qv[cc]) >= 65520.f;
                 report_range(a.status, big, kRangeDecodeQ);
 #pragma unroll
-                for (int x = 0; x < D / 16; x++) {
-                    const float* v = qv + 4 * x;
-                    const halfx4 hi = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-                    const halfx4 lo = {(_Float16)(v[0] - (float)hi[0]), (_Float16)(v[1] - (float)hi[1]),
-                                       (_Float16)(v[2] - (float)hi[2]), (_Float16)(v[3] - (float)hi[3])};
-                    const floatx2 hw = __builtin_bit_cast(floatx2, hi), lw = __builtin_bit_cast(floatx2, lo);
-                    qv[4 * x] = hw[0];
-                    qv[4 * x + 1] = hw[1];
-                    qv[4 * x + 2] = lw[0];
-                    qv[4 * x + 3] = lw[1];
-                }
+                for (int x = 0; x < D / 16; x++) pack_hi_lo(qv + 4 * x, qv + 4 * x);
             }
         }
 
