@@ -325,6 +325,10 @@ struct State {
     floatx4 acc_m;  // Q4-20B: sum of p * dmin/32 (the same for every dim of a lane's column)
     float m;
     float l;
+    // Q4-20B: 0x64006400 held in a register (opaque to the compiler), so that
+    // mask-and-insert of the nibbles is one v_and_or_b32 (gfx9 VOP3 takes no
+    // literal and one scalar operand)
+    uint32_t k6464;
 };
 
 // Max over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four quads of one column)
@@ -529,9 +533,11 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             if constexpr (KVT == NYION_KV_Q4_20B) st.acc_m[r] *= ar;
         }
     }
+    // Q4-20B: pr = 32p (the P.V operand), l accumulated in units of 32
+    const float mp = KVT == NYION_KV_Q4_20B ? st.m - 5.f : st.m;
     float pr[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - st.m);
+    for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - mp);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
     if constexpr (KVT == NYION_KV_F16) {
         // O += P.V on binary16 MFMAs: A = this lane's four p (tokens 4kq..+3
@@ -558,12 +564,12 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
                 pa, __builtin_bit_cast(halfx4, u32x2{b01, b23}), st.acc[z], 0, 0, 0);
         }
     } else if constexpr (KVT == NYION_KV_Q4_20B) {
-        // O += P.V on binary16 MFMAs: A = 32p rounded to binary16 (as for
-        // binary16 KV; 32p <= 2^13), B = V/32 split into binary16 high and low
-        // parts (V dequantised exactly as dequant_block, then scaled by 2^-5,
-        // which is exact and keeps d*15 + dmin <= 2^20 inside binary16 range)
-        const halfx4 pa = {(_Float16)(32.f * pr[0]), (_Float16)(32.f * pr[1]), (_Float16)(32.f * pr[2]),
-                           (_Float16)(32.f * pr[3])};
+        // O += P.V on binary16 MFMAs: A = 32p rounded to binary16 (pr is 32p;
+        // as for binary16 KV; 32p <= 2^13), B = V/32 split into binary16 high
+        // and low parts (V dequantised exactly as dequant_block, then scaled by
+        // 2^-5, which is exact and keeps d*15 + dmin <= 2^20 inside binary16
+        // range)
+        const halfx4 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
         // v/32 = (d/32) nib + dmin/32 as three exact binary16 terms: hi =
         // (d/32) nib rounded, lo = fma(d/32, nib, -hi) (exact: the product has
         // at most 15 significant bits), and dmin/32, whose product with P is
@@ -590,31 +596,25 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         const halfx2 mm01 = __builtin_bit_cast(halfx2, m01) * s32, mm23 = __builtin_bit_cast(halfx2, m23) * s32;
         st.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{mm01[0], mm01[1], mm23[0], mm23[1]},
                                                          st.acc_m, 0, 0, 0);
-        // each row's nibbles split into even and odd elements, one per byte,
-        // with 0x64 in the spare bytes (binary16 1024 + e after a permute)
+        // byte b of the nibble words of rows 2p and 2p+1 side by side, [row
+        // 2p byte b, 0, row 2p+1 byte b, 0] (one permute per pair and byte):
+        // its low nibbles are element 2b of the two rows and its high nibbles
+        // element 2b + 1, each as binary16 1024 + e after a mask and 0x64 in
+        // the high bytes
+        constexpr int NBY = DPL / 2;  // nibble bytes per row: 2 at head_dim 64, 4 at 128
         const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        uint32_t ev[4][2], od[4][2];  // [row][word]: one word at head_dim 64, two at 128
+        uint32_t pw[2][NBY];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            if constexpr (DPL == 4) {
-                ev[r][0] = (t.v[r] & 0x0f0fu) | 0x64640000u;
-                od[r][0] = ((t.v[r] >> 4) & 0x0f0fu) | 0x64640000u;
-            } else {  // eight nibbles: two words each
-                const uint32_t e = t.v[r] & 0x0f0f0f0fu, o = (t.v[r] >> 4) & 0x0f0f0f0fu;
-                ev[r][0] = (e & 0xffffu) | 0x64640000u;
-                ev[r][1] = (e >> 16) | 0x64640000u;
-                od[r][0] = (o & 0xffffu) | 0x64640000u;
-                od[r][1] = (o >> 16) | 0x64640000u;
-            }
-        }
+        for (int p = 0; p < 2; p++)
+#pragma unroll
+            for (int b = 0; b < NBY; b++)
+                pw[p][b] = __builtin_amdgcn_perm(t.v[2 * p + 1], t.v[2 * p],
+                                                 0x0c000c00u | ((4u + b) << 16) | (uint32_t)b);
 #pragma unroll
         for (int z = 0; z < DPL; z++) {  // element z: nibble z of the lane's word
-            const int wz = (z >> 1) >> 1, bz = (z >> 1) & 1;  // word and byte of the element
-            const uint32_t sel = bz ? 0x07050301u : 0x06040200u;
-            const uint32_t n01 = (z & 1) ? __builtin_amdgcn_perm(od[1][wz], od[0][wz], sel)
-                                         : __builtin_amdgcn_perm(ev[1][wz], ev[0][wz], sel);
-            const uint32_t n23 = (z & 1) ? __builtin_amdgcn_perm(od[3][wz], od[2][wz], sel)
-                                         : __builtin_amdgcn_perm(ev[3][wz], ev[2][wz], sel);
+            const int b = z >> 1;
+            const uint32_t n01 = (((z & 1) ? pw[0][b] >> 4 : pw[0][b]) & 0x000f000fu) | st.k6464;
+            const uint32_t n23 = (((z & 1) ? pw[1][b] >> 4 : pw[1][b]) & 0x000f000fu) | st.k6464;
             const halfx2 e01 = __builtin_bit_cast(halfx2, n01) - k1024;
             const halfx2 e23 = __builtin_bit_cast(halfx2, n23) - k1024;
             const halfx2 h01 = dd01 * e01, h23 = dd23 * e23;
@@ -672,9 +672,9 @@ __device__ __forceinline__ void load_span(SpanTile<D>& t, const void* kb, const 
     const uint8_t* v = (const uint8_t*)vb + base;
 #pragma unroll
     for (int c = 0; c < SpanTile<D>::KC; c++) {
-        const int ch = min(lane + 64 * c, SpanTile<D>::CH - 1);
-        t.k[c] = __builtin_nontemporal_load((const u32x4a*)(k + 16 * ch));
-        t.v[c] = __builtin_nontemporal_load((const u32x4a*)(v + 16 * ch));
+        const uint32_t off = 16u * (uint32_t)min(lane + 64 * c, SpanTile<D>::CH - 1);
+        t.k[c] = __builtin_nontemporal_load((const u32x4a*)(k + off));
+        t.v[c] = __builtin_nontemporal_load((const u32x4a*)(v + off));
     }
 }
 
@@ -859,6 +859,14 @@ __device__ __forceinline__ uint32_t global_offsets(const DecodeArgs& a, const Ex
     return mask;
 }
 
+// Contiguous walks load Q4-20B tiles as spans at head_dim 64; head_dim 128
+// keeps per-row loads (twice the bytes per load; its span tiles and staged
+// operands exceed the register budget).
+template <int D, int KVT>
+constexpr bool span_tiles() {
+    return KVT == NYION_KV_Q4_20B && D == 64;
+}
+
 // Tiles whose loads a wavefront keeps in flight: the one being consumed and
 // NB - 1 ahead.  A Q4-20B span tile (head_dim 64) is 1280 bytes, a sixth of
 // an f32 tile, so it takes a ring of four.  Gathered tiles (position lists,
@@ -875,16 +883,13 @@ constexpr int tile_ring() {
 // loads (at the end, repeats of the last tile that are never consumed), so the
 // number of loads in flight is the same on every path and each tile waits
 // only for its own loads.  CONTIG: the offsets describe tiles of 16
-// consecutive rows (koff - j * TS is the first row of the tile), and Q4-20B
-// tiles are loaded as spans (SpanTile).
+// consecutive rows, and span tiles (span_tiles) are loaded as such, koff
+// being the tile's first row.
 template <int D, int KVT, bool TRACK, typename Offsets, bool CONTIG = false>
 __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, const float* qv, int n,
                                            int j, int kq, float* srow, Offsets offsets) {
-    // head_dim 128 keeps per-row loads (twice the bytes per load; its span
-    // tiles and staged operands exceed the register budget)
-    constexpr bool SPAN = CONTIG && KVT == NYION_KV_Q4_20B && D == 64;
+    constexpr bool SPAN = CONTIG && span_tiles<D, KVT>();
     constexpr int NB = tile_ring<D, KVT, SPAN>();
-    constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
     using RingTile = typename std::conditional<SPAN, SpanTile<D>, Tile<D, KVT>>::type;
     RingTile t[NB];
     uint32_t msk[NB];
@@ -893,20 +898,9 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
     const int lane = threadIdx.x & 63;
     auto load = [&](RingTile& x) {
         if constexpr (SPAN)
-            load_span<D>(x, a.k, a.v, ko - (long long)j * TS, lane);
+            load_span<D>(x, a.k, a.v, ko, lane);
         else
             load_tile<D, KVT>(x, a.k, a.v, ko, vo, j, kq);
-    };
-    auto eat = [&](const RingTile& x, uint32_t m, const int* p) {
-        if constexpr (SPAN) {
-            if (!m) return;
-            Tile<D, KVT> y;
-            uint32_t khr[D / 32][4];
-            stage_span<D>(x, y, khr, j, kq);
-            consume<D, KVT, TRACK>(st, y, qv, m, kq, a.scale_log2, srow, p, khr);
-        } else {
-            consume<D, KVT, TRACK>(st, x, qv, m, kq, a.scale_log2, srow, p);
-        }
     };
     if (n <= 0) return;
 #pragma unroll
@@ -920,7 +914,16 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
             const int s = (k + NB - 1) % NB;  // the slot consumed NB - 1 steps from now
             msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
             load(t[s]);
-            if (k == 0 || i + k < n) eat(t[k], msk[k], pos[k]);
+            if ((k == 0 || i + k < n) && msk[k]) {
+                if constexpr (SPAN) {
+                    Tile<D, KVT> y;
+                    uint32_t khr[D / 32][4];
+                    stage_span<D>(t[k], y, khr, j, kq);
+                    consume<D, KVT, TRACK>(st, y, qv, msk[k], kq, a.scale_log2, srow, pos[k], khr);
+                } else {
+                    consume<D, KVT, TRACK>(st, t[k], qv, msk[k], kq, a.scale_log2, srow, pos[k]);
+                }
+            }
         }
     }
 }
@@ -1081,8 +1084,11 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         } else if (table) {
             w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
         }
+        // span tiles take the tile's first row (row 0 for every lane: a
+        // wave-uniform offset)
+        constexpr bool SPAN = span_tiles<D, KVT>();
         auto offs = [&](int i, long long& ko, long long* vo, int* pos) {
-            return aligned_offsets<D, KVT, ZONE>(a, w, f + i, j, kq, ko, vo, pos);
+            return aligned_offsets<D, KVT, ZONE>(a, w, f + i, SPAN ? 0 : j, kq, ko, vo, pos);
         };
         walk_tiles<D, KVT, TRACK, decltype(offs), true>(st, a, qv, nc, j, kq, srow, offs);
     }
@@ -1373,6 +1379,8 @@ void decode_kernel(DecodeArgs a) {
         st.acc_m = floatx4{0.f, 0.f, 0.f, 0.f};
         st.m = -INFINITY;
         st.l = 0.f;
+        st.k6464 = 0x64006400u;
+        asm volatile("" : "+v"(st.k6464));
 
         // TRACK: this lane's head's row of the score buffer (pad heads: none)
         float* srow = nullptr;
@@ -1425,6 +1433,7 @@ void decode_kernel(DecodeArgs a) {
         if constexpr (KVT == NYION_KV_Q4_20B) {  // the dmin/32 term belongs to every dim
 #pragma unroll
             for (int x = 0; x < DPL; x++) st.acc[x] += st.acc_m;
+            st.l *= 0.03125f;  // accumulated in units of 32 (exact)
         }
 
         // ---- merge the four wavefronts through LDS (wave 0 keeps the result)
