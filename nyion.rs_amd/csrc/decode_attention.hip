@@ -64,6 +64,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 // 16 bytes at 8-byte alignment (binary16 rows): one dwordx4 load
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(8)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
@@ -199,8 +200,9 @@ __device__ __forceinline__ int virt_to_pos(const DecodeArgs& a, const Extent& e,
 //        bytes)
 //   Q4 : per 32-element group g, the lane's four nibble bytes 4kq .. 4kq+3
 //        (elements 8kq .. 8kq+7, element 2i in the low nibble of byte i) as
-//        two binary16 MFMAs: class a takes elements 8kq + {0, 4, 2, 6}, class
-//        b elements 8kq + {1, 5, 3, 7} (q_operand_q4)
+//        the eight values of a 16x16x32 binary16 MFMA: class a, elements
+//        8kq + {0, 4, 2, 6}, then class b, elements 8kq + {1, 5, 3, 7}
+//        (q_operand_q4)
 // The Q operand uses the same map (qk_dim; q_operand_q4 for Q4).  V operand
 // of lane (col j, quad kq), row 4kq+r: DPL = D/16 consecutive dims from
 // DPL*j.
@@ -356,12 +358,13 @@ __device__ __forceinline__ void pack_hi_lo(const float* v, float* w) {
 }
 
 // Q operand of the Q4-20B QK product for lane (head j, quad kq), the B side
-// of the K tile's class a / class b MFMAs: per group g, words 8g .. 8g+3 =
-// elements 32g + 8kq + {0, 4, 2, 6} split by pack_hi_lo, words 8g+4 .. 8g+7
-// = elements 32g + 8kq + {1, 5, 3, 7} divided by 16, split the same way;
-// word D/4 + g = 2^-24 times the sum of the head's q over group g.  ok =
-// false (a pad head) gives zeros.  Returns whether some |q| >= 65520, whose
-// binary16 high part rounds to infinity.
+// of the K tile's 16x16x32 MFMAs (eight binary16 values per lane: class a,
+// elements 32g + 8kq + {0, 4, 2, 6}, then class b, elements 32g + 8kq +
+// {1, 5, 3, 7} divided by 16): per group g, words 8g .. 8g+3 = the eight
+// values rounded to binary16, words 8g+4 .. 8g+7 = their binary16
+// residuals; word D/4 + g = 2^-24 times the sum of the head's q over group
+// g.  ok = false (a pad head) gives zeros.  Returns whether some |q| >=
+// 65520, whose binary16 high part rounds to infinity.
 template <int D>
 __device__ __forceinline__ bool q_operand_q4(const float* qrow, bool ok, int kq, float* qv) {
     bool big = false;
@@ -382,8 +385,17 @@ __device__ __forceinline__ bool q_operand_q4(const float* qrow, bool ok, int kq,
         qv[D / 4 + g] = sum * 0x1p-24f;
         const float ca[4] = {e[0], e[4], e[2], e[6]};
         const float cb[4] = {e[1] * 0.0625f, e[5] * 0.0625f, e[3] * 0.0625f, e[7] * 0.0625f};
-        pack_hi_lo(ca, qv + 8 * g);
-        pack_hi_lo(cb, qv + 8 * g + 4);
+        float wa[4], wb[4];
+        pack_hi_lo(ca, wa);
+        pack_hi_lo(cb, wb);
+        qv[8 * g + 0] = wa[0];
+        qv[8 * g + 1] = wa[1];
+        qv[8 * g + 2] = wb[0];
+        qv[8 * g + 3] = wb[1];
+        qv[8 * g + 4] = wa[2];
+        qv[8 * g + 5] = wa[3];
+        qv[8 * g + 6] = wb[2];
+        qv[8 * g + 7] = wb[3];
     }
     return big;
 }
@@ -461,21 +473,20 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         // gathered tile): the headers come from the lanes that loaded them,
         // written to the exchange slot before the MFMAs and read after.
         if (!khr) q4_headers_put<D>(t, kq);
+        // one 16x16x32 MFMA per group and q part: the lane's eight values
+        // are class a then class b (q_operand_q4 orders q the same way)
         floatx4 sg[D / 32];
 #pragma unroll
         for (int g = 0; g < D / 32; g++) {
             const uint32_t w = t.kn[g], w8 = w >> 8;
-            const halfx4 ka = __builtin_bit_cast(halfx4, u32x2{w & 0x000f000fu, w8 & 0x000f000fu});
-            const halfx4 kb = __builtin_bit_cast(halfx4, u32x2{w & 0x00f000f0u, w8 & 0x00f000f0u});
+            const halfx8 kab = __builtin_bit_cast(
+                halfx8, u32x4{w & 0x000f000fu, w8 & 0x000f000fu, w & 0x00f000f0u, w8 & 0x00f000f0u});
             const float* qg = qv + 8 * g;
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                ka, __builtin_bit_cast(halfx4, floatx2{qg[0], qg[1]}), floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, __builtin_bit_cast(halfx4, floatx2{qg[2], qg[3]}),
-                                                          sg[g], 0, 0, 0);
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, __builtin_bit_cast(halfx4, floatx2{qg[4], qg[5]}),
-                                                          sg[g], 0, 0, 0);
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, __builtin_bit_cast(halfx4, floatx2{qg[6], qg[7]}),
-                                                          sg[g], 0, 0, 0);
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                kab, __builtin_bit_cast(halfx8, floatx4{qg[0], qg[1], qg[2], qg[3]}), floatx4{0.f, 0.f, 0.f, 0.f},
+                0, 0, 0);
+            sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                kab, __builtin_bit_cast(halfx8, floatx4{qg[4], qg[5], qg[6], qg[7]}), sg[g], 0, 0, 0);
         }
         uint32_t hx[D / 32][4];
         if (!khr) {
