@@ -432,34 +432,15 @@ __device__ __forceinline__ void q4_headers_get(int kq, uint32_t (*khr)[4]) {
 // exp2(s - m) <= 2^8 and the O rescale is rare after the first tiles.
 constexpr float kRescaleLog2 = 8.0f;
 
-// One tile: bit i of `mask` (wave-uniform) marks row i of the 16 valid;
-// MASKED = false is the all-valid fast path.  TRACK: also store the scaled
-// scores of this lane's head (rows 4kq+r, at positions pos[r]) into srow.
-template <int D, int KVT, bool MASKED, bool TRACK>
-__device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t, const float* qv,
-                                             uint32_t mask, int kq, float scale_log2, float* srow,
-                                             const int* pos, const uint32_t (*khr)[4]) {
+// S of one Q4-20B tile for lane (head j, quad kq): rows 4kq+r, scaled by
+// 2^-24.  khr: the K headers of rows 4kq+r (null for a gathered tile:
+// exchanged through LDS).
+template <int D>
+__device__ __forceinline__ floatx4 q4_tile_scores(const Tile<D, NYION_KV_Q4_20B>& t, const float* qv, int kq,
+                                                  const uint32_t (*khr)[4]) {
     constexpr int NC = D / 4;
-    constexpr int DPL = D / 16;
     floatx4 s = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (KVT == NYION_KV_F16) {
-        // binary16 K as stored against q split into binary16 high and low
-        // parts (qv words 4x, 4x+1 and 4x+2, 4x+3): the products are exact in
-        // f32, so S keeps f32 accuracy at a quarter of the f32 MFMA cycles.
-        // Call x takes words 2(x&1), +1 of K load x/2 (dims 32(x/2) + 8kq +
-        // 4(x&1) .. +3).  The words are copied to scalars first: this
-        // compiler's __builtin_bit_cast of a vector element yields the bits
-        // of element 0.
-#pragma unroll
-        for (int x = 0; x < D / 16; x++) {
-            const uint32_t k0 = t.k[x >> 1][2 * (x & 1)], k1 = t.k[x >> 1][2 * (x & 1) + 1];
-            const halfx4 kx = __builtin_bit_cast(halfx4, u32x2{k0, k1});
-            const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
-            const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
-            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, s, 0, 0, 0);
-        }
-    } else if constexpr (KVT == NYION_KV_Q4_20B) {
+    {
         // k = d*nib + dmin per 32-element group g, so q.k = sum_g d*(nib.q)_g
         // + dmin*sum(q_g): the nibbles are exact binary16 operands against q
         // split into binary16 high and low parts (q_operand_q4; qv[NC + g] =
@@ -503,6 +484,159 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             }
             s[r] = acc;
         }
+    }
+    return s;
+}
+
+// Log2-unit scores of one tile (masked rows -1e30); TRACK: stored into srow
+// at positions pos[r] (rows 4kq+r of this lane's head).
+template <int KVT, bool MASKED, bool TRACK>
+__device__ __forceinline__ void tile_logits(const floatx4& s, float scale_log2, uint32_t mask, int kq,
+                                            float* srow, const int* pos, float* sv) {
+    // Q4-20B scores come out of the MFMAs scaled by 2^-24 (exact: a power of two)
+    const float sc = KVT == NYION_KV_Q4_20B ? scale_log2 * 16777216.f : scale_log2;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sv[r] = s[r] * sc;
+        if (MASKED) sv[r] = ((mask >> (4 * kq + r)) & 1u) ? sv[r] : -1e30f;
+    }
+    if (TRACK && srow) {
+        const uint32_t mq = (mask >> (4 * kq)) & 0xfu;
+        if (mq == 0xfu && pos[3] == pos[0] + 3) {
+            // four consecutive positions: one store (dword alignment suffices)
+            typedef float floatx4u __attribute__((ext_vector_type(4), aligned(4)));
+            *(floatx4u*)(srow + pos[0]) = floatx4u{sv[0], sv[1], sv[2], sv[3]};
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if ((mq >> r) & 1u) srow[pos[r]] = sv[r];
+        }
+    }
+}
+
+// Online-softmax step over the lane's N scores (N / 4 tiles; score i is row
+// 4kq + (i & 3) of its tile): the running max moves, with the O rescale, only
+// when the scores' max exceeds it by more than kRescaleLog2 (wave-uniform;
+// always on the first step).  pr = exp2(s - m) (Q4-20B: 32 exp2(s - m), the
+// P.V operand, l accumulated in units of 32).
+template <int D, int KVT, int N>
+__device__ __forceinline__ void softmax_step(State<D>& st, const float* sv, int kq, float* pr) {
+    constexpr int DPL = D / 16;
+    float mx = sv[0];
+#pragma unroll
+    for (int i = 1; i < N; i++) mx = fmaxf(mx, sv[i]);
+    const float mt = max_across_quads(mx);
+    if (__any(mt > st.m + kRescaleLog2)) {
+        const float mnew = fmaxf(st.m, mt);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+        st.l *= alpha;
+        st.m = mnew;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * kq + r);
+#pragma unroll
+            for (int x = 0; x < DPL; x++) st.acc[x][r] *= ar;
+            if constexpr (KVT == NYION_KV_Q4_20B) st.acc_m[r] *= ar;
+        }
+    }
+    const float mp = KVT == NYION_KV_Q4_20B ? st.m - 5.f : st.m;
+#pragma unroll
+    for (int i = 0; i < N; i++) pr[i] = __builtin_amdgcn_exp2f(sv[i] - mp);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; i += 4) ls += (pr[i] + pr[i + 1]) + (pr[i + 2] + pr[i + 3]);
+    st.l += ls;
+}
+
+// B operands of one Q4-20B tile's P.V product for lane (col j, quad kq):
+// v/32 = (d/32) nib + dmin/32 as three exact binary16 terms: hi = (d/32) nib
+// rounded, lo = fma(d/32, nib, -hi) (exact: the product has at most 15
+// significant bits), and dmin/32, whose product with P is the same for every
+// element of the lane's column (acc_m).  d/32 and dmin/32 are exact for |d|,
+// |dmin| >= 2^-9 (below, the scaled header rounds by at most 2^-25), and
+// d/32 * 15 stays inside binary16 range.  Words hold rows (0, 1) and (2, 3):
+// hi[z], lo[z] for output dim DPL*j + z, mm the dmin/32 terms.
+template <int D>
+struct Q4VOperands {
+    uint32_t hi[D / 16][2], lo[D / 16][2], mm[2];
+};
+
+template <int D, bool MASKED>
+__device__ __forceinline__ Q4VOperands<D> q4_v_operands(const Tile<D, NYION_KV_Q4_20B>& t, uint32_t mask,
+                                                        int kq, uint32_t k6464) {
+    constexpr int DPL = D / 16;
+    Q4VOperands<D> o;
+    const halfx2 s32 = {(_Float16)0.03125f, (_Float16)0.03125f};
+    uint32_t d01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x05040100u);
+    uint32_t d23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x05040100u);
+    uint32_t m01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x07060302u);
+    uint32_t m23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x07060302u);
+    if (MASKED) {  // masked rows may hold uninitialised slots: their terms are 0
+        const uint32_t q = (mask >> (4 * kq)) & 0xfu;
+        const uint32_t k01 = ((q & 1u) ? 0xffffu : 0u) | ((q & 2u) ? 0xffff0000u : 0u);
+        const uint32_t k23 = ((q & 4u) ? 0xffffu : 0u) | ((q & 8u) ? 0xffff0000u : 0u);
+        d01 &= k01;
+        m01 &= k01;
+        d23 &= k23;
+        m23 &= k23;
+    }
+    const halfx2 dd01 = __builtin_bit_cast(halfx2, d01) * s32, dd23 = __builtin_bit_cast(halfx2, d23) * s32;
+    o.mm[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(halfx2, m01) * s32);
+    o.mm[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(halfx2, m23) * s32);
+    // byte b of the nibble words of rows 2p and 2p+1 side by side, [row 2p
+    // byte b, 0, row 2p+1 byte b, 0] (one permute per pair and byte): its low
+    // nibbles are element 2b of the two rows and its high nibbles element
+    // 2b + 1, each as binary16 1024 + e after a mask and 0x64 in the high
+    // bytes (k6464)
+    constexpr int NBY = DPL / 2;  // nibble bytes per row: 2 at head_dim 64, 4 at 128
+    const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    uint32_t pw[2][NBY];
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+        for (int b = 0; b < NBY; b++)
+            pw[p][b] = __builtin_amdgcn_perm(t.v[2 * p + 1], t.v[2 * p], 0x0c000c00u | ((4u + b) << 16) | (uint32_t)b);
+#pragma unroll
+    for (int z = 0; z < DPL; z++) {  // element z: nibble z of the lane's word
+        const int b = z >> 1;
+        const uint32_t n01 = (((z & 1) ? pw[0][b] >> 4 : pw[0][b]) & 0x000f000fu) | k6464;
+        const uint32_t n23 = (((z & 1) ? pw[1][b] >> 4 : pw[1][b]) & 0x000f000fu) | k6464;
+        const halfx2 e01 = __builtin_bit_cast(halfx2, n01) - k1024;
+        const halfx2 e23 = __builtin_bit_cast(halfx2, n23) - k1024;
+        const halfx2 h01 = dd01 * e01, h23 = dd23 * e23;
+        o.hi[z][0] = __builtin_bit_cast(uint32_t, h01);
+        o.hi[z][1] = __builtin_bit_cast(uint32_t, h23);
+        o.lo[z][0] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(dd01, e01, -h01));
+        o.lo[z][1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(dd23, e23, -h23));
+    }
+    return o;
+}
+
+// f32 and binary16 KV: one tile, scores through the online softmax to P.V.
+template <int D, int KVT, bool MASKED, bool TRACK>
+__device__ __forceinline__ void consume_tile_fh(State<D>& st, const Tile<D, KVT>& t, const float* qv,
+                                             uint32_t mask, int kq, float scale_log2, float* srow,
+                                             const int* pos) {
+    constexpr int NC = D / 4;
+    constexpr int DPL = D / 16;
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KVT == NYION_KV_F16) {
+        // binary16 K as stored against q split into binary16 high and low
+        // parts (qv words 4x, 4x+1 and 4x+2, 4x+3): the products are exact in
+        // f32, so S keeps f32 accuracy at a quarter of the f32 MFMA cycles.
+        // Call x takes words 2(x&1), +1 of K load x/2 (dims 32(x/2) + 8kq +
+        // 4(x&1) .. +3).  The words are copied to scalars first: this
+        // compiler's __builtin_bit_cast of a vector element yields the bits
+        // of element 0.
+#pragma unroll
+        for (int x = 0; x < D / 16; x++) {
+            const uint32_t k0 = t.k[x >> 1][2 * (x & 1)], k1 = t.k[x >> 1][2 * (x & 1) + 1];
+            const halfx4 kx = __builtin_bit_cast(halfx4, u32x2{k0, k1});
+            const halfx4 qh = __builtin_bit_cast(halfx4, floatx2{qv[4 * x], qv[4 * x + 1]});
+            const halfx4 ql = __builtin_bit_cast(halfx4, floatx2{qv[4 * x + 2], qv[4 * x + 3]});
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, qh, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, ql, s, 0, 0, 0);
+        }
     } else {
         float kv[NC];
         decode_k<D, KVT>(t, kv);
@@ -510,8 +644,7 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
         for (int c = 0; c < NC; c++) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c], qv[c], s, 0, 0, 0);
     }
 
-    // Q4-20B scores come out of the MFMAs scaled by 2^-24 (exact: a power of two)
-    const float sc = KVT == NYION_KV_Q4_20B ? scale_log2 * 16777216.f : scale_log2;
+    const float sc = scale_log2;
     float sv[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -541,14 +674,11 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             const float ar = __shfl(alpha, 4 * kq + r);
 #pragma unroll
             for (int x = 0; x < DPL; x++) st.acc[x][r] *= ar;
-            if constexpr (KVT == NYION_KV_Q4_20B) st.acc_m[r] *= ar;
         }
     }
-    // Q4-20B: pr = 32p (the P.V operand), l accumulated in units of 32
-    const float mp = KVT == NYION_KV_Q4_20B ? st.m - 5.f : st.m;
     float pr[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - mp);
+    for (int r = 0; r < 4; r++) pr[r] = __builtin_amdgcn_exp2f(sv[r] - st.m);
     st.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
     if constexpr (KVT == NYION_KV_F16) {
         // O += P.V on binary16 MFMAs: A = this lane's four p (tokens 4kq..+3
@@ -574,68 +704,6 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
             st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(
                 pa, __builtin_bit_cast(halfx4, u32x2{b01, b23}), st.acc[z], 0, 0, 0);
         }
-    } else if constexpr (KVT == NYION_KV_Q4_20B) {
-        // O += P.V on binary16 MFMAs: A = 32p rounded to binary16 (pr is 32p;
-        // as for binary16 KV; 32p <= 2^13), B = V/32 split into binary16 high
-        // and low parts (V dequantised exactly as dequant_block, then scaled by
-        // 2^-5, which is exact and keeps d*15 + dmin <= 2^20 inside binary16
-        // range)
-        const halfx4 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
-        // v/32 = (d/32) nib + dmin/32 as three exact binary16 terms: hi =
-        // (d/32) nib rounded, lo = fma(d/32, nib, -hi) (exact: the product has
-        // at most 15 significant bits), and dmin/32, whose product with P is
-        // the same for every element of the lane's column and is accumulated
-        // once per tile (acc_m).  d/32 and dmin/32 are exact for |d|, |dmin|
-        // >= 2^-9 (below, the scaled header rounds by at most 2^-25), and
-        // d/32 * 15 stays inside binary16 range.  Pairs of rows (0, 1) and
-        // (2, 3) share one packed operation.
-        const halfx2 s32 = {(_Float16)0.03125f, (_Float16)0.03125f};
-        uint32_t d01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x05040100u);
-        uint32_t d23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x05040100u);
-        uint32_t m01 = __builtin_amdgcn_perm(t.vhdr[1], t.vhdr[0], 0x07060302u);
-        uint32_t m23 = __builtin_amdgcn_perm(t.vhdr[3], t.vhdr[2], 0x07060302u);
-        if (MASKED) {  // masked rows may hold uninitialised slots: their terms are 0
-            const uint32_t q = (mask >> (4 * kq)) & 0xfu;
-            const uint32_t k01 = ((q & 1u) ? 0xffffu : 0u) | ((q & 2u) ? 0xffff0000u : 0u);
-            const uint32_t k23 = ((q & 4u) ? 0xffffu : 0u) | ((q & 8u) ? 0xffff0000u : 0u);
-            d01 &= k01;
-            m01 &= k01;
-            d23 &= k23;
-            m23 &= k23;
-        }
-        const halfx2 dd01 = __builtin_bit_cast(halfx2, d01) * s32, dd23 = __builtin_bit_cast(halfx2, d23) * s32;
-        const halfx2 mm01 = __builtin_bit_cast(halfx2, m01) * s32, mm23 = __builtin_bit_cast(halfx2, m23) * s32;
-        st.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{mm01[0], mm01[1], mm23[0], mm23[1]},
-                                                         st.acc_m, 0, 0, 0);
-        // byte b of the nibble words of rows 2p and 2p+1 side by side, [row
-        // 2p byte b, 0, row 2p+1 byte b, 0] (one permute per pair and byte):
-        // its low nibbles are element 2b of the two rows and its high nibbles
-        // element 2b + 1, each as binary16 1024 + e after a mask and 0x64 in
-        // the high bytes
-        constexpr int NBY = DPL / 2;  // nibble bytes per row: 2 at head_dim 64, 4 at 128
-        const halfx2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        uint32_t pw[2][NBY];
-#pragma unroll
-        for (int p = 0; p < 2; p++)
-#pragma unroll
-            for (int b = 0; b < NBY; b++)
-                pw[p][b] = __builtin_amdgcn_perm(t.v[2 * p + 1], t.v[2 * p],
-                                                 0x0c000c00u | ((4u + b) << 16) | (uint32_t)b);
-#pragma unroll
-        for (int z = 0; z < DPL; z++) {  // element z: nibble z of the lane's word
-            const int b = z >> 1;
-            const uint32_t n01 = (((z & 1) ? pw[0][b] >> 4 : pw[0][b]) & 0x000f000fu) | st.k6464;
-            const uint32_t n23 = (((z & 1) ? pw[1][b] >> 4 : pw[1][b]) & 0x000f000fu) | st.k6464;
-            const halfx2 e01 = __builtin_bit_cast(halfx2, n01) - k1024;
-            const halfx2 e23 = __builtin_bit_cast(halfx2, n23) - k1024;
-            const halfx2 h01 = dd01 * e01, h23 = dd23 * e23;
-            const halfx2 l01 = __builtin_elementwise_fma(dd01, e01, -h01);
-            const halfx2 l23 = __builtin_elementwise_fma(dd23, e23, -h23);
-            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{h01[0], h01[1], h23[0], h23[1]},
-                                                              st.acc[z], 0, 0, 0);
-            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, halfx4{l01[0], l01[1], l23[0], l23[1]},
-                                                              st.acc[z], 0, 0, 0);
-        }
     } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -653,6 +721,38 @@ __device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t
     }
 }
 
+// One tile: bit i of `mask` (wave-uniform) marks row i of the 16 valid;
+// MASKED = false is the all-valid fast path.  TRACK: also store the scaled
+// scores of this lane's head (rows 4kq+r, at positions pos[r]) into srow.
+template <int D, int KVT, bool MASKED, bool TRACK>
+__device__ __forceinline__ void consume_tile(State<D>& st, const Tile<D, KVT>& t, const float* qv,
+                                             uint32_t mask, int kq, float scale_log2, float* srow,
+                                             const int* pos, const uint32_t (*khr)[4]) {
+    constexpr int DPL = D / 16;
+    if constexpr (KVT != NYION_KV_Q4_20B) {
+        consume_tile_fh<D, KVT, MASKED, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos);
+    } else {
+        float sv[4], pr[4];
+        tile_logits<KVT, MASKED, TRACK>(q4_tile_scores<D>(t, qv, kq, khr), scale_log2, mask, kq, srow, pos, sv);
+        softmax_step<D, KVT, 4>(st, sv, kq, pr);
+        // O += P.V on binary16 MFMAs: A = 32p rounded to binary16 (pr is 32p;
+        // as for binary16 KV; 32p <= 2^13), B = V/32 as q4_v_operands (V
+        // dequantised exactly as dequant_block, then scaled by 2^-5, which is
+        // exact and keeps d*15 + dmin <= 2^20 inside binary16 range)
+        const halfx4 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3]};
+        const Q4VOperands<D> o = q4_v_operands<D, MASKED>(t, mask, kq, st.k6464);
+        st.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(halfx4, u32x2{o.mm[0], o.mm[1]}),
+                                                         st.acc_m, 0, 0, 0);
+#pragma unroll
+        for (int z = 0; z < DPL; z++) {
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                pa, __builtin_bit_cast(halfx4, u32x2{o.hi[z][0], o.hi[z][1]}), st.acc[z], 0, 0, 0);
+            st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                pa, __builtin_bit_cast(halfx4, u32x2{o.lo[z][0], o.lo[z][1]}), st.acc[z], 0, 0, 0);
+        }
+    }
+}
+
 template <int D, int KVT, bool TRACK>
 __device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, const float* qv,
                                         uint32_t mask, int kq, float scale_log2, float* srow,
@@ -661,6 +761,40 @@ __device__ __forceinline__ void consume(State<D>& st, const Tile<D, KVT>& t, con
         consume_tile<D, KVT, false, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos, khr);
     else if (mask)
         consume_tile<D, KVT, true, TRACK>(st, t, qv, mask, kq, scale_log2, srow, pos, khr);
+}
+
+// Two consecutive Q4-20B tiles as one 32-token step: one max reduction and
+// rescale check, and P.V on 16x16x32 MFMAs whose eight values per lane are
+// the lane's four rows of tile a then of tile b (the same order for P and
+// V).  Masks as consume_tile (a tile past the walk has mask 0).
+template <int D, bool MASKED, bool TRACK>
+__device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, NYION_KV_Q4_20B>& ta,
+                                                   const Tile<D, NYION_KV_Q4_20B>& tb, const float* qv,
+                                                   uint32_t ma, uint32_t mb, int kq, float scale_log2,
+                                                   float* srow, const int* pa_pos, const int* pb_pos,
+                                                   const uint32_t (*khra)[4], const uint32_t (*khrb)[4]) {
+    constexpr int KVT = NYION_KV_Q4_20B;
+    constexpr int DPL = D / 16;
+    float sv[8], pr[8];
+    tile_logits<KVT, MASKED, TRACK>(q4_tile_scores<D>(ta, qv, kq, khra), scale_log2, ma, kq, srow, pa_pos, sv);
+    tile_logits<KVT, MASKED, TRACK>(q4_tile_scores<D>(tb, qv, kq, khrb), scale_log2, mb, kq, srow, pb_pos,
+                                    sv + 4);
+    softmax_step<D, KVT, 8>(st, sv, kq, pr);
+    const halfx8 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3],
+                       (_Float16)pr[4], (_Float16)pr[5], (_Float16)pr[6], (_Float16)pr[7]};
+    const Q4VOperands<D> oa = q4_v_operands<D, MASKED>(ta, ma, kq, st.k6464);
+    const Q4VOperands<D> ob = q4_v_operands<D, MASKED>(tb, mb, kq, st.k6464);
+    st.acc_m = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        pa, __builtin_bit_cast(halfx8, u32x4{oa.mm[0], oa.mm[1], ob.mm[0], ob.mm[1]}), st.acc_m, 0, 0, 0);
+#pragma unroll
+    for (int z = 0; z < DPL; z++) {
+        st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            pa, __builtin_bit_cast(halfx8, u32x4{oa.hi[z][0], oa.hi[z][1], ob.hi[z][0], ob.hi[z][1]}), st.acc[z],
+            0, 0, 0);
+        st.acc[z] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            pa, __builtin_bit_cast(halfx8, u32x4{oa.lo[z][0], oa.lo[z][1], ob.lo[z][0], ob.lo[z][1]}), st.acc[z],
+            0, 0, 0);
+    }
 }
 
 // A Q4-20B tile of a contiguous walk (aligned blocks of >= 16 tokens, zone
@@ -900,7 +1034,11 @@ template <int D, int KVT, bool TRACK, typename Offsets, bool CONTIG = false>
 __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, const float* qv, int n,
                                            int j, int kq, float* srow, Offsets offsets) {
     constexpr bool SPAN = CONTIG && span_tiles<D, KVT>();
+    // untracked span tiles go in pairs (the tracked form's score positions
+    // leave no registers for the second staged tile)
+    constexpr bool PAIRS = SPAN && !TRACK;
     constexpr int NB = tile_ring<D, KVT, SPAN>();
+    static_assert(!PAIRS || NB % 2 == 0, "pairs take slots 2i, 2i+1");
     using RingTile = typename std::conditional<SPAN, SpanTile<D>, Tile<D, KVT>>::type;
     RingTile t[NB];
     uint32_t msk[NB];
@@ -923,9 +1061,32 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
 #pragma unroll
         for (int k = 0; k < NB; k++) {
             const int s = (k + NB - 1) % NB;  // the slot consumed NB - 1 steps from now
-            msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
-            load(t[s]);
-            if ((k == 0 || i + k < n) && msk[k]) {
+            if constexpr (!PAIRS) {
+                msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
+                load(t[s]);
+            }
+            if constexpr (PAIRS) {
+                // span tiles go in pairs (32-token steps): slots k-1 and k, at
+                // odd k, before this step's load refills slot k-1
+                if (k & 1) {
+                    const uint32_t ma = i + k - 1 < n ? msk[k - 1] : 0u;
+                    const uint32_t mb = i + k < n ? msk[k] : 0u;
+                    if (ma | mb) {
+                        Tile<D, KVT> ya, yb;
+                        uint32_t khra[D / 32][4], khrb[D / 32][4];
+                        stage_span<D>(t[k - 1], ya, khra, j, kq);
+                        stage_span<D>(t[k], yb, khrb, j, kq);
+                        if ((ma & mb) == 0xffffu)
+                            consume_pair_tiles<D, false, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow,
+                                                                pos[k - 1], pos[k], khra, khrb);
+                        else
+                            consume_pair_tiles<D, true, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow,
+                                                               pos[k - 1], pos[k], khra, khrb);
+                    }
+                }
+                msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
+                load(t[s]);
+            } else if ((k == 0 || i + k < n) && msk[k]) {
                 if constexpr (SPAN) {
                     Tile<D, KVT> y;
                     uint32_t khr[D / 32][4];
