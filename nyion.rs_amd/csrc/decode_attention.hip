@@ -823,20 +823,20 @@ __device__ __forceinline__ void load_span(SpanTile<D>& t, const void* kb, const 
     }
 }
 
-// Operands of a span tile: the chunks go to a per-wavefront LDS slot (rows at
-// TS-byte strides, K then V), from which each lane reads the words the tile
-// layout gives it (Tile<D, Q4-20B>: K row j's nibble words, V rows 4kq+r's
-// header and nibbles) and the K headers of rows 4kq+r (khr[g][r]).  The
-// wavefront's LDS operations complete in order: the next tile's writes come
-// after these reads.
+// Operands of a span tile: the chunks go to one of the wavefront's two LDS
+// slots (rows at TS-byte strides, K then V), from which each lane reads the
+// words the tile layout gives it (Tile<D, Q4-20B>: K row j's nibble words, V
+// rows 4kq+r's header and nibbles) and the K headers of rows 4kq+r
+// (khr[g][r]).  The wavefront's LDS operations complete in order: a later
+// tile's writes to the slot come after these reads.
 template <int D>
 __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_KV_Q4_20B>& t,
-                                           uint32_t (*khr)[4], int j, int kq) {
+                                           uint32_t (*khr)[4], int j, int kq, int slot = 0) {
     constexpr int TS = SpanTile<D>::TS, KC = SpanTile<D>::KC, DPL = D / 16;
-    __shared__ u32x4 sm_span[4][2][KC * 64];
+    __shared__ u32x4 sm_span[4][2][2][KC * 64];
     const int lane = threadIdx.x & 63;
-    u32x4* ks = sm_span[threadIdx.x >> 6][0];
-    u32x4* vs = sm_span[threadIdx.x >> 6][1];
+    u32x4* ks = sm_span[threadIdx.x >> 6][slot][0];
+    u32x4* vs = sm_span[threadIdx.x >> 6][slot][1];
 #pragma unroll
     for (int c = 0; c < KC; c++) {
         ks[lane + 64 * c] = sp.k[c];
@@ -1074,8 +1074,8 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
                     if (ma | mb) {
                         Tile<D, KVT> ya, yb;
                         uint32_t khra[D / 32][4], khrb[D / 32][4];
-                        stage_span<D>(t[k - 1], ya, khra, j, kq);
-                        stage_span<D>(t[k], yb, khrb, j, kq);
+                        stage_span<D>(t[k - 1], ya, khra, j, kq, 0);
+                        stage_span<D>(t[k], yb, khrb, j, kq, 1);
                         if ((ma & mb) == 0xffffu)
                             consume_pair_tiles<D, false, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow,
                                                                 pos[k - 1], pos[k], khra, khrb);
