@@ -864,17 +864,18 @@ __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_
 }
 
 // Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
-// one block; valid rows [vlo, vhi].  ZONE: the blocks are 32-token units of
-// zone pages (every zone page is a whole number of them, and a unit's rows
-// of one (layer, kv head) are consecutive); lane l holds the offset of row
-// (layer, kv head 0) of unit bi_first + l, low word in tblv, high in tblh
-// (-1: page absent).
+// one block; valid rows [vlo, vhi].  Lane l holds a 64-bit row offset, low
+// word in tblv, high in tblh (-1: no rows): paged blocks, the first row of
+// this kv head in the block of block index bi_first + l; ZONE, the blocks
+// are 32-token units of zone pages (every zone page is a whole number of
+// them, and a unit's rows of one (layer, kv head) are consecutive), the
+// offset of row (layer, kv head 0) of unit bi_first + l.
 struct AlignedWalk {
     int base;        // lo & ~15
     int lo, hi;
     int bi_first;    // first block index of this wavefront's tiles
-    int tblv;        // lane l: block id of block index bi_first + l (or -1)
-    int tblh;        // ZONE: high word of the lane's row offset
+    int tblv;        // lane l: low word of the row offset
+    int tblh;        // lane l: high word of the row offset
     int kvh;         // ZONE: the kv head
     long long head_off;
 };
@@ -888,9 +889,12 @@ __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const A
     const int t0 = w.base + 16 * tile;
 #pragma unroll
     for (int r = 0; r < 4; r++) pos[r] = t0 + 4 * kq + r;
-    const int vlo = max(w.lo - t0, 0);
-    const int vhi = min(w.hi - t0, 15);
-    uint32_t mask = (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
+    uint32_t mask = 0xffffu;  // interior tiles: all valid
+    if (__builtin_expect(t0 < w.lo || t0 + 15 > w.hi, 0)) {
+        const int vlo = max(w.lo - t0, 0);
+        const int vhi = min(w.hi - t0, 15);
+        mask = (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
+    }
     // rows of a paged pool are contiguous: the token stride is the row size
     constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
     long long base;
@@ -905,14 +909,15 @@ __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const A
             mask = 0;   // least 32), and the tile is masked
         }
     } else {
-        int blk = 0;
-        if (a.tables) blk = __builtin_amdgcn_readlane(w.tblv, (t0 >> a.bt_log2) - w.bi_first);
-        if (blk < 0) {  // block index past the table or block id out of range
-            blk = 0;
+        // the block's first row of this kv head, precomputed per run
+        const int idx = (t0 >> a.bt_log2) - w.bi_first;
+        const long long row = ((long long)__builtin_amdgcn_readlane(w.tblh, idx) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane(w.tblv, idx);
+        base = row + (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
+        if (row < 0) {  // block index past the table or block id out of range
+            base = 0;
             mask = 0;
         }
-        base = (long long)blk * a.block_stride + w.head_off +
-               (long long)(t0 & ((1 << a.bt_log2) - 1)) * TS;
     }
     koff = base + j * TS;
     const long long vbase = base + 4 * kq * TS;
@@ -1253,8 +1258,15 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
             const long long row = u <= u_last ? zone_row_offset(*zone, u << kZoneUnitLog2, 0, TS) : -1;
             w.tblv = (int)(uint32_t)row;
             w.tblh = (int)(row >> 32);
-        } else if (table) {
-            w.tblv = (have_pref && c0 == 0) ? tbl_pref : run_table_entry(a, table, w.base, f, nc, lane);
+        } else {
+            // lane l: the first row of this kv head in the block of block index
+            // bi_first + l (-1: past the table or an invalid block id)
+            const int blk = !table ? 0
+                            : (have_pref && c0 == 0) ? tbl_pref
+                                                     : run_table_entry(a, table, w.base, f, nc, lane);
+            const long long row = blk < 0 ? -1 : (long long)blk * a.block_stride + head_off;
+            w.tblv = (int)(uint32_t)row;
+            w.tblh = (int)(row >> 32);
         }
         // span tiles take the tile's first row (row 0 for every lane: a
         // wave-uniform offset)
