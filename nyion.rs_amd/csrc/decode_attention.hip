@@ -1062,43 +1062,67 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
         msk[k] = offsets(min(k, n - 1), ko, vo, pos[k]);
         load(t[k]);
     }
-    for (int i = 0; i < n; i += NB) {
+    if constexpr (PAIRS) {
+        // span tiles go in pairs (32-token steps): slots k-1 and k at odd k,
+        // before that step's load refills slot k-1
+        auto eat_pair = [&](const RingTile& x, const RingTile& y, uint32_t ma, uint32_t mb, const int* pa,
+                            const int* pb) {
+            Tile<D, KVT> ya, yb;
+            uint32_t khra[D / 32][4], khrb[D / 32][4];
+            stage_span<D>(x, ya, khra, j, kq, 0);
+            stage_span<D>(y, yb, khrb, j, kq, 1);
+            if ((ma & mb) == 0xffffu)
+                consume_pair_tiles<D, false, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow, pa, pb, khra,
+                                                    khrb);
+            else
+                consume_pair_tiles<D, true, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow, pa, pb, khra,
+                                                   khrb);
+        };
+        // whole ring iterations, every tile within the walk: a pair with no
+        // valid row (absent blocks) takes the masked path rather than a
+        // branch around it, which would make the compiler copy the running
+        // state on every pair; its scores are -1e30 and its V rows zero, so
+        // it adds nothing once the running max is finite, and a wavefront
+        // that has seen no valid row yet is left with m = -1e30 and a
+        // nonzero l, which the first valid tile multiplies away exactly
+        // (alpha = exp2(-1e30 - m) = 0) and which otherwise yields the same
+        // zero output as an empty walk
+        int i = 0;
+        for (; i + NB <= n; i += NB) {
 #pragma unroll
-        for (int k = 0; k < NB; k++) {
-            const int s = (k + NB - 1) % NB;  // the slot consumed NB - 1 steps from now
-            if constexpr (!PAIRS) {
+            for (int k = 0; k < NB; k++) {
+                const int s = (k + NB - 1) % NB;
+                if (k & 1) eat_pair(t[k - 1], t[k], msk[k - 1], msk[k], pos[k - 1], pos[k]);
                 msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
                 load(t[s]);
             }
-            if constexpr (PAIRS) {
-                // span tiles go in pairs (32-token steps): slots k-1 and k, at
-                // odd k, before this step's load refills slot k-1
-                if (k & 1) {
-                    const uint32_t ma = i + k - 1 < n ? msk[k - 1] : 0u;
-                    const uint32_t mb = i + k < n ? msk[k] : 0u;
-                    if (ma | mb) {
-                        Tile<D, KVT> ya, yb;
-                        uint32_t khra[D / 32][4], khrb[D / 32][4];
-                        stage_span<D>(t[k - 1], ya, khra, j, kq, 0);
-                        stage_span<D>(t[k], yb, khrb, j, kq, 1);
-                        if ((ma & mb) == 0xffffu)
-                            consume_pair_tiles<D, false, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow,
-                                                                pos[k - 1], pos[k], khra, khrb);
-                        else
-                            consume_pair_tiles<D, true, TRACK>(st, ya, yb, qv, ma, mb, kq, a.scale_log2, srow,
-                                                               pos[k - 1], pos[k], khra, khrb);
-                    }
-                }
+        }
+        // the last, partial iteration: its tiles are in slots 0 .. n-i-1,
+        // loaded by the steps before; no further loads
+        if (i < n) {
+#pragma unroll
+            for (int k = 1; k < NB; k += 2) {
+                const uint32_t ma = i + k - 1 < n ? msk[k - 1] : 0u;
+                const uint32_t mb = i + k < n ? msk[k] : 0u;
+                if (ma | mb) eat_pair(t[k - 1], t[k], ma, mb, pos[k - 1], pos[k]);
+            }
+        }
+    } else {
+        for (int i = 0; i < n; i += NB) {
+#pragma unroll
+            for (int k = 0; k < NB; k++) {
+                const int s = (k + NB - 1) % NB;  // the slot consumed NB - 1 steps from now
                 msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
                 load(t[s]);
-            } else if ((k == 0 || i + k < n) && msk[k]) {
-                if constexpr (SPAN) {
-                    Tile<D, KVT> y;
-                    uint32_t khr[D / 32][4];
-                    stage_span<D>(t[k], y, khr, j, kq);
-                    consume<D, KVT, TRACK>(st, y, qv, msk[k], kq, a.scale_log2, srow, pos[k], khr);
-                } else {
-                    consume<D, KVT, TRACK>(st, t[k], qv, msk[k], kq, a.scale_log2, srow, pos[k]);
+                if ((k == 0 || i + k < n) && msk[k]) {
+                    if constexpr (SPAN) {
+                        Tile<D, KVT> y;
+                        uint32_t khr[D / 32][4];
+                        stage_span<D>(t[k], y, khr, j, kq);
+                        consume<D, KVT, TRACK>(st, y, qv, msk[k], kq, a.scale_log2, srow, pos[k], khr);
+                    } else {
+                        consume<D, KVT, TRACK>(st, t[k], qv, msk[k], kq, a.scale_log2, srow, pos[k]);
+                    }
                 }
             }
         }
@@ -1659,9 +1683,14 @@ void decode_kernel(DecodeArgs a) {
                 mh[r] = M;
                 lh[r] = L;
             }
+            // span walks: the store offsets are formed here, from a copy of kq
+            // the compiler cannot see through; hoisted out of the piece loop
+            // they would be held across the walk, where registers are short
+            int kqs = kq;
+            if constexpr (span_tiles<D, KVT>()) asm volatile("" : "+v"(kqs));
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int hh = 4 * kq + r;
+                const int hh = 4 * kqs + r;
                 if (hh >= g_local) continue;
                 if (TRACK && whole && j == 0) {  // final (m, l) of the head: row end
                     float* sr = a.scores + ((long long)b * a.n_heads + head0 + hh) * a.scores_stride;
