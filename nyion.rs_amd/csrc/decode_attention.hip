@@ -1516,6 +1516,22 @@ void decode_kernel(DecodeArgs a) {
             e = extent_of<ALIGNED>(a, int2{len, qp});
             wa = min(wa0, e.tiles);
             wb = min(wb0, e.tiles);
+            if (KVT == NYION_KV_Q4_20B && ALIGNED && e.n_glob > 0 && e.main_tiles > t0 &&
+                e.main_tiles < t0 + cd) {
+                // no wavefront walks both sides of the boundary between the
+                // contiguous tiles and the globals (two serial chains of round
+                // trips): the piece's inner wave boundary nearest to it moves
+                // onto it when its neighbours enclose it; the piece's tiles
+                // are the same, two wavefronts trade a few.  4-bit kernels
+                // only: in the f32 and binary16 ones the extra scalar state
+                // spills scalar registers inside the walk loops.
+                const int mt = e.main_tiles;
+                const int kb = min(3, max(1, (8 * (mt - t0) + cd) / (2 * cd)));
+                if (t0 + ((kb - 1) * cd) / 4 <= mt && mt <= t0 + ((kb + 1) * cd) / 4) {
+                    if (wave == kb - 1) wb = mt;
+                    if (wave == kb) wa = mt;
+                }
+            }
             whole = P == 1;
             pieces = P;
             slot = (int)blockIdx.x;
@@ -1902,6 +1918,26 @@ static int wg_tiles_for(long long total_tiles) {
 // segments the stream-K prologue (lengths, prefix sums, a search) is a
 // dependent round trip and two barriers that the direct form skips.
 constexpr int kDirectMaxSegments = 64;
+// Direct partition of small tiles (4-bit rows, binary16 at head_dim 64): the
+// tiles per workgroup double while a workgroup's K+V bytes stay within
+// kDirectWgBytes and the launch keeps kDirectMinGrid workgroups.  Such a
+// launch's time is the chain of round trips of its pieces (rows, partial
+// stores and their acknowledgement, the arrival atomic, the merge's
+// reloads), not their walks, and fewer pieces publish and re-read fewer
+// partials.  The tuning override, when set, is used as it is.
+constexpr long long kDirectWgBytes = 96 << 10;
+constexpr long long kDirectMinGrid = 128;
+
+template <int D, int KVT>
+static int direct_wg_tiles(int wg, int seg_tiles, long long segs) {
+    if (g_wg_tiles_override.load(std::memory_order_relaxed) > 0) return wg;
+    constexpr long long tile_bytes =
+        32LL * (KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : KVT == NYION_KV_F16 ? 2 * D : 4 * D);
+    while (2 * wg * tile_bytes <= kDirectWgBytes && 2 * wg <= seg_tiles &&
+           (seg_tiles + 2LL * wg - 1) / (2LL * wg) * segs >= kDirectMinGrid)
+        wg *= 2;
+    return wg;
+}
 
 template <int D, int KVT, bool AL, bool TR, bool ZN = false>
 static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
@@ -1931,7 +1967,8 @@ static void launch_dk(const DecodePlan& pl, hipStream_t stream) {
             // pieces per segment from the tiles per workgroup, within the
             // partial slots the workspace holds (one per workgroup)
             const int seg_tiles = a.mode == MODE_FULL ? (a.max_len + 15) / 16 : pl.tiles_max;
-            long long P = pl.ws_bytes == 0 ? 1 : (seg_tiles + wg - 1) / wg;
+            const int wgd = direct_wg_tiles<D, KVT>(wg, seg_tiles, segs);
+            long long P = pl.ws_bytes == 0 ? 1 : (seg_tiles + wgd - 1) / wgd;
             const long long limit = std::min<long long>(cap, pl.grid_bound);
             if (P * segs > limit) P = std::max<long long>(1, limit / segs);
             if (P > 1 || pl.ws_bytes == 0 || nb == 1) {

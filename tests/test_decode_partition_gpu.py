@@ -1,0 +1,54 @@
+"""Window-mode decode with strided globals over the direct partition (gpu).
+
+ops::attention_sparse (swamp-engine/src/ops.rs:85-168) over a few
+sequences: each (sequence, kv head) segment is cut into pieces of a fixed
+number of tiles, four wavefronts to a piece, the window's contiguous tiles
+first and the globals' gathered tiles after them.  The windows, lengths and
+partition sizes below put the boundary between the two inside a piece at
+every offset a wavefront split can take, so the piece's wave ranges are
+re-cut there; the default partition (0) sizes pieces by the bytes of the KV
+format.  Every KV format and head size against the oracle, tolerance as for
+every attention output: max-abs-err <= 2e-3 and max|diff| / max|ref| <= 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import workloads as W
+from test_decode_gpu import assert_close
+
+pytestmark = pytest.mark.gpu
+
+CTX = [3000, 2531, 1777, 2222]
+PARTITIONS = [64, 128, 256, 512, 1024, 0]
+
+
+def to_dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def decode(gpu, pb, window, stride):
+    out = torch.full((pb.batch, pb.n_heads, pb.head_dim), float("nan"), device="cuda")
+    gpu.paged_decode(to_dev(pb.q), to_dev(pb.k_pool), to_dev(pb.v_pool), to_dev(pb.tables),
+                     to_dev(pb.ctx_lens), out, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                     pb.block_tokens, kv_dtype=pb.kv_dtype, window=window, global_stride=stride,
+                     max_ctx=int(pb.ctx_lens.max()))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_F16, oracle.KV_Q4], ids=["f32", "f16", "q4"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_window_globals_direct_partitions(gpu, kv_dtype, head_dim):
+    pb = W.paged_batch(CTX, n_heads=16, n_kv_heads=4, head_dim=head_dim, block_tokens=16,
+                       seed=head_dim + kv_dtype, kv_dtype=kv_dtype)
+    for window, stride in ((300, 16), (1000, 16), (1500, 7)):
+        ref = W.reference_decode(pb, window=window, global_stride=stride)
+        for p in PARTITIONS:
+            try:
+                gpu.set_partition_tokens(p)
+                got = decode(gpu, pb, window, stride)
+            finally:
+                gpu.set_partition_tokens(0)
+            assert_close(got, ref, f"window {window} stride {stride} partition {p}")
