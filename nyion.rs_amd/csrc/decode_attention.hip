@@ -873,32 +873,48 @@ __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_
 struct AlignedWalk {
     int base;        // lo & ~15
     int lo, hi;
-    int bi_first;    // first block index of this wavefront's tiles
-    int tblv;        // lane l: low word of the row offset
-    int tblh;        // lane l: high word of the row offset
+    int f;           // the run's first tile (tile t starts at base + 16 t)
+    int ia, nint;    // tile tables: run tiles ia .. ia + nint - 1 are interior
+                     // (16 valid rows, block present); 0 if any is absent
+    int bi_first;    // block tables: the run's first block index (ZONE: unit)
+    int tblv;        // lane l: low word of the row offset of run tile l (tile
+    int tblh;        // tables) or of block bi_first + l; high word
     int kvh;         // ZONE: the kv head
     long long head_off;
 };
 
 constexpr int kZoneUnitLog2 = 5;  // zone walks: 32-token units
 
+// Paged walks of 4-bit rows keep a lane table of tile row offsets (lane l:
+// run tile l), so a tile's offset is one lane read and an interior tile's
+// mask an index compare; f32 and binary16 walks keep a table of block row
+// offsets (lane l: block bi_first + l), whose per-tile arithmetic is
+// scalar work their tiles amortise (a tile table ran the f32 head_dim-64
+// layer 1.5 % slower).
+template <int KVT, bool ZONE>
+constexpr bool tile_table() {
+    return KVT == NYION_KV_Q4_20B && !ZONE;
+}
+
+// Offsets of run tile i (i < 64, wave-uniform) of an aligned walk.
 template <int D, int KVT, bool ZONE = false>
 __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const AlignedWalk& w,
-                                                    int tile, int j, int kq, long long& koff,
+                                                    int i, int j, int kq, long long& koff,
                                                     long long* voff, int* pos) {
-    const int t0 = w.base + 16 * tile;
+    const int t0 = w.base + 16 * (w.f + i);
 #pragma unroll
     for (int r = 0; r < 4; r++) pos[r] = t0 + 4 * kq + r;
-    uint32_t mask = 0xffffu;  // interior tiles: all valid
-    if (__builtin_expect(t0 < w.lo || t0 + 15 > w.hi, 0)) {
+    auto edge_mask = [&]() -> uint32_t {
         const int vlo = max(w.lo - t0, 0);
         const int vhi = min(w.hi - t0, 15);
-        mask = (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
-    }
+        return (vhi >= vlo) ? (((2u << vhi) - 1u) & ~((1u << vlo) - 1u)) : 0u;
+    };
     // rows of a paged pool are contiguous: the token stride is the row size
     constexpr int TS = KVT == NYION_KV_Q4_20B ? q4_row_bytes(D) : D;
+    uint32_t mask = 0xffffu;  // interior tiles: all valid
     long long base;
     if constexpr (ZONE) {
+        if (__builtin_expect(t0 < w.lo || t0 + 15 > w.hi, 0)) mask = edge_mask();
         const int idx = (t0 >> kZoneUnitLog2) - w.bi_first;
         const long long row = ((long long)__builtin_amdgcn_readlane(w.tblh, idx) << 32) |
                               (uint32_t)__builtin_amdgcn_readlane(w.tblv, idx);
@@ -908,7 +924,20 @@ __device__ __forceinline__ uint32_t aligned_offsets(const DecodeArgs& a, const A
             base = 0;   // loads read the pool's first rows (the host keeps at
             mask = 0;   // least 32), and the tile is masked
         }
+    } else if constexpr (tile_table<KVT, ZONE>()) {
+        // the tile's first row in this kv head, precomputed per run; the
+        // edge tiles and runs with an absent block take the full test
+        base = ((long long)__builtin_amdgcn_readlane(w.tblh, i) << 32) |
+               (uint32_t)__builtin_amdgcn_readlane(w.tblv, i);
+        if (__builtin_expect((unsigned)(i - w.ia) >= (unsigned)w.nint, 0)) {
+            mask = edge_mask();
+            if (base < 0) {  // block index past the table or block id out of range
+                base = 0;
+                mask = 0;
+            }
+        }
     } else {
+        if (__builtin_expect(t0 < w.lo || t0 + 15 > w.hi, 0)) mask = edge_mask();
         // the block's first row of this kv head, precomputed per run
         const int idx = (t0 >> a.bt_log2) - w.bi_first;
         const long long row = ((long long)__builtin_amdgcn_readlane(w.tblh, idx) << 32) |
@@ -1236,17 +1265,18 @@ __device__ void merge_segment(const float* acc0, const float2* ml0, int np, int 
 // ---------------------------------------------------------------- kernel
 
 // Main tiles [first, first + n) of one segment on the aligned path, in runs of
-// at most 64 tiles: lane l holds the block id of the run's l-th block index
-// (with blocks of >= 16 tokens a run of 64 tiles spans at most 64 blocks).
-// Lane l's block id of block index bi_first + l, for the run of tiles
-// [f, f + nc) from position base (-1 past the run, past the table or out of
+// at most 64 tiles (blocks of >= 16 tokens: a tile lies in one block, and a
+// run spans at most 64 blocks).  Lane l's block id for the run [f, f + nc)
+// from position base: TILES, that of the block holding run tile l; else that
+// of the run's l-th block (-1 past the run, past the table or out of
 // [0, num_blocks)).
+template <bool TILES>
 __device__ __forceinline__ int run_table_entry(const DecodeArgs& a, const int32_t* table, int base,
                                                int f, int nc, int lane) {
-    const int bi = ((base + 16 * f) >> a.bt_log2) + lane;
-    const int bi_last = (base + 16 * (f + nc) - 1) >> a.bt_log2;
+    const int bi = TILES ? (base + 16 * (f + lane)) >> a.bt_log2 : ((base + 16 * f) >> a.bt_log2) + lane;
+    const bool in_run = TILES ? lane < nc : bi <= (base + 16 * (f + nc) - 1) >> a.bt_log2;
     int blk = -1;
-    if (bi <= bi_last && bi < a.table_stride) {
+    if (in_run && bi < a.table_stride) {
         blk = table[bi];
         if ((unsigned)blk >= (unsigned)a.num_blocks) blk = -1;
     }
@@ -1267,7 +1297,8 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         w.lo = e.lo;
         w.hi = e.hi;
         w.head_off = head_off;
-        w.bi_first = (w.base + 16 * f) >> a.bt_log2;
+        w.f = f;
+        w.bi_first = (w.base + 16 * f) >> a.bt_log2;  // zone walks: 32-token units
         w.tblv = 0;
         // the first run's entries may have been loaded ahead (a superset of
         // the run from the same first block index: entries past the run are
@@ -1282,12 +1313,31 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
             const long long row = u <= u_last ? zone_row_offset(*zone, u << kZoneUnitLog2, 0, TS) : -1;
             w.tblv = (int)(uint32_t)row;
             w.tblh = (int)(row >> 32);
+        } else if constexpr (tile_table<KVT, ZONE>()) {
+            // lane l: the first row of run tile l in this kv head (-1: past
+            // the table or an invalid block id)
+            constexpr int TS = q4_row_bytes(D);
+            const int blk = !table ? 0
+                            : (have_pref && c0 == 0) ? tbl_pref
+                                                     : run_table_entry<true>(a, table, w.base, f, nc, lane);
+            const int t = w.base + 16 * (f + lane);
+            const long long row =
+                blk < 0 ? -1
+                        : (long long)blk * a.block_stride + head_off + (long long)(t & ((1 << a.bt_log2) - 1)) * TS;
+            w.tblv = (int)(uint32_t)row;
+            w.tblh = (int)(row >> 32);
+            // interior tiles: from base + 16 t >= lo to base + 16 t + 15 <= hi
+            const int ta = (e.lo & 15) != 0;
+            const int tb = (e.hi - w.base + 1) >> 4;
+            const bool absent = __ballot(lane < nc && blk < 0) != 0;
+            w.ia = ta - f;
+            w.nint = absent ? 0 : max(tb - ta, 0);
         } else {
             // lane l: the first row of this kv head in the block of block index
             // bi_first + l (-1: past the table or an invalid block id)
             const int blk = !table ? 0
                             : (have_pref && c0 == 0) ? tbl_pref
-                                                     : run_table_entry(a, table, w.base, f, nc, lane);
+                                                     : run_table_entry<false>(a, table, w.base, f, nc, lane);
             const long long row = blk < 0 ? -1 : (long long)blk * a.block_stride + head_off;
             w.tblv = (int)(uint32_t)row;
             w.tblh = (int)(row >> 32);
@@ -1296,7 +1346,7 @@ __device__ __forceinline__ void walk_main(State<D>& st, const DecodeArgs& a, con
         // wave-uniform offset)
         constexpr bool SPAN = span_tiles<D, KVT>();
         auto offs = [&](int i, long long& ko, long long* vo, int* pos) {
-            return aligned_offsets<D, KVT, ZONE>(a, w, f + i, SPAN ? 0 : j, kq, ko, vo, pos);
+            return aligned_offsets<D, KVT, ZONE>(a, w, i, SPAN ? 0 : j, kq, ko, vo, pos);
         };
         walk_tiles<D, KVT, TRACK, decltype(offs), true>(st, a, qv, nc, j, kq, srow, offs);
     }
@@ -1509,8 +1559,8 @@ void decode_kernel(DecodeArgs a) {
             const int wa0 = t0 + (wave * cd) / 4, wb0 = t0 + ((wave + 1) * cd) / 4;
             pref = ALIGNED && a.mode == MODE_FULL && a.tables && wb0 > wa0;
             if (pref)
-                tbl_pref = run_table_entry(a, a.tables + (long long)b * a.table_stride, 0, wa0,
-                                           min(64, wb0 - wa0), lane);
+                tbl_pref = run_table_entry<tile_table<KVT, ZONE>()>(
+                    a, a.tables + (long long)b * a.table_stride, 0, wa0, min(64, wb0 - wa0), lane);
             const int len = a.ctx_lens ? sload(a.ctx_lens + b) : a.uniform_len;
             const int qp = a.q_pos ? sload(a.q_pos + b) : len - 1;
             e = extent_of<ALIGNED>(a, int2{len, qp});
