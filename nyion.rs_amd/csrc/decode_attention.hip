@@ -344,6 +344,22 @@ __device__ __forceinline__ float max_across_quads(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// max_across_quads with v_max_f32 applied to the swapped words as they are:
+// fmaxf first quiets its operands (two canonicalising maxes per step, the
+// lane swap's results not being known canonical); for scores, which hold
+// no signalling NaN, the result is the same
+__device__ __forceinline__ float max_across_quads_raw(float x) {
+    auto vmax = [](uint32_t p, uint32_t q) {
+        float r;
+        asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(__uint_as_float(p)), "v"(__uint_as_float(q)));
+        return r;
+    };
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = vmax(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return vmax(b[0], b[1]);
+}
+
 // Four values as binary16 (two words) and their binary16 residuals (two
 // more): hi + lo carries 22 significant bits of each value.
 __device__ __forceinline__ void pack_hi_lo(const float* v, float* w) {
@@ -474,15 +490,16 @@ __device__ __forceinline__ floatx4 q4_tile_scores(const Tile<D, NYION_KV_Q4_20B>
             q4_headers_get<D>(kq, hx);
             khr = hx;
         }
+        // row r: fma(d, S_g, fma(dmin, qsum_g, acc)) over g in order; the
+        // four rows' chains are formed step by step side by side, so that
+        // consecutive FMAs do not depend on each other
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float acc = 0.f;
+        for (int g = 0; g < D / 32; g++) {
 #pragma unroll
-            for (int g = 0; g < D / 32; g++) {
-                const float d = f16_bits_to_f32(khr[g][r]), dmin = f16_bits_to_f32(khr[g][r] >> 16);
-                acc = __builtin_fmaf(d, sg[g][r], __builtin_fmaf(dmin, qv[NC + g], acc));
-            }
-            s[r] = acc;
+            for (int r = 0; r < 4; r++)
+                s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r] >> 16), qv[NC + g], s[r]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r]), sg[g][r], s[r]);
         }
     }
     return s;
@@ -542,9 +559,43 @@ __device__ __forceinline__ void softmax_step(State<D>& st, const float* sv, int 
     const float mp = KVT == NYION_KV_Q4_20B ? st.m - 5.f : st.m;
 #pragma unroll
     for (int i = 0; i < N; i++) pr[i] = __builtin_amdgcn_exp2f(sv[i] - mp);
-    float ls = 0.f;
+    float ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
 #pragma unroll
-    for (int i = 0; i < N; i += 4) ls += (pr[i] + pr[i + 1]) + (pr[i + 2] + pr[i + 3]);
+    for (int i = 4; i < N; i += 4) ls += (pr[i] + pr[i + 1]) + (pr[i + 2] + pr[i + 3]);
+    st.l += ls;
+}
+
+// The online-softmax step of an unmasked, untracked pair of 4-bit tiles from
+// their raw scores x (log2 units times 1/sc; sc > 0): the max is taken on x
+// and scaled once (scaling by sc > 0 is monotonic, so max(x) * sc is the
+// max of the scaled scores), and each weight is 32 exp2(x sc - m) with the
+// scale and the shift in one FMA.  Otherwise as softmax_step.
+template <int D, int N>
+__device__ __forceinline__ void softmax_step_raw(State<D>& st, const float* x, float sc, int kq, float* pr) {
+    constexpr int DPL = D / 16;
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < N; i++) mx = fmaxf(mx, x[i]);
+    const float mt = max_across_quads_raw(mx) * sc;
+    if (__any(mt > st.m + kRescaleLog2)) {
+        const float mnew = fmaxf(st.m, mt);
+        const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+        st.l *= alpha;
+        st.m = mnew;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * kq + r);
+#pragma unroll
+            for (int xx = 0; xx < DPL; xx++) st.acc[xx][r] *= ar;
+            st.acc_m[r] *= ar;
+        }
+    }
+    const float nmp = 5.f - st.m;  // -(m - 5): weights in units of 1/32
+#pragma unroll
+    for (int i = 0; i < N; i++) pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], sc, nmp));
+    float ls = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+    for (int i = 4; i < N; i += 4) ls += (pr[i] + pr[i + 1]) + (pr[i + 2] + pr[i + 3]);
     st.l += ls;
 }
 
@@ -776,10 +827,16 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
     constexpr int KVT = NYION_KV_Q4_20B;
     constexpr int DPL = D / 16;
     float sv[8], pr[8];
-    tile_logits<KVT, MASKED, TRACK>(q4_tile_scores<D>(ta, qv, kq, khra), scale_log2, ma, kq, srow, pa_pos, sv);
-    tile_logits<KVT, MASKED, TRACK>(q4_tile_scores<D>(tb, qv, kq, khrb), scale_log2, mb, kq, srow, pb_pos,
-                                    sv + 4);
-    softmax_step<D, KVT, 8>(st, sv, kq, pr);
+    const floatx4 xa = q4_tile_scores<D>(ta, qv, kq, khra), xb = q4_tile_scores<D>(tb, qv, kq, khrb);
+    if constexpr (!MASKED && !TRACK) {
+        // the scores come out of the MFMAs scaled by 2^-24 (exact)
+        const float x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+        softmax_step_raw<D, 8>(st, x, scale_log2 * 16777216.f, kq, pr);
+    } else {
+        tile_logits<KVT, MASKED, TRACK>(xa, scale_log2, ma, kq, srow, pa_pos, sv);
+        tile_logits<KVT, MASKED, TRACK>(xb, scale_log2, mb, kq, srow, pb_pos, sv + 4);
+        softmax_step<D, KVT, 8>(st, sv, kq, pr);
+    }
     const halfx8 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3],
                        (_Float16)pr[4], (_Float16)pr[5], (_Float16)pr[6], (_Float16)pr[7]};
     const Q4VOperands<D> oa = q4_v_operands<D, MASKED>(ta, ma, kq, st.k6464);
