@@ -451,6 +451,44 @@ constexpr float kRescaleLog2 = 8.0f;
 // S of one Q4-20B tile for lane (head j, quad kq): rows 4kq+r, scaled by
 // 2^-24.  khr: the K headers of rows 4kq+r (null for a gathered tile:
 // exchanged through LDS).
+// One 16x16x32 MFMA per group and q part: the lane's eight values are class
+// a then class b (q_operand_q4 orders q the same way); sg[g] = nib.q of
+// group g, scaled by 2^-24.
+template <int D>
+__device__ __forceinline__ void q4_tile_mfma(const Tile<D, NYION_KV_Q4_20B>& t, const float* qv, floatx4* sg) {
+#pragma unroll
+    for (int g = 0; g < D / 32; g++) {
+        const uint32_t w = t.kn[g], w8 = w >> 8;
+        const halfx8 kab = __builtin_bit_cast(
+            halfx8, u32x4{w & 0x000f000fu, w8 & 0x000f000fu, w & 0x00f000f0u, w8 & 0x00f000f0u});
+        const float* qg = qv + 8 * g;
+        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            kab, __builtin_bit_cast(halfx8, floatx4{qg[0], qg[1], qg[2], qg[3]}), floatx4{0.f, 0.f, 0.f, 0.f},
+            0, 0, 0);
+        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            kab, __builtin_bit_cast(halfx8, floatx4{qg[4], qg[5], qg[6], qg[7]}), sg[g], 0, 0, 0);
+    }
+}
+
+// Row r's score from the group products: fma(d, S_g, fma(dmin, qsum_g, acc))
+// over g in order (khr[g][r]: the header of row 4kq+r, group g; qv[D/4 + g]:
+// 2^-24 times head j's q summed over group g).  The four rows' chains are
+// formed step by step side by side, so that consecutive FMAs do not depend
+// on each other.
+template <int D>
+__device__ __forceinline__ floatx4 q4_tile_combine(const floatx4* sg, const float* qv, const uint32_t (*khr)[4]) {
+    constexpr int NC = D / 4;
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < D / 32; g++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r] >> 16), qv[NC + g], s[r]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r]), sg[g][r], s[r]);
+    }
+    return s;
+}
+
 template <int D>
 __device__ __forceinline__ floatx4 q4_tile_scores(const Tile<D, NYION_KV_Q4_20B>& t, const float* qv, int kq,
                                                   const uint32_t (*khr)[4]) {
@@ -470,37 +508,14 @@ __device__ __forceinline__ floatx4 q4_tile_scores(const Tile<D, NYION_KV_Q4_20B>
         // gathered tile): the headers come from the lanes that loaded them,
         // written to the exchange slot before the MFMAs and read after.
         if (!khr) q4_headers_put<D>(t, kq);
-        // one 16x16x32 MFMA per group and q part: the lane's eight values
-        // are class a then class b (q_operand_q4 orders q the same way)
         floatx4 sg[D / 32];
-#pragma unroll
-        for (int g = 0; g < D / 32; g++) {
-            const uint32_t w = t.kn[g], w8 = w >> 8;
-            const halfx8 kab = __builtin_bit_cast(
-                halfx8, u32x4{w & 0x000f000fu, w8 & 0x000f000fu, w & 0x00f000f0u, w8 & 0x00f000f0u});
-            const float* qg = qv + 8 * g;
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                kab, __builtin_bit_cast(halfx8, floatx4{qg[0], qg[1], qg[2], qg[3]}), floatx4{0.f, 0.f, 0.f, 0.f},
-                0, 0, 0);
-            sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                kab, __builtin_bit_cast(halfx8, floatx4{qg[4], qg[5], qg[6], qg[7]}), sg[g], 0, 0, 0);
-        }
+        q4_tile_mfma<D>(t, qv, sg);
         uint32_t hx[D / 32][4];
         if (!khr) {
             q4_headers_get<D>(kq, hx);
             khr = hx;
         }
-        // row r: fma(d, S_g, fma(dmin, qsum_g, acc)) over g in order; the
-        // four rows' chains are formed step by step side by side, so that
-        // consecutive FMAs do not depend on each other
-#pragma unroll
-        for (int g = 0; g < D / 32; g++) {
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r] >> 16), qv[NC + g], s[r]);
-#pragma unroll
-            for (int r = 0; r < 4; r++) s[r] = __builtin_fmaf(f16_bits_to_f32(khr[g][r]), sg[g][r], s[r]);
-        }
+        s = q4_tile_combine<D>(sg, qv, khr);
     }
     return s;
 }
@@ -827,7 +842,11 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
     constexpr int KVT = NYION_KV_Q4_20B;
     constexpr int DPL = D / 16;
     float sv[8], pr[8];
-    const floatx4 xa = q4_tile_scores<D>(ta, qv, kq, khra), xb = q4_tile_scores<D>(tb, qv, kq, khrb);
+    // both tiles' MFMAs before either combine (span tiles: headers in khr)
+    floatx4 sga[D / 32], sgb[D / 32];
+    q4_tile_mfma<D>(ta, qv, sga);
+    q4_tile_mfma<D>(tb, qv, sgb);
+    const floatx4 xa = q4_tile_combine<D>(sga, qv, khra), xb = q4_tile_combine<D>(sgb, qv, khrb);
     if constexpr (!MASKED && !TRACK) {
         // the scores come out of the MFMAs scaled by 2^-24 (exact)
         const float x[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
