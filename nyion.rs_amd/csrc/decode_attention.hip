@@ -109,6 +109,9 @@ struct DecodeArgs {
     unsigned* status;  // the device's range-status word (binary16 q overflow)
     int direct;        // > 0: direct partition, pieces per segment (else stream-K)
     int seg_tiles;     // direct: host bound on the tiles of one segment
+    int spec_len;      // window mode: the host's max_ctx, whose window start a
+                       // walk's block-table loads may assume before the
+                       // length arrives (0: none)
     // zone geometry (gather path): sequence b's page offsets at
     // page_bases + b * zone.n_pages; zone.page_base unused
     const int64_t* page_bases;
@@ -1634,9 +1637,20 @@ void decode_kernel(DecodeArgs a) {
             const int t0 = piece * cd;
             const int wa0 = t0 + (wave * cd) / 4, wb0 = t0 + ((wave + 1) * cd) / 4;
             pref = ALIGNED && a.mode == MODE_FULL && a.tables && wb0 > wa0;
+            // untracked 4-bit span walks of paged windows: the walk of a
+            // sequence at the host's max_ctx (q at its end) starts at block
+            // position pref_base; its entries are requested with the length,
+            // kept if the extent confirms that start
+            constexpr bool kSpec = tile_table<KVT, ZONE>() && span_tiles<D, KVT>() && !TRACK;
+            int pref_base = 0;
+            if (kSpec && ALIGNED && a.mode == MODE_WINDOW && a.spec_len > 0 && a.tables && wb0 > wa0) {
+                const int ve = a.spec_len - 1;
+                pref_base = (ve > a.window ? ve - a.window + 1 : 0) & ~15;
+                pref = true;
+            }
             if (pref)
                 tbl_pref = run_table_entry<tile_table<KVT, ZONE>()>(
-                    a, a.tables + (long long)b * a.table_stride, 0, wa0, min(64, wb0 - wa0), lane);
+                    a, a.tables + (long long)b * a.table_stride, pref_base, wa0, min(64, wb0 - wa0), lane);
             const int len = a.ctx_lens ? sload(a.ctx_lens + b) : a.uniform_len;
             const int qp = a.q_pos ? sload(a.q_pos + b) : len - 1;
             e = extent_of<ALIGNED>(a, int2{len, qp});
@@ -1658,6 +1672,9 @@ void decode_kernel(DecodeArgs a) {
                     if (wave == kb) wa = mt;
                 }
             }
+            // (the entries cover tiles wa0 .. wb0 - 1: a walk start moved or
+            // an end moved past wb0 by the re-cut above loads its own)
+            if (kSpec && pref && ((e.lo & ~15) != pref_base || wa != wa0 || wb > wb0)) pref = false;
             whole = P == 1;
             pieces = P;
             slot = (int)blockIdx.x;
@@ -2376,6 +2393,7 @@ static int paged_decode_common(const float* d_q, const void* k_pool, const void*
     a.mode = window > 0 ? MODE_WINDOW : MODE_FULL;
     a.window = window;
     a.global_stride = global_stride;
+    a.spec_len = window > 0 ? max_ctx : 0;
     a.scores = d_scores;
     a.scores_stride = scores_stride;
     if (track && d_prev_scores) {
