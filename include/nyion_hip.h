@@ -471,9 +471,12 @@ int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion
  * per workgroup; the grid is sized for `tokens` per workgroup (a power of two
  * in 64..4096; 0 restores the default: the launch's tokens divided by the CU
  * count, within 128..256) and capped at the workgroups the device holds
- * resident.  Process-wide; for tuning.  The getter returns the
- * tokens per workgroup the current setting gives for `batch` sequences of
- * max_len tokens. */
+ * resident.  A launch of at most 64 segments cuts each segment into pieces
+ * of that many tokens instead; by default a piece of small rows (4-bit, or
+ * binary16 at head_dim 64) doubles while its K+V stays within 96 KiB and the
+ * launch keeps 128 workgroups.  Process-wide; for tuning.  The getter
+ * returns the tokens per workgroup the current setting gives for `batch`
+ * sequences of max_len tokens of f32 KV. */
 int nyion_set_decode_partition_tokens(int tokens);
 int nyion_get_decode_partition_tokens(int batch, int n_kv_heads, int head_dim, int max_len);
 
