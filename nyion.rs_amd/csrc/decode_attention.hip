@@ -877,29 +877,28 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
 }
 
 // A Q4-20B tile of a contiguous walk (aligned blocks of >= 16 tokens, zone
-// units of 32): its 16 K rows and its 16 V rows are each one span of 16 * TS
-// bytes (TS = row bytes), loaded as CH = TS chunks of 16 bytes, lane l taking
-// chunks l and l + 64 (lanes past the span take its last chunk again): one
-// or two wide loads per span instead of a narrow load per row and field.
+// units of 32) at head_dim 64: its 16 K rows and its 16 V rows are each one
+// span of 16 * 40 bytes, together 80 chunks of 16 bytes.  Lane l takes chunk
+// l of K then V (lanes 0-39 the K chunks, 40-63 the first 24 V chunks) with
+// one 16-byte load, and bytes 384 + 4l of the V span with one 4-byte load:
+// five registers a tile, every byte loaded once.
 template <int D>
 struct SpanTile {
+    static_assert(D == 64, "span tiles: head_dim 64");
     static constexpr int TS = q4_row_bytes(D);
-    static constexpr int CH = TS;
-    static constexpr int KC = (CH + 63) / 64;
-    u32x4a k[KC], v[KC];
+    static constexpr int KCH = TS;                // 16-byte chunks of a span
+    static constexpr int VTAIL = 16 * (64 - KCH);  // V bytes in the 16-byte loads
+    u32x4a c;
+    uint32_t w;
 };
 
 template <int D>
 __device__ __forceinline__ void load_span(SpanTile<D>& t, const void* kb, const void* vb, long long base,
                                           int lane) {
-    const uint8_t* k = (const uint8_t*)kb + base;
-    const uint8_t* v = (const uint8_t*)vb + base;
-#pragma unroll
-    for (int c = 0; c < SpanTile<D>::KC; c++) {
-        const uint32_t off = 16u * (uint32_t)min(lane + 64 * c, SpanTile<D>::CH - 1);
-        t.k[c] = __builtin_nontemporal_load((const u32x4a*)(k + off));
-        t.v[c] = __builtin_nontemporal_load((const u32x4a*)(v + off));
-    }
+    constexpr int KCH = SpanTile<D>::KCH, VTAIL = SpanTile<D>::VTAIL;
+    const uint8_t* p = lane < KCH ? (const uint8_t*)kb + 16 * lane : (const uint8_t*)vb + 16 * (lane - KCH);
+    t.c = __builtin_nontemporal_load((const u32x4a*)(p + base));
+    t.w = __builtin_nontemporal_load((const uint32_t*)((const uint8_t*)vb + VTAIL + 4 * lane + base));
 }
 
 // Operands of a span tile: the chunks go to one of the wavefront's two LDS
@@ -911,18 +910,15 @@ __device__ __forceinline__ void load_span(SpanTile<D>& t, const void* kb, const 
 template <int D>
 __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_KV_Q4_20B>& t,
                                            uint32_t (*khr)[4], int j, int kq, int slot = 0) {
-    constexpr int TS = SpanTile<D>::TS, KC = SpanTile<D>::KC, DPL = D / 16;
-    __shared__ u32x4 sm_span[4][2][2][KC * 64];
+    constexpr int TS = SpanTile<D>::TS, DPL = D / 16;
+    // K at bytes 0 .. 16 TS - 1 of the slot, V after it
+    __shared__ u32x4 sm_span[4][2][2 * SpanTile<D>::KCH];
     const int lane = threadIdx.x & 63;
-    u32x4* ks = sm_span[threadIdx.x >> 6][slot][0];
-    u32x4* vs = sm_span[threadIdx.x >> 6][slot][1];
-#pragma unroll
-    for (int c = 0; c < KC; c++) {
-        ks[lane + 64 * c] = sp.k[c];
-        vs[lane + 64 * c] = sp.v[c];
-    }
-    const uint8_t* kr = (const uint8_t*)ks;
-    const uint8_t* vr = (const uint8_t*)vs;
+    u32x4* sb = sm_span[threadIdx.x >> 6][slot];
+    sb[lane] = sp.c;
+    ((uint32_t*)(sb + 64))[lane] = sp.w;
+    const uint8_t* kr = (const uint8_t*)sb;
+    const uint8_t* vr = kr + 16 * TS;
 #pragma unroll
     for (int g = 0; g < D / 32; g++) {
         t.kn[g] = *(const uint32_t*)(kr + TS * j + kQ4GroupBytes * g + 4 + 4 * kq);
