@@ -12,7 +12,8 @@ workgroup every wavefront has at most one tile; at 256 a 1337-token
 sequence's 84 tiles go to six workgroups of 14, i.e. wavefronts of 3 and 4
 tiles; at 4096 one workgroup takes a whole segment.  Tolerance as for
 every attention output: max-abs-err <= 2e-3 and max|diff| / max|ref| <=
-1e-3; the tracked form's importance as in test_decode_gpu.
+1e-3; the tracked form's importance as in test_decode_gpu.  The Attention
+node's contiguous 4-bit layout is held to the same bar.
 """
 import numpy as np
 import pytest
@@ -79,3 +80,30 @@ def test_q4_span_walk_tracked(gpu, tokens):
         _, ref_imp = oracle.attention(pb.q[b].reshape(-1), pb.layout(b), L, Q_POS[b], pb.n_heads,
                                       pb.n_kv_heads, pb.head_dim, importance=True)
         W.assert_importance(imp[b][:L], ref_imp, f"{tokens} tokens: importance b={b}")
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("seq_len", [1, 17, 128, 1000])
+def test_q4_attention_node(gpu, head_dim, seq_len):
+    """The Attention node on Q4-20B rows laid out [Hkv][kv_stride][row]
+    (compute_graph.rs:14-25 with the 4-bit cache): no block table, so a span
+    walk's tile offsets come from the row positions alone (head_dim 64;
+    head_dim 128 walks per-row tiles), with and without the scores buffer
+    (whole segments, or split-K pieces merged through it)."""
+    rng = np.random.default_rng(seq_len + head_dim)
+    hq, hkv, stride = 32, 4, seq_len + 24
+    q = rng.standard_normal((hq, head_dim), dtype=np.float32)
+    k = oracle.q4_quantize_rows(rng.standard_normal((hkv, stride, head_dim), dtype=np.float32))
+    v = oracle.q4_quantize_rows(rng.standard_normal((hkv, stride, head_dim), dtype=np.float32))
+    ref = oracle.attention(q.reshape(-1), oracle.contiguous_layout(k, v, stride, head_dim, oracle.KV_Q4),
+                           seq_len, seq_len - 1, hq, hkv, head_dim).reshape(hq, head_dim)
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    out = torch.full_like(dq, float("nan"))
+    gpu.attention_node(dq, dk, dv, out, hq, hkv, seq_len, head_dim, stride, kv_dtype=oracle.KV_Q4)
+    scores = torch.empty(hq * seq_len, device="cuda")
+    split = torch.full_like(dq, float("nan"))
+    gpu.attention_node(dq, dk, dv, split, hq, hkv, seq_len, head_dim, stride, kv_dtype=oracle.KV_Q4,
+                       scores=scores)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"q4 node, {seq_len} positions")
+    assert_close(split.cpu().numpy(), ref, f"q4 node with scores buffer, {seq_len} positions")
