@@ -7,8 +7,8 @@ first and the globals' gathered tiles after them.  The windows, lengths and
 partition sizes below put the boundary between the two inside a piece at
 every offset a wavefront split can take, so the piece's wave ranges are
 re-cut there; the default partition (0) sizes pieces by the bytes of the KV
-format.  Every KV format and head size, blocks of one tile and of four,
-against the oracle, tolerance as for every attention output: max-abs-err
+format.  Every KV format and head size, blocks of one, four and sixteen
+tiles, against the oracle, tolerance as for every attention output: max-abs-err
 <= 2e-3 and max|diff| / max|ref| <= 1e-3.
 """
 import numpy as np
@@ -42,7 +42,7 @@ def decode(gpu, pb, window, stride, q_pos=None):
 
 @pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_F16, oracle.KV_Q4], ids=["f32", "f16", "q4"])
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("block_tokens", [16, 64])
+@pytest.mark.parametrize("block_tokens", [16, 64, 256])
 def test_window_globals_direct_partitions(gpu, kv_dtype, head_dim, block_tokens):
     pb = W.paged_batch(CTX, n_heads=16, n_kv_heads=4, head_dim=head_dim, block_tokens=block_tokens,
                        seed=head_dim + kv_dtype + block_tokens, kv_dtype=kv_dtype)
