@@ -451,9 +451,6 @@ __device__ __forceinline__ void q4_headers_get(int kq, uint32_t (*khr)[4]) {
 // exp2(s - m) <= 2^8 and the O rescale is rare after the first tiles.
 constexpr float kRescaleLog2 = 8.0f;
 
-// S of one Q4-20B tile for lane (head j, quad kq): rows 4kq+r, scaled by
-// 2^-24.  khr: the K headers of rows 4kq+r (null for a gathered tile:
-// exchanged through LDS).
 // One 16x16x32 MFMA per group and q part: the lane's eight values are class
 // a then class b (q_operand_q4 orders q the same way); sg[g] = nib.q of
 // group g, scaled by 2^-24.
@@ -492,35 +489,33 @@ __device__ __forceinline__ floatx4 q4_tile_combine(const floatx4* sg, const floa
     return s;
 }
 
+// S of one Q4-20B tile for lane (head j, quad kq): rows 4kq+r, scaled by
+// 2^-24.  khr: the K headers of rows 4kq+r (null for a gathered tile:
+// exchanged through LDS).
+//
+// k = d*nib + dmin per 32-element group g, so q.k = sum_g d*(nib.q)_g +
+// dmin*sum(q_g): the nibbles are exact binary16 operands against q split
+// into binary16 high and low parts (q_operand_q4; qv[D/4 + g] = 2^-24 times
+// the sum of head j's q over group g), one accumulator per group, then each
+// row's d and dmin (khr[g][r]: the header of row 4kq+r, group g).  A nibble
+// masked in place is a binary16 denormal: bits e (elements 8kq + {0, 4, 2,
+// 6}, class a) or 16e (elements 8kq + {1, 5, 3, 7}, class b, whose q carries
+// 1/16), times 2^-24; the MFMA takes denormal inputs exactly, so the scores
+// come out scaled by 2^-24 (undone with the softmax scale).  khr null (a
+// gathered tile): the headers come from the lanes that loaded them, written
+// to the exchange slot before the MFMAs and read after.
 template <int D>
 __device__ __forceinline__ floatx4 q4_tile_scores(const Tile<D, NYION_KV_Q4_20B>& t, const float* qv, int kq,
                                                   const uint32_t (*khr)[4]) {
-    constexpr int NC = D / 4;
-    floatx4 s = {0.f, 0.f, 0.f, 0.f};
-    {
-        // k = d*nib + dmin per 32-element group g, so q.k = sum_g d*(nib.q)_g
-        // + dmin*sum(q_g): the nibbles are exact binary16 operands against q
-        // split into binary16 high and low parts (q_operand_q4; qv[NC + g] =
-        // 2^-24 times the sum of head j's q over group g), one accumulator
-        // per group, then each row's d and dmin (khr[g][r]: the header of
-        // row 4kq+r, group g).  A nibble masked in place is a binary16
-        // denormal: bits e (elements 8kq + {0, 4, 2, 6}, class a) or 16e
-        // (elements 8kq + {1, 5, 3, 7}, class b, whose q carries 1/16), times
-        // 2^-24; the MFMA takes denormal inputs exactly, so the scores come
-        // out scaled by 2^-24 (undone with the softmax scale).  khr null (a
-        // gathered tile): the headers come from the lanes that loaded them,
-        // written to the exchange slot before the MFMAs and read after.
-        if (!khr) q4_headers_put<D>(t, kq);
-        floatx4 sg[D / 32];
-        q4_tile_mfma<D>(t, qv, sg);
-        uint32_t hx[D / 32][4];
-        if (!khr) {
-            q4_headers_get<D>(kq, hx);
-            khr = hx;
-        }
-        s = q4_tile_combine<D>(sg, qv, khr);
+    if (!khr) q4_headers_put<D>(t, kq);
+    floatx4 sg[D / 32];
+    q4_tile_mfma<D>(t, qv, sg);
+    uint32_t hx[D / 32][4];
+    if (!khr) {
+        q4_headers_get<D>(kq, hx);
+        khr = hx;
     }
-    return s;
+    return q4_tile_combine<D>(sg, qv, khr);
 }
 
 // Log2-unit scores of one tile (masked rows -1e30); TRACK: stored into srow
@@ -915,8 +910,8 @@ __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_
     __shared__ u32x4 sm_span[4][2][2 * SpanTile<D>::KCH];
     const int lane = threadIdx.x & 63;
     u32x4* sb = sm_span[threadIdx.x >> 6][slot];
-    sb[lane] = sp.c;
-    ((uint32_t*)(sb + 64))[lane] = sp.w;
+    sb[lane] = sp.c;                         // bytes 0 .. 1023: K, then V bytes 0 .. 383
+    ((uint32_t*)(sb + 64))[lane] = sp.w;     // V bytes 384 + 4 lane
     const uint8_t* kr = (const uint8_t*)sb;
     const uint8_t* vr = kr + 16 * TS;
 #pragma unroll
@@ -931,20 +926,18 @@ __device__ __forceinline__ void stage_span(const SpanTile<D>& sp, Tile<D, NYION_
     for (int r = 0; r < 4; r++) {
         const uint8_t* row = vr + TS * (4 * kq + r) + kQ4GroupBytes * gv;
         t.vhdr[r] = *(const uint32_t*)row;
-        if constexpr (D == 64)
-            t.v[r] = *(const uint16_t*)(row + nv);
-        else
-            t.v[r] = *(const uint32_t*)(row + nv);
+        t.v[r] = *(const uint16_t*)(row + nv);  // head_dim 64: four dims, two bytes
     }
 }
 
-// Row offsets of tile `tile` on the aligned path: positions t0 .. t0+15 of
-// one block; valid rows [vlo, vhi].  Lane l holds a 64-bit row offset, low
-// word in tblv, high in tblh (-1: no rows): paged blocks, the first row of
-// this kv head in the block of block index bi_first + l; ZONE, the blocks
-// are 32-token units of zone pages (every zone page is a whole number of
-// them, and a unit's rows of one (layer, kv head) are consecutive), the
-// offset of row (layer, kv head 0) of unit bi_first + l.
+// A run of an aligned walk: tiles of positions t0 .. t0+15 within one block;
+// valid rows [lo, hi].  Lane l holds a 64-bit row offset, low word in tblv,
+// high in tblh (-1: no rows): 4-bit paged walks, the first row of run tile l
+// in this kv head; other paged walks, the first row of this kv head in the
+// block of block index bi_first + l; ZONE, the blocks are 32-token units of
+// zone pages (every zone page is a whole number of them, and a unit's rows
+// of one (layer, kv head) are consecutive), the offset of row (layer, kv
+// head 0) of unit bi_first + l.
 struct AlignedWalk {
     int base;        // lo & ~15
     int lo, hi;
