@@ -93,6 +93,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const void* base,
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
 
+// Wavefront max / sum through DPP row operations, a fixed tree (the result
+// does not depend on timing): lane pairs, quads, half rows, rows, then the
+// rows combined through row broadcasts; returns lane 63's result, which is
+// the whole wavefront's, to every lane.  No LDS traffic.
+template <bool MAX, int CTRL, int ROW_MASK>
+__device__ __forceinline__ float wave_dpp_step(float x) {
+    const float id = MAX ? -INFINITY : 0.0f;
+    const float y = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+    return MAX ? fmaxf(x, y) : x + y;
+}
+
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce_dpp(float x) {
+    x = wave_dpp_step<MAX, 0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
+    x = wave_dpp_step<MAX, 0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
+    x = wave_dpp_step<MAX, 0x141, 0xf>(x);  // row_half_mirror
+    x = wave_dpp_step<MAX, 0x140, 0xf>(x);  // row_mirror: each row's lanes hold the row's value
+    x = wave_dpp_step<MAX, 0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x = wave_dpp_step<MAX, 0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 static inline bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
 static inline int ilog2(long long x) {
     int r = 0;

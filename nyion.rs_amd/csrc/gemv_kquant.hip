@@ -344,10 +344,7 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
             for (int i = 0; i < R; i++)
 #pragma unroll
                 for (int b = 0; b < B; b++) {
-                    float v = acc[i][b];
-#pragma unroll
-                    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-                    acc[i][b] = v;
+                    acc[i][b] = wave_reduce_dpp<false>(acc[i][b]);
                 }
             if (P == 1) {
                 if (lane == 0)

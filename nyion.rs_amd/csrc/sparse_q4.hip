@@ -106,33 +106,6 @@ __device__ __forceinline__ void sq4_half(const uint32_t* w5, int half, float* ou
     }
 }
 
-// Wavefront max / sum through DPP row operations (a fixed tree, so the sum
-// is the same on every call): lane pairs, quads, half rows, rows, then the
-// rows combined through row broadcasts; every lane gets lane 63's result.
-template <bool MAX>
-__device__ __forceinline__ float sq4_op(float x, float y) {
-    return MAX ? fmaxf(x, y) : x + y;
-}
-
-template <bool MAX, int CTRL, int ROW_MASK>
-__device__ __forceinline__ float sq4_dpp_step(float x) {
-    const float id = MAX ? -INFINITY : 0.0f;
-    const float y = __int_as_float(
-        __builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
-    return sq4_op<MAX>(x, y);
-}
-
-template <bool MAX>
-__device__ __forceinline__ float sq4_wave_reduce(float x) {
-    x = sq4_dpp_step<MAX, 0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
-    x = sq4_dpp_step<MAX, 0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
-    x = sq4_dpp_step<MAX, 0x141, 0xf>(x);  // row_half_mirror
-    x = sq4_dpp_step<MAX, 0x140, 0xf>(x);  // row_mirror: each row's lanes hold the row's value
-    x = sq4_dpp_step<MAX, 0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
-    x = sq4_dpp_step<MAX, 0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
-
 typedef const __attribute__((address_space(4))) float* sq4_cfloat_ptr;
 
 template <int D>
@@ -200,13 +173,13 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_scores_kernel(Sq4Args a) {
         float v[4];
 #pragma unroll
         for (int x = 0; x < 4; x++) v[x] = sc_s[r * kSq4Threads + lane + 64 * x];
-        const float m = sq4_wave_reduce<true>(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        const float m = wave_reduce_dpp<true>(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
         float e = 0.0f;
         if (m != -INFINITY) {
 #pragma unroll
             for (int x = 0; x < 4; x++) e += v[x] == -INFINITY ? 0.0f : expf(v[x] - m);
         }
-        e = sq4_wave_reduce<false>(e);
+        e = wave_reduce_dpp<false>(e);
         if (lane == 0) a.ml[((long long)seg * a.pieces + piece) * a.group + r] = float2{m, e};
     }
 }
@@ -255,18 +228,18 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
         const float2 mine = lane < used ? mlr[(long long)lane * a.group] : float2{-INFINITY, 0.0f};
         float m = mine.x;
         for (int p = lane + 64; p < used; p += 64) m = fmaxf(m, mlr[(long long)p * a.group].x);
-        m = sq4_wave_reduce<true>(m);
+        m = wave_reduce_dpp<true>(m);
         float sum = 0.0f;
         if (m != -INFINITY) {
             float e = mine.x == -INFINITY ? 0.0f : mine.y * expf(mine.x - m);
-            sum = sq4_wave_reduce<false>(e);
+            sum = wave_reduce_dpp<false>(e);
             for (int p0 = 64; p0 < used; p0 += 64) {  // more than 64 pieces
                 e = 0.0f;
                 if (p0 + lane < used) {
                     const float2 x = mlr[(long long)(p0 + lane) * a.group];
                     e = x.x == -INFINITY ? 0.0f : x.y * expf(x.x - m);
                 }
-                sum += sq4_wave_reduce<false>(e);
+                sum += wave_reduce_dpp<false>(e);
             }
         }
         if (lane == 0) {
