@@ -47,6 +47,7 @@
 // several launches).
 #include "common.hpp"
 
+#include <algorithm>
 #include <vector>
 
 namespace nyion {
@@ -120,6 +121,9 @@ struct Q4kFormat {
     // registers and costs the four-row kernel a wavefront per SIMD
     // (8B-shaped gate/up 22.5 -> 25.5 us)
     static constexpr bool kAlternateBuffers = false;
+    // four rows per unit: 155 registers, three wavefronts per SIMD (two rows
+    // ran the 8B-shaped gate/up 22.8 -> 24.1 us)
+    static constexpr int kMaxRows = 4;
     static constexpr const char* kName = "gemv q4k";
     // the block's 16-byte header and the chunk's 16 nibble bytes
     struct Raw {
@@ -175,6 +179,9 @@ struct Q6kFormat {
     // words between steps at the same occupancy (output projection 19.5 ->
     // 18.9 us)
     static constexpr bool kAlternateBuffers = true;
+    // two rows per unit: four take 202 registers, two wavefronts per SIMD
+    // (the 32000 x 2048 output projection 19.3 -> 18.1 us at two)
+    static constexpr int kMaxRows = 2;
     static constexpr const char* kName = "gemv q6k";
     // dword-aligned words covering the chunk's 16 ql bytes and 16 qh bytes
     // (four plus one each), its two scales and the word holding d, and the
@@ -437,14 +444,15 @@ static void launch_p(const GemvArgs& a, int P, int units, hipStream_t st) {
 }
 
 // Wavefronts per row: enough for one pass of 64 chunks each up to 16384
-// columns (longer rows take several passes).  Rows per unit: the largest R
-// in {1, 2, 4} that still gives every SIMD four wavefronts (two at four
-// inputs and eight wavefronts per row, which would not fit four rows).
+// columns (longer rows take several passes).  Rows per unit: R in {1, 2, 4}
+// doubles while the launch keeps at least 4096 (unit, wavefront) pairs, up
+// to the format's kMaxRows (two at four inputs and eight wavefronts per row,
+// which would not fit four rows).
 template <class F, int B>
 static void launch_gemv(GemvArgs& a, int total_rows, hipStream_t st) {
     const int chunks = a.nb * 8;
     const int P = chunks <= 64 ? 1 : chunks <= 128 ? 2 : chunks <= 256 ? 4 : 8;
-    const int r_max = (B == 4 && P == 8) ? 2 : 4;
+    const int r_max = std::min(F::kMaxRows, (B == 4 && P == 8) ? 2 : 4);
     int R = 1;
     while (R < r_max && (long long)(total_rows / (2 * R)) * P >= 4096) R *= 2;
     int units = 0;
