@@ -126,3 +126,38 @@ def test_random_tracked_pipelined(gpu, seed):
                 want = np.zeros(got.shape[0])
                 want[:L] = imp
             W.assert_importance(got, want, f"{c}: layer {i} importance b={b}")
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_decode_partitioned(gpu, seed):
+    """The draws above on the aligned walks (pages of 16..256 tokens) with
+    the tiles per workgroup overridden (64..2048 tokens): where the direct
+    partition's piece and wave boundaries fall against the window start,
+    the globals and the page edges moves with every case."""
+    c = draw(3000 + seed)
+    rng = np.random.default_rng(4000 + seed)
+    c["bt"] = int(rng.choice([16, 32, 64, 128, 256]))
+    tokens = int(rng.choice([64, 128, 256, 512, 1024, 2048]))
+    print(f"case {seed}: {c} partition {tokens}", flush=True)
+    pb = W.paged_batch(c["ctx"], n_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"],
+                       block_tokens=c["bt"], seed=seed, kv_dtype=c["kv"])
+    q = to_dev(pb.q)
+    kp, vp = to_dev(pb.k_pool), to_dev(pb.v_pool)
+    tab, ctx = to_dev(pb.tables), to_dev(pb.ctx_lens)
+    qp = None if c["q_pos"] is None else to_dev(np.asarray(c["q_pos"], np.int32))
+    out = torch.full_like(q, float("nan"))
+    try:
+        gpu.set_partition_tokens(tokens)
+        gpu.paged_decode(q, kp, vp, tab, ctx, out, pb.n_heads, pb.n_kv_heads, pb.head_dim,
+                         pb.block_tokens, kv_dtype=pb.kv_dtype, window=c["window"],
+                         global_stride=c["stride"], max_ctx=int(pb.ctx_lens.max()), q_pos=qp)
+        torch.cuda.synchronize()
+    finally:
+        gpu.set_partition_tokens(0)
+    got = out.cpu().numpy().astype(np.float64)
+    ref = W.reference_decode(pb, window=c["window"], global_stride=c["stride"], q_pos=c["q_pos"],
+                             threads=8).astype(np.float64)
+    assert np.all(np.isfinite(got)), c
+    err = np.max(np.abs(got - ref))
+    rel = err / max(np.max(np.abs(ref)), 1e-30)
+    assert err <= ATOL and rel <= RTOL, f"{c} partition {tokens}: max-abs {err:.3e} rel {rel:.3e}"
