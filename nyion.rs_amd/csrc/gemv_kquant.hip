@@ -257,9 +257,15 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
     const long long row_bytes = (long long)a.nb * F::kBlockBytes;
 
     // x runs of every input for chunk c (16 low-run and 16 high-run values)
-    // and their sums; zero for a chunk past the row
+    // and their sums.  A chunk past the row reads block 0's (in bounds),
+    // which its lane never uses: it skips the chunk's arithmetic.  Once per
+    // call (one pass per row) the loads go out together; zeroing the values
+    // of such a chunk would make each pair of loads wait for the one before.
+    // Per pass (longer rows), the zeroing stays: without it the compiler
+    // moves those loads ahead and holds up to 43 more registers, a wavefront
+    // per SIMD in most instantiations.
     float xl[B][16], xh[B][16], sl[B], sh[B];
-    auto load_x = [&](int c) __attribute__((always_inline)) {
+    auto load_x = [&](int c, bool zero_past) __attribute__((always_inline)) {
         const bool ok = c < n_chunks;
         const int blk = ok ? c >> 3 : 0;
 #pragma unroll
@@ -269,7 +275,7 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
             for (int v = 0; v < 4; v++) {
                 float4 lo = *(const float4*)(xp + 4 * v);
                 float4 hi = *(const float4*)(xp + F::kRunGap + 4 * v);
-                if (!ok) lo = hi = float4{0.f, 0.f, 0.f, 0.f};
+                if (zero_past && !ok) lo = hi = float4{0.f, 0.f, 0.f, 0.f};
                 xl[b][4 * v] = lo.x; xl[b][4 * v + 1] = lo.y; xl[b][4 * v + 2] = lo.z; xl[b][4 * v + 3] = lo.w;
                 xh[b][4 * v] = hi.x; xh[b][4 * v + 1] = hi.y; xh[b][4 * v + 2] = hi.z; xh[b][4 * v + 3] = hi.w;
             }
@@ -307,7 +313,10 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
     // steps of this workgroup: its units blockIdx.x, +G, ... times the passes
     const int units_here = (int)blockIdx.x < U ? (U - (int)blockIdx.x + G - 1) / G : 0;
     const int T = units_here * npass;
-    if (npass == 1) load_x(lane + 64 * kp);  // the same chunk positions for every row
+    // x before the first weights: a wavefront's loads complete in order, so
+    // the x sums wait for x alone (the weights requested first made them wait
+    // for those too: the TinyLlama step 485 -> 497 us)
+    if (npass == 1) load_x(lane + 64 * kp, false);  // the same chunk positions for every row
     GemvStep<F, R> buf[2];  // current and next step's raw weights
     if (T > 0) load_w(0, buf[0]);
     float acc[R][B];
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(64 * P) void gemv_kquant_kernel(GemvArgs a) {
         if (t + 1 < T) load_w(t + 1, nxt);  // next step's weights in flight
         const int pass = t % npass;
         const int c = lane + 64 * (kp + P * pass);
-        if (npass > 1) load_x(c);
+        if (npass > 1) load_x(c, true);
         if (c < n_chunks) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
