@@ -842,6 +842,12 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
     float sv[8], pr[8];
     // both tiles' MFMAs before either combine (span tiles: headers in khr)
     floatx4 sga[D / 32], sgb[D / 32];
+    // the scores through the softmax at raised issue priority: of two
+    // wavefronts on a SIMD, the one in this stretch of MFMAs, exchanges and
+    // exponentials goes first while the other builds V operands and runs
+    // its P.V products (c3q 115.5 -> 110.0 us; C4, one wavefront per SIMD,
+    // 14.8 -> 15.0 us)
+    __builtin_amdgcn_s_setprio(1);
     q4_tile_mfma<D>(ta, qv, sga);
     q4_tile_mfma<D>(tb, qv, sgb);
     const floatx4 xa = q4_tile_combine<D>(sga, qv, khra), xb = q4_tile_combine<D>(sgb, qv, khrb);
@@ -856,6 +862,7 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
     }
     const halfx8 pa = {(_Float16)pr[0], (_Float16)pr[1], (_Float16)pr[2], (_Float16)pr[3],
                        (_Float16)pr[4], (_Float16)pr[5], (_Float16)pr[6], (_Float16)pr[7]};
+    __builtin_amdgcn_s_setprio(0);
     const Q4VOperands<D> oa = q4_v_operands<D, MASKED>(ta, ma, kq, st.k6464);
     const Q4VOperands<D> ob = q4_v_operands<D, MASKED>(tb, mb, kq, st.k6464);
     st.acc_m = __builtin_amdgcn_mfma_f32_16x16x32_f16(
