@@ -845,8 +845,8 @@ __device__ __forceinline__ void consume_pair_tiles(State<D>& st, const Tile<D, N
     // the scores through the softmax at raised issue priority: of two
     // wavefronts on a SIMD, the one in this stretch of MFMAs, exchanges and
     // exponentials goes first while the other builds V operands and runs
-    // its P.V products (c3q 115.5 -> 110.0 us; C4, one wavefront per SIMD,
-    // 14.8 -> 15.0 us)
+    // its P.V products (64 sequences of 512-32768 tokens: 115.5 -> 110.0 us;
+    // 8 windows of 4096 tokens, one wavefront per SIMD: 14.8 -> 15.0 us)
     __builtin_amdgcn_s_setprio(1);
     q4_tile_mfma<D>(ta, qv, sga);
     q4_tile_mfma<D>(tb, qv, sgb);
