@@ -1197,8 +1197,14 @@ __device__ __forceinline__ void walk_tiles(State<D>& st, const DecodeArgs& a, co
             for (int k = 0; k < NB; k++) {
                 const int s = (k + NB - 1) % NB;
                 if (k & 1) eat_pair(t[k - 1], t[k], msk[k - 1], msk[k], pos[k - 1], pos[k]);
+                // the refill's offsets and loads at the highest priority the
+                // walk uses, so its requests leave ahead of the other
+                // wavefront's arithmetic (the 64-sequence 4-bit batch
+                // 111.0 -> 109.6 us, the 4096-token windows 15.06 -> 14.95 us)
+                __builtin_amdgcn_s_setprio(2);
                 msk[s] = offsets(min(i + k + NB - 1, n - 1), ko, vo, pos[s]);
                 load(t[s]);
+                __builtin_amdgcn_s_setprio(0);
             }
         }
         // the last, partial iteration: its tiles are in slots 0 .. n-i-1,
