@@ -474,7 +474,9 @@ int nyion_decode_workspace_init(void* d_workspace, size_t workspace_bytes, nyion
  * resident.  A launch of at most 64 segments cuts each segment into pieces
  * of that many tokens instead; by default a piece of small rows (4-bit, or
  * binary16 at head_dim 64) doubles while its K+V stays within 96 KiB and the
- * launch keeps 128 workgroups.  Process-wide; for tuning.  The getter
+ * launch keeps 128 workgroups, and the pieces are then raised to one
+ * workgroup per CU where each keeps 16 tiles.  Process-wide; for tuning.
+ * The getter
  * returns the tokens per workgroup the current setting gives for `batch`
  * sequences of max_len tokens of f32 KV. */
 int nyion_set_decode_partition_tokens(int tokens);
