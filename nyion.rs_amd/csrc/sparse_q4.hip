@@ -222,6 +222,16 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
 #pragma unroll
         for (int x = 0; x < W; x++) vw[x] = rw[x];
     }
+    // every head's score of this position, requested with the V row and
+    // ahead of the pieces' (max, sum) below, none of which it depends on
+    float sv[kSq4MaxGroup];
+    {
+        const float* src = a.scores + (long long)seg * a.group * ((long long)a.pieces * kSq4Threads) +
+                           first + tid;
+#pragma unroll
+        for (int r = 0; r < kSq4MaxGroup; r++)
+            sv[r] = r < a.group && tid < n_here ? src[(long long)r * a.pieces * kSq4Threads] : -INFINITY;
+    }
     // the head's max and 1/sum over the pieces, in piece order
     for (int r = wave; r < a.group; r += kSq4Threads / 64) {
         const float2* mlr = a.ml + (long long)seg * a.pieces * a.group + r;
@@ -249,13 +259,7 @@ __global__ __launch_bounds__(kSq4Threads) void sq4_values_kernel(Sq4Args a) {
     }
     __syncthreads();
     {
-        // every head's weight of this position; score loads in flight together
-        float sv[kSq4MaxGroup];
-        const float* src = a.scores + (long long)seg * a.group * ((long long)a.pieces * kSq4Threads) +
-                           first + tid;
-#pragma unroll
-        for (int r = 0; r < kSq4MaxGroup; r++)
-            sv[r] = r < a.group && tid < n_here ? src[(long long)r * a.pieces * kSq4Threads] : -INFINITY;
+        // every head's weight of this position
 #pragma unroll
         for (int r = 0; r < kSq4MaxGroup; r++) {
             if (r < WP) {
